@@ -1,0 +1,40 @@
+import os
+import sys
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+GOLDEN = os.path.join(ROOT, "tests", "golden")
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU")
+
+
+def load_golden(name):
+    with np.load(os.path.join(GOLDEN, name + ".npz"), allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
+
+
+@pytest.fixture
+def golden():
+    return load_golden
+
+
+def assert_close(actual, expected, atol, rtol, what=""):
+    """|actual - expected| <= atol + rtol * |expected| elementwise (NaN fails)."""
+    a = np.asarray(actual, dtype=np.float64)
+    e = np.asarray(expected, dtype=np.float64)
+    assert a.shape == e.shape, (a.shape, e.shape)
+    err = np.abs(a - e)
+    bound = atol + rtol * np.abs(e)
+    bad = ~(err <= bound)
+    if bad.any():
+        idx = np.unravel_index(np.argmax(np.where(bad, err - bound, -np.inf)), a.shape)
+        raise AssertionError(
+            f"{what}: {int(bad.sum())}/{a.size} elements outside atol={atol} rtol={rtol}; "
+            f"worst at {idx}: got {a[idx]!r} expected {e[idx]!r}; max abs err {err.max():.3e}")
