@@ -1,0 +1,300 @@
+#!/usr/bin/env python3
+"""Throughput of the loom_hip kernels on one MI355X.
+
+The headline line (one JSON object on stdout) measures @batch_matmul at the
+BASELINE configuration B16 x 2048^3 (bf16 in, fp32 accumulate): K timed steps
+of one call each, inputs resident in HBM.  It carries
+
+  roofline      the GEMM kernel's achieved TFLOP/s (algorithmic 2*B*M*N*K per
+                launch / mean launch time from HIP events on the launch
+                stream) against the dense bf16 MFMA peak;
+  cpu_baseline  the fp32 C oracle (OpenMP, all host threads) on a bounded
+                sample of the same batches;
+  kernels       every BASELINE configuration (mm, bmm, split-K, flashattn,
+                mqa_decode, mamba_chunk_scan) timed per call between cache
+                flushes, with its roofline fraction.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+                       [--kernels all|none|mm,bmm,...]
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "loom-dataflow_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+PEAK_BF16_TFLOPS = 2516.6   # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    ap.add_argument("--kernels", default="all", help="per-kernel table: all, none or a list")
+    ap.add_argument("--iters", type=int, default=10, help="timed calls per kernel in the table")
+    return ap.parse_args()
+
+
+def traffic_for(kernel):
+    """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE),
+    if a measurement has been recorded for this kernel."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            return json.load(f).get(kernel)
+    except (OSError, ValueError):
+        return None
+
+
+class Flusher:
+    """Evicts L2 and the 256 MB Infinity Cache by writing 512 MB."""
+
+    def __init__(self, torch):
+        self.buf = torch.empty(512 << 20, dtype=torch.uint8, device="cuda")
+
+    def __call__(self):
+        self.buf.fill_(1)
+
+
+def time_calls(torch, fn, iters, flush=None):
+    """Per-call durations (ms) from HIP events around each call on the
+    current stream (the stream the library launches on)."""
+    s = torch.cuda.current_stream()
+    evs = []
+    for _ in range(iters):
+        if flush is not None:
+            flush()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(s)
+        fn()
+        b.record(s)
+        evs.append((a, b))
+    torch.cuda.synchronize()
+    return [a.elapsed_time(b) for a, b in evs]
+
+
+def median(xs):
+    xs = sorted(xs)
+    n = len(xs)
+    return xs[n // 2] if n % 2 else 0.5 * (xs[n // 2 - 1] + xs[n // 2])
+
+
+# --------------------------------------------------------------------------
+# BASELINE configurations
+# --------------------------------------------------------------------------
+
+def make_cases(torch, lh):
+    cuda = "cuda"
+    bf = torch.bfloat16
+    g = torch.Generator(device=cuda)
+    g.manual_seed(1234)
+
+    def randn(*shape, std=1.0, dtype=bf):
+        return (torch.randn(*shape, generator=g, device=cuda) * std).to(dtype)
+
+    def unif(*shape):
+        return (torch.rand(*shape, generator=g, device=cuda) * 2 - 1).to(bf)
+
+    cases = {}
+
+    def mm():
+        x, y = unif(1024, 1024), unif(1024, 1024)
+        out = torch.empty(1024, 1024, dtype=bf, device=cuda)
+        return dict(fn=lambda: lh.matmul(x, y, out, tile_m=128, tile_n=128, tile_k=64),
+                    flop=2 * 1024 ** 3, bytes=3 * 1024 * 1024 * 2, bound="mfma",
+                    desc="mm 1024^3 bf16, tile 128x128")
+    cases["mm"] = mm
+
+    def bmm():
+        a0, a1 = randn(16, 2048, 2048, std=0.02), randn(16, 2048, 2048, std=0.02)
+        out = torch.empty(16, 2048, 2048, dtype=bf, device=cuda)
+        return dict(fn=lambda: lh.batch_matmul(a0, a1, out, tile_m=256, tile_n=256),
+                    flop=2 * 16 * 2048 ** 3, bytes=3 * 16 * 2048 * 2048 * 2, bound="mfma",
+                    desc="bmm 16x2048^3 bf16, tile 256x256")
+    cases["bmm"] = bmm
+
+    def splitk():
+        a, b = randn(512, 16384, std=0.02), randn(16384, 512, std=0.02)
+        out = torch.empty(512, 512, dtype=bf, device=cuda)
+        parts = torch.empty(16, 512, 512, dtype=torch.float32, device=cuda)
+        return dict(fn=lambda: lh.split_k_matmul_gather(a, b, out, parts, tile_m=64, tile_n=64,
+                                                        tile_k=1024),
+                    flop=2 * 512 * 512 * 16384,
+                    bytes=(512 * 16384 * 2) * 2 + 16 * 512 * 512 * 4 * 2 + 512 * 512 * 2,
+                    bound="hbm", desc="split-K 512x512x16384, 16 slabs, fp32 partials")
+    cases["split_k"] = splitk
+
+    def flashattn():
+        BH, S, D = 128, 4096, 128
+        k, v, q = randn(BH, D, S), randn(BH, S, D), randn(BH, S, D)
+        out = torch.empty(BH, S, D, dtype=bf, device=cuda)
+        return dict(fn=lambda: lh.attention(k, v, q, out, causal=True, tile_m=128, tile_n=64),
+                    flop=4 * BH * S * S * D // 2, bytes=4 * BH * S * D * 2, bound="mfma",
+                    desc="flashattn fwd B4 H32 S4096 D128 causal")
+    cases["flashattn"] = flashattn
+
+    def decode():
+        B, H, D, S = 32, 32, 128, 8192
+        k, v, q = randn(B, D, S), randn(B, S, D), randn(B, H, D)
+        out = torch.empty(B, H, D, dtype=bf, device=cuda)
+        ws = torch.empty(lh.flash_decode_workspace_bytes(B, H, D, S, 512), dtype=torch.uint8,
+                         device=cuda)
+        return dict(fn=lambda: lh.flash_decode(k, v, q, out, ws, tile_s=512, tile_n=128),
+                    flop=4 * B * H * S * D, bytes=2 * B * S * D * 2 + 2 * B * H * D * 2,
+                    bound="hbm", desc="mqa_decode B32 H32/1KV D128 S8192, tile_s 512")
+    cases["mqa_decode"] = decode
+
+    def mamba():
+        b, L, H, P, N, Q = 4, 4096, 32, 64, 128, 256
+        nc = L // Q
+        x = randn(b, H, L, P)
+        C = randn(b, 1, L, N)
+        cb = randn(b, nc, 1, Q, Q)
+        dt = torch.nn.functional.softplus(torch.randn(b, H, nc, Q, generator=g, device=cuda))
+        A = -torch.exp(torch.rand(H, generator=g, device=cuda))
+        dA = torch.cumsum(dt * A[None, :, None, None], dim=-1)
+        Dh = torch.randn(H, generator=g, device=cuda)
+        prev = torch.randn(b, nc, H, N, P, generator=g, device=cuda)
+        out = torch.empty(b, H, L, P, dtype=bf, device=cuda)
+        nbytes = (cb.numel() + x.numel() + C.numel() + out.numel()) * 2 + \
+            (dt.numel() + dA.numel() + prev.numel() + Dh.numel()) * 4
+        flop = 2 * b * H * L * N * P + b * H * nc * Q * Q * P + 2 * b * H * L * P
+        return dict(fn=lambda: lh.helion_mamba2_chunk_scan_kernel(
+            cb, x, dt, dA, C, Dh, prev, out, tile_m=256, tile_n=64, tile_k=64),
+            flop=flop, bytes=nbytes, bound="hbm",
+            desc="mamba chunk_scan b4 L4096 h32 P64 N128 g1 Q256")
+    cases["mamba_chunk_scan"] = mamba
+    return cases
+
+
+def report(case, ms):
+    s = ms / 1e3
+    tflops = case["flop"] / s / 1e12
+    gbs = case["bytes"] / s / 1e9
+    if case["bound"] == "mfma":
+        frac = tflops / PEAK_BF16_TFLOPS
+    else:
+        # attainable: min(peak, AI * BW); bandwidth-bound configs report GB/s
+        frac = gbs / PEAK_HBM_GBS
+    return {"desc": case["desc"], "ms": round(ms, 5), "tflops": round(tflops, 2),
+            "gbs": round(gbs, 1), "bound": case["bound"], "roofline_frac": round(frac, 4)}
+
+
+def cpu_baseline(torch, a0, a1, budget_s=12.0):
+    """The fp32 C oracle on whole batches of the same workload until the time
+    budget is spent (at least one batch)."""
+    import numpy as np
+
+    import oracle
+    h0 = a0.view(torch.int16).cpu().numpy().view(np.uint16)
+    h1 = a1.view(torch.int16).cpu().numpy().view(np.uint16)
+    oracle.lib()
+    B, M, K = h0.shape
+    N = h1.shape[2]
+    done, t0 = 0, time.perf_counter()
+    while done < B:
+        oracle.batch_matmul(h0[done:done + 1], h1[done:done + 1], 1, 256, 256, 64)
+        done += 1
+        if time.perf_counter() - t0 > budget_s:
+            break
+    el = time.perf_counter() - t0
+    return {"value": round(2 * done * M * N * K / el / 1e12, 4), "unit": "TFLOP/s",
+            "cores": oracle.num_threads(), "kind": "port",
+            "sample": f"{done} of {B} batches of {M}x{N}x{K} (fp32 oracle, OpenMP), "
+                      f"{el:.1f} s"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print("bench.py: this build measures one GPU only (the kernels are single-GPU; "
+              "multi-GPU sharding is a design note), so --gpus must be 1", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import loom_hip as lh
+
+    assert torch.cuda.is_available(), "bench.py needs a ROCm GPU"
+    torch.cuda.set_device(0)
+    print(f"# device: {torch.cuda.get_device_name(0)}; {lh.__version__}", file=sys.stderr,
+          flush=True)
+
+    cases = make_cases(torch, lh)
+    head = cases["bmm"]()
+    for _ in range(args.warmup):
+        head["fn"]()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    durs = time_calls(torch, head["fn"], args.steps)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_step = elapsed / args.steps * 1e3
+    ms_kernel = sum(durs) / len(durs)
+    value = head["flop"] / (ms_step / 1e3) / 1e12
+    achieved = head["flop"] / (ms_kernel / 1e3) / 1e12
+    print(f"# bmm: {ms_step:.4f} ms/step wall, {ms_kernel:.4f} ms/launch (events)",
+          file=sys.stderr, flush=True)
+
+    line = {
+        "metric": "TFLOP/s and % of MI355X roofline per kernel; GB/s for mqa_decode (1 GPU)",
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded normal(0, 0.02) bf16, resident in HBM)",
+        "config": {"workload": "batch_matmul B16 M=N=K=2048 bf16, fp32 accumulate "
+                               "(BASELINE configs[1])",
+                   "tile_m": 256, "tile_n": 256, "tile_k": 64},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2),
+                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                     "traffic": traffic_for("gemm_bf16_kernel_256x256")},
+    }
+    a0_a1 = None
+    if not args.no_cpu:
+        gen = torch.Generator(device="cuda")
+        gen.manual_seed(1234)
+        a0 = (torch.randn(16, 2048, 2048, generator=gen, device="cuda") * 0.02).to(torch.bfloat16)
+        a1 = (torch.randn(16, 2048, 2048, generator=gen, device="cuda") * 0.02).to(torch.bfloat16)
+        a0_a1 = (a0, a1)
+        line["cpu_baseline"] = cpu_baseline(torch, a0, a1)
+        print(f"# cpu baseline: {line['cpu_baseline']}", file=sys.stderr, flush=True)
+    else:
+        line["cpu_baseline"] = None
+    del head, a0_a1
+    torch.cuda.empty_cache()
+
+    if args.kernels != "none":
+        names = list(cases) if args.kernels == "all" else args.kernels.split(",")
+        flush = Flusher(torch)
+        table = {}
+        for name in names:
+            case = cases[name]()
+            for _ in range(2):
+                case["fn"]()
+            torch.cuda.synchronize()
+            ms = median(time_calls(torch, case["fn"], args.iters, flush))
+            table[name] = report(case, ms)
+            print(f"# {name}: {table[name]}", file=sys.stderr, flush=True)
+            del case
+            torch.cuda.empty_cache()
+        line["kernels"] = table
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

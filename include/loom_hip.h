@@ -1,0 +1,131 @@
+/*
+ * loom_hip.h -- C ABI of the MI355X (gfx950) backend for the six loom-dataflow
+ * example kernels.
+ *
+ * One entry point per kernel, named after the MLIR function it implements and
+ * taking that function's tensors in the same order.  Tensors are plain device
+ * pointers to contiguous row-major buffers with the reference's layouts; bf16
+ * tensors hold raw bf16 bits, fp32 tensors IEEE floats.  Extents are explicit.
+ * The tile_* arguments are the loom.sym block sizes the staged-ETG solver
+ * binds (the `__tile_*` suffix of a materialized variant); each entry point
+ * validates them and documents how it maps them onto the GPU.
+ *
+ * Conventions shared by every entry point:
+ *   - `stream` is a hipStream_t (NULL = the default stream); work is only
+ *     enqueued, nothing synchronises.
+ *   - Return 0 on success; otherwise nonzero (1 = invalid argument,
+ *     2 = configuration not built for gfx950, 3 = HIP runtime error) with a
+ *     NUL-terminated message in err[0..errlen).  Nothing throws.
+ *   - The library never allocates per call and never frees caller memory;
+ *     kernels that gather partial results take a caller-owned workspace whose
+ *     size the matching *_workspace_bytes function returns.
+ *   - Calls are re-entrant; calls on different streams do not share state.
+ *
+ * Reference boundary replaced: the reference lowers these functions for a
+ * Tenstorrent backend after materialization
+ * (lib/pipeline/src/loom_materialization_pipeline.cpp:307-313, marked as
+ * the place to gate on a backend at :309-310); this library is what a
+ * gfx950 backend launches instead of those passes' output.
+ */
+#ifndef LOOM_HIP_H
+#define LOOM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Library version string ("loom_hip <major>.<minor>.<patch> gfx950").
+ * Counterpart of the pybind module's __version__
+ * (lib/pipeline/src/loom_pybind.cpp:17-20). */
+const char* loom_hip_version(void);
+
+/* @matmul -- examples/mm/IR/00_from_helion_frontend.mlir:2
+ *   (x: memref<MxK>, y: memref<KxN>, out: memref<MxN>)
+ * out = x . y, bf16 in, fp32 accumulate, bf16 out.
+ * (tile_m, tile_n) is the workgroup output tile: (64,64), (128,128) or
+ * (256,256).  tile_k is the K step of the reference loop; any value >= 1 is
+ * accepted and the kernel stages K in 64-deep LDS tiles (the result does not
+ * depend on it). */
+int loom_hip_matmul(const void* x, const void* y, void* out, int64_t M, int64_t N, int64_t K,
+                    int64_t tile_m, int64_t tile_n, int64_t tile_k, void* stream, char* err,
+                    size_t errlen);
+
+/* @batch_matmul -- examples/bmm_2Dmesh/IR/00_from_helion_frontend.mlir:4
+ *   (arg0: memref<BxMxK>, arg1: memref<BxKxN>, arg2: memref<BxMxN>)
+ * arg2[b] = arg0[b] . arg1[b].  Tiles as for loom_hip_matmul; tile_b >= 1
+ * groups batches in the reference grid and does not change the result. */
+int loom_hip_batch_matmul(const void* arg0, const void* arg1, void* arg2, int64_t B, int64_t M,
+                          int64_t N, int64_t K, int64_t tile_b, int64_t tile_m, int64_t tile_n,
+                          int64_t tile_k, void* stream, char* err, size_t errlen);
+
+/* Bytes of the fp32 partial stack [S, M, N], S = ceil(K / tile_k), that
+ * loom_hip_split_k_matmul_gather gathers into (the loom.gather target of
+ * examples/split_k_mm_gather/IR/00_from_helion_frontend.mlir:30-33). */
+size_t loom_hip_split_k_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t tile_k);
+
+/* @split_k_matmul_gather -- examples/split_k_mm_gather/IR/00_from_helion_frontend.mlir:2
+ *   (a: memref<MxK>, b: memref<KxN>, out: memref<MxN>)
+ * partials[s] = a[:, s*tile_k : (s+1)*tile_k] . b[s*tile_k : (s+1)*tile_k, :]
+ * in fp32 (slab s at gather index s), then out = bf16(sum_s partials[s]) in
+ * ascending s.  On return `partials` holds the gathered stack.  tile_k
+ * (1 <= tile_k <= K) fixes the slabs; (tile_m, tile_n) as for matmul. */
+int loom_hip_split_k_matmul_gather(const void* a, const void* b, void* out, void* partials,
+                                   size_t partials_bytes, int64_t M, int64_t N, int64_t K,
+                                   int64_t tile_m, int64_t tile_n, int64_t tile_k, void* stream,
+                                   char* err, size_t errlen);
+
+/* @attention -- examples/flashattn/IR/00_from_helion_frontend.mlir:4
+ *   (k: memref<BHxDxSkv>, v: memref<BHxSkvxD>, q: memref<BHxSqxD>, out: memref<BHxSqxD>)
+ * Flash-attention forward with online softmax; `scale` multiplies q.k (the
+ * reference hard-codes the f16 constant 0.08837890625 at :10); `causal`
+ * (not in the reference; needs Sq == Skv) hides key j from query i < j.
+ * tile_m (64 or 128) is the workgroup's query tile; tile_b (<= BH) and
+ * tile_n (<= Skv, the online-softmax step) are validated, the kernel steps
+ * KV in 64-key LDS blocks.  D = 64 or 128, Skv a multiple of 8. */
+int loom_hip_attention(const void* k, const void* v, const void* q, void* out, int64_t BH,
+                       int64_t Sq, int64_t Skv, int64_t D, float scale, int causal,
+                       int64_t tile_b, int64_t tile_m, int64_t tile_n, void* stream, char* err,
+                       size_t errlen);
+
+/* Bytes of the gathered split-KV partials of loom_hip_flash_decode: lse
+ * [ns, B, H] fp32 at offset 0, then o [ns, B, H, D] fp32 at offset
+ * align256(ns*B*H*4), ns = ceil(S / tile_s)
+ * (examples/mqa_decode/IR/00_from_helion_frontend.mlir:139-146). */
+size_t loom_hip_flash_decode_workspace_bytes(int64_t B, int64_t H, int64_t D, int64_t S,
+                                             int64_t tile_s);
+
+/* @flash_decode -- examples/mqa_decode/IR/00_from_helion_frontend.mlir:6
+ *   (k: memref<BxDxS>, v: memref<BxSxD>, q: memref<BxHxD>, out: memref<BxHxD>)
+ * H query heads share one KV head.  Split s covers keys
+ * [s*tile_s, (s+1)*tile_s); its (lse_s, o_s) land in the workspace and the
+ * split-0 combine writes out.  tile_b (<= B) and tile_n (<= S) are validated
+ * and do not change the result.  D = 64 or 128, H <= 32. */
+int loom_hip_flash_decode(const void* k, const void* v, const void* q, void* out,
+                          void* workspace, size_t workspace_bytes, int64_t B, int64_t H,
+                          int64_t D, int64_t S, float scale, int64_t tile_b, int64_t tile_s,
+                          int64_t tile_n, void* stream, char* err, size_t errlen);
+
+/* @helion_mamba2_chunk_scan_kernel -- examples/mamba_chunk_scan/IR/00_from_helion_frontend.mlir:4
+ *   (cb: [b,c,G,Q,Q] bf16, x: [b,H,L,P] bf16, dt: [b,H,c,Q] fp32,
+ *    dA_cumsum: [b,H,c,Q] fp32, C: [b,G,L,N] bf16, D: [H] fp32,
+ *    prev_states_T: [b,c,H,N,P] fp32, out: [b,H,L,P] bf16), L = c*Q.
+ * Mamba-2 SSD chunk scan with the intra-chunk causal mask k <= m.
+ * tile_b = tile_h = tile_c = 1 (the reference's size-1 subviews skip work
+ * otherwise); tile_m in {64,128,192,256} rows and tile_n in {16,32,64}
+ * columns form the workgroup tile; tile_k >= 1 is the reference's k step and
+ * does not change the result.  Q <= 256, N <= 128, Q, N, P multiples of 8. */
+int loom_hip_helion_mamba2_chunk_scan_kernel(
+    const void* cb, const void* x, const void* dt, const void* dA_cumsum, const void* C,
+    const void* D, const void* prev_states_T, void* out, int64_t batch, int64_t nchunks,
+    int64_t nheads, int64_t ngroups, int64_t chunk_size, int64_t headdim, int64_t dstate,
+    int64_t tile_b, int64_t tile_h, int64_t tile_c, int64_t tile_m, int64_t tile_n,
+    int64_t tile_k, void* stream, char* err, size_t errlen);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LOOM_HIP_H */

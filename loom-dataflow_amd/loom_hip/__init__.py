@@ -1,0 +1,237 @@
+"""Python front end of the gfx950 backend (``libloom_hip.so``).
+
+Mirrors the reference's kernel functions one for one -- same names, same
+tensor arguments in the same order, same ``tile_*`` block-size parameters --
+and calls the C ABI declared in ``include/loom_hip.h`` through ctypes on
+torch's current HIP stream.  Like the reference's Python API
+(``lib/pipeline/__init__.py:97-98,129-130``) a failure raises
+``RuntimeError`` (here the subclass ``LoomHipError``, carrying the ABI's
+return code) with the library's message.
+
+Tensors are torch tensors on a ROCm device: bf16 arguments as
+``torch.bfloat16``, fp32 arguments as ``torch.float32``, contiguous.  There
+is no CPU fallback: if the shared library is missing, importing this module
+raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(os.path.dirname(_HERE), "libloom_hip.so")
+
+if not os.path.exists(LIB_PATH):
+    raise ImportError(f"loom_hip: {LIB_PATH} is not built (run __graft_entry__.build())")
+
+_lib = ctypes.CDLL(LIB_PATH)
+
+_i64 = ctypes.c_int64
+_vp = ctypes.c_void_p
+_sz = ctypes.c_size_t
+_f32 = ctypes.c_float
+_ERR = (ctypes.c_char_p, _sz)
+
+_SIGS = {
+    "loom_hip_matmul": [_vp] * 3 + [_i64] * 6 + [_vp, *_ERR],
+    "loom_hip_batch_matmul": [_vp] * 3 + [_i64] * 8 + [_vp, *_ERR],
+    "loom_hip_split_k_matmul_gather": [_vp] * 4 + [_sz] + [_i64] * 6 + [_vp, *_ERR],
+    "loom_hip_attention": [_vp] * 4 + [_i64] * 4 + [_f32, ctypes.c_int] + [_i64] * 3
+    + [_vp, *_ERR],
+    "loom_hip_flash_decode": [_vp] * 5 + [_sz] + [_i64] * 4 + [_f32] + [_i64] * 3
+    + [_vp, *_ERR],
+    "loom_hip_helion_mamba2_chunk_scan_kernel": [_vp] * 8 + [_i64] * 13 + [_vp, *_ERR],
+}
+for _name, _args in _SIGS.items():
+    _fn = getattr(_lib, _name)
+    _fn.argtypes = _args
+    _fn.restype = ctypes.c_int
+_lib.loom_hip_split_k_workspace_bytes.argtypes = [_i64] * 4
+_lib.loom_hip_split_k_workspace_bytes.restype = _sz
+_lib.loom_hip_flash_decode_workspace_bytes.argtypes = [_i64] * 5
+_lib.loom_hip_flash_decode_workspace_bytes.restype = _sz
+_lib.loom_hip_version.restype = ctypes.c_char_p
+
+EXPORTED = tuple(_SIGS) + ("loom_hip_split_k_workspace_bytes",
+                           "loom_hip_flash_decode_workspace_bytes", "loom_hip_version")
+
+__version__ = _lib.loom_hip_version().decode()
+
+
+class LoomHipError(RuntimeError):
+    """A loom_hip entry point returned nonzero (``code``: 1 invalid argument,
+    2 not built for gfx950, 3 HIP runtime error)."""
+
+    def __init__(self, fn: str, code: int, msg: str):
+        super().__init__(f"{fn} failed (code {code}): {msg}")
+        self.code = code
+
+
+def _call(name: str, *args):
+    buf = ctypes.create_string_buffer(512)
+    rc = getattr(_lib, name)(*args, buf, len(buf))
+    if rc != 0:
+        raise LoomHipError(name, rc, buf.value.decode(errors="replace"))
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _need(t: torch.Tensor, name: str, dtype: torch.dtype, ndim: int) -> int:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name}: expected a torch.Tensor")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name}: must be on a ROCm device, got {t.device}")
+    if t.dtype != dtype:
+        raise TypeError(f"{name}: expected {dtype}, got {t.dtype}")
+    if t.dim() != ndim:
+        raise ValueError(f"{name}: expected {ndim} dims, got shape {tuple(t.shape)}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name}: must be contiguous")
+    return t.data_ptr()
+
+
+_bf16, _fp32 = torch.bfloat16, torch.float32
+
+
+# ---------------------------------------------------------------------------
+# kernels (examples/<k>/IR/00_from_helion_frontend.mlir)
+# ---------------------------------------------------------------------------
+
+def matmul(x, y, out=None, *, tile_m=128, tile_n=128, tile_k=64):
+    """@matmul (examples/mm/IR/00_from_helion_frontend.mlir:2): out = x . y."""
+    M, K = x.shape
+    N = y.shape[1]
+    if y.shape[0] != K:
+        raise ValueError(f"matmul: inner dims differ: {tuple(x.shape)} . {tuple(y.shape)}")
+    if out is None:
+        out = torch.empty((M, N), dtype=_bf16, device=x.device)
+    if tuple(out.shape) != (M, N):
+        raise ValueError("matmul: out shape mismatch")
+    _call("loom_hip_matmul", _need(x, "x", _bf16, 2), _need(y, "y", _bf16, 2),
+          _need(out, "out", _bf16, 2), M, N, K, tile_m, tile_n, tile_k, _stream(x))
+    return out
+
+
+def batch_matmul(arg0, arg1, arg2=None, *, tile_b=1, tile_m=256, tile_n=256, tile_k=64):
+    """@batch_matmul (examples/bmm_2Dmesh/IR/00_from_helion_frontend.mlir:4)."""
+    B, M, K = arg0.shape
+    N = arg1.shape[2]
+    if tuple(arg1.shape[:2]) != (B, K):
+        raise ValueError("batch_matmul: arg1 shape mismatch")
+    if arg2 is None:
+        arg2 = torch.empty((B, M, N), dtype=_bf16, device=arg0.device)
+    if tuple(arg2.shape) != (B, M, N):
+        raise ValueError("batch_matmul: arg2 shape mismatch")
+    _call("loom_hip_batch_matmul", _need(arg0, "arg0", _bf16, 3), _need(arg1, "arg1", _bf16, 3),
+          _need(arg2, "arg2", _bf16, 3), B, M, N, K, tile_b, tile_m, tile_n, tile_k,
+          _stream(arg0))
+    return arg2
+
+
+def split_k_workspace_bytes(M, N, K, tile_k) -> int:
+    return int(_lib.loom_hip_split_k_workspace_bytes(M, N, K, tile_k))
+
+
+def split_k_matmul_gather(a, b, out=None, partials=None, *, tile_m=64, tile_n=64, tile_k=1024):
+    """@split_k_matmul_gather (examples/split_k_mm_gather/IR/00_from_helion_frontend.mlir:2).
+
+    Returns (out [M,N] bf16, partials [S,M,N] fp32 -- the gathered K-slab
+    products, S = ceil(K / tile_k))."""
+    M, K = a.shape
+    N = b.shape[1]
+    if b.shape[0] != K:
+        raise ValueError("split_k_matmul_gather: inner dims differ")
+    S = -(-K // tile_k) if tile_k > 0 else 0
+    if out is None:
+        out = torch.empty((M, N), dtype=_bf16, device=a.device)
+    if partials is None:
+        partials = torch.empty((max(S, 1), M, N), dtype=_fp32, device=a.device)
+    _call("loom_hip_split_k_matmul_gather", _need(a, "a", _bf16, 2), _need(b, "b", _bf16, 2),
+          _need(out, "out", _bf16, 2), _need(partials, "partials", _fp32, 3),
+          partials.numel() * 4, M, N, K, tile_m, tile_n, tile_k, _stream(a))
+    return out, partials
+
+
+def attention(k, v, q, out=None, *, scale=None, causal=False, tile_b=1, tile_m=128,
+              tile_n=64):
+    """@attention (examples/flashattn/IR/00_from_helion_frontend.mlir:4).
+
+    k [BH,D,Skv] (keys transposed), v [BH,Skv,D], q [BH,Sq,D] -> out [BH,Sq,D].
+    ``scale`` defaults to 1/sqrt(D)."""
+    BH, D, Skv = k.shape
+    Sq = q.shape[1]
+    if tuple(v.shape) != (BH, Skv, D) or tuple(q.shape) != (BH, Sq, D):
+        raise ValueError("attention: k/v/q shapes disagree")
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    if out is None:
+        out = torch.empty((BH, Sq, D), dtype=_bf16, device=q.device)
+    _call("loom_hip_attention", _need(k, "k", _bf16, 3), _need(v, "v", _bf16, 3),
+          _need(q, "q", _bf16, 3), _need(out, "out", _bf16, 3), BH, Sq, Skv, D,
+          float(scale), int(bool(causal)), tile_b, tile_m, tile_n, _stream(q))
+    return out
+
+
+def flash_decode_workspace_bytes(B, H, D, S, tile_s) -> int:
+    return int(_lib.loom_hip_flash_decode_workspace_bytes(B, H, D, S, tile_s))
+
+
+def flash_decode(k, v, q, out=None, workspace=None, *, scale=None, tile_b=1, tile_s=512,
+                 tile_n=128, return_partials=False):
+    """@flash_decode (examples/mqa_decode/IR/00_from_helion_frontend.mlir:6).
+
+    k [B,D,S] (transposed), v [B,S,D], q [B,H,D] -> out [B,H,D].  With
+    ``return_partials`` also returns the gathered (lse [ns,B,H], o [ns,B,H,D])."""
+    B, D, S = k.shape
+    H = q.shape[1]
+    if tuple(v.shape) != (B, S, D) or tuple(q.shape) != (B, H, D):
+        raise ValueError("flash_decode: k/v/q shapes disagree")
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    if out is None:
+        out = torch.empty((B, H, D), dtype=_bf16, device=q.device)
+    nbytes = flash_decode_workspace_bytes(B, H, D, S, tile_s)
+    if workspace is None:
+        workspace = torch.empty(max(nbytes, 4), dtype=torch.uint8, device=q.device)
+    if workspace.device != q.device or workspace.dtype != torch.uint8 or \
+            not workspace.is_contiguous():
+        raise ValueError("flash_decode: workspace must be a contiguous uint8 tensor")
+    _call("loom_hip_flash_decode", _need(k, "k", _bf16, 3), _need(v, "v", _bf16, 3),
+          _need(q, "q", _bf16, 3), _need(out, "out", _bf16, 3), workspace.data_ptr(),
+          workspace.numel(), B, H, D, S, float(scale), tile_b, tile_s, tile_n, _stream(q))
+    if not return_partials:
+        return out
+    ns = -(-S // tile_s)
+    n_lse = ns * B * H
+    off = (n_lse * 4 + 255) // 256 * 256
+    lse = workspace[:n_lse * 4].view(torch.float32).view(ns, B, H)
+    o = workspace[off:off + n_lse * D * 4].view(torch.float32).view(ns, B, H, D)
+    return out, lse, o
+
+
+def helion_mamba2_chunk_scan_kernel(cb, x, dt, dA_cumsum, C, D, prev_states_T, out=None, *,
+                                    tile_b=1, tile_h=1, tile_c=1, tile_m=256, tile_n=64,
+                                    tile_k=64):
+    """@helion_mamba2_chunk_scan_kernel
+    (examples/mamba_chunk_scan/IR/00_from_helion_frontend.mlir:4)."""
+    b, nc, G, Q, _ = cb.shape
+    _, H, L, P = x.shape
+    N = C.shape[-1]
+    if L != nc * Q or tuple(C.shape) != (b, G, L, N) or tuple(dt.shape) != (b, H, nc, Q) \
+            or tuple(dA_cumsum.shape) != (b, H, nc, Q) or tuple(D.shape) != (H,) \
+            or tuple(prev_states_T.shape) != (b, nc, H, N, P):
+        raise ValueError("helion_mamba2_chunk_scan_kernel: argument shapes disagree")
+    if out is None:
+        out = torch.empty((b, H, L, P), dtype=_bf16, device=x.device)
+    _call("loom_hip_helion_mamba2_chunk_scan_kernel", _need(cb, "cb", _bf16, 5),
+          _need(x, "x", _bf16, 4), _need(dt, "dt", _fp32, 4),
+          _need(dA_cumsum, "dA_cumsum", _fp32, 4), _need(C, "C", _bf16, 4),
+          _need(D, "D", _fp32, 1), _need(prev_states_T, "prev_states_T", _fp32, 5),
+          _need(out, "out", _bf16, 4), b, nc, H, G, Q, P, N, tile_b, tile_h, tile_c,
+          tile_m, tile_n, tile_k, _stream(x))
+    return out
