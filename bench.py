@@ -11,8 +11,10 @@ of one call each, inputs resident in HBM.  It carries
   cpu_baseline  the fp32 C oracle (OpenMP, all host threads) on a bounded
                 sample of the same batches;
   kernels       every BASELINE configuration (mm, bmm, split-K, flashattn,
-                mqa_decode, mamba_chunk_scan) timed per call between cache
-                flushes, with its roofline fraction.
+                mqa_decode, mamba_chunk_scan): mean GPU time of calls enqueued
+                back to back, each call on a different copy of its inputs so
+                operands never stay in the 256 MB Infinity Cache between
+                calls, with its roofline fraction.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
                        [--kernels all|none|mm,bmm,...]
@@ -41,7 +43,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--kernels", default="all", help="per-kernel table: all, none or a list")
-    ap.add_argument("--iters", type=int, default=10, help="timed calls per kernel in the table")
+    ap.add_argument("--iters", type=int, default=20, help="timed calls per kernel in the table")
     return ap.parse_args()
 
 
@@ -55,31 +57,7 @@ def traffic_for(kernel):
         return None
 
 
-class Flusher:
-    """Evicts L2 and the 256 MB Infinity Cache by writing 512 MB."""
-
-    def __init__(self, torch):
-        self.buf = torch.empty(512 << 20, dtype=torch.uint8, device="cuda")
-
-    def __call__(self):
-        self.buf.fill_(1)
-
-
-def time_calls(torch, fn, iters, flush=None):
-    """Per-call durations (ms) from HIP events around each call on the
-    current stream (the stream the library launches on)."""
-    s = torch.cuda.current_stream()
-    evs = []
-    for _ in range(iters):
-        if flush is not None:
-            flush()
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record(s)
-        fn()
-        b.record(s)
-        evs.append((a, b))
-    torch.cuda.synchronize()
-    return [a.elapsed_time(b) for a, b in evs]
+MALL_BYTES = 256 << 20       # MI355X Infinity Cache
 
 
 def median(xs):
@@ -88,8 +66,26 @@ def median(xs):
     return xs[n // 2] if n % 2 else 0.5 * (xs[n // 2 - 1] + xs[n // 2])
 
 
+def time_back_to_back(torch, fn, iters):
+    """Mean GPU time (ms) of `iters` calls enqueued back to back, from one
+    pair of HIP events on the current stream (the stream the library launches
+    on).  fn(i) is the i-th call."""
+    s = torch.cuda.current_stream()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    a.record(s)
+    for i in range(iters):
+        fn(i)
+    b.record(s)
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / iters
+
+
 # --------------------------------------------------------------------------
-# BASELINE configurations
+# BASELINE configurations.  Each case holds enough independent copies of its
+# inputs that consecutive calls read more than three times the Infinity
+# Cache, so a call never finds its operands left in cache by the previous one
+# (the mm operands, 6 MB, stay cache resident whatever is done).
 # --------------------------------------------------------------------------
 
 def make_cases(torch, lh):
@@ -104,73 +100,87 @@ def make_cases(torch, lh):
     def unif(*shape):
         return (torch.rand(*shape, generator=g, device=cuda) * 2 - 1).to(bf)
 
+    def copies(nbytes):
+        return max(1, min(4, -(-3 * MALL_BYTES // nbytes)))
+
     cases = {}
 
     def mm():
         x, y = unif(1024, 1024), unif(1024, 1024)
         out = torch.empty(1024, 1024, dtype=bf, device=cuda)
-        return dict(fn=lambda: lh.matmul(x, y, out, tile_m=128, tile_n=128, tile_k=64),
-                    flop=2 * 1024 ** 3, bytes=3 * 1024 * 1024 * 2, bound="mfma",
-                    desc="mm 1024^3 bf16, tile 128x128")
+        return dict(fn=lambda i: lh.matmul(x, y, out, tile_m=128, tile_n=128, tile_k=64),
+                    flop=2 * 1024 ** 3, bytes=3 * 1024 * 1024 * 2, bound="mfma", sets=1,
+                    desc="mm 1024^3 bf16, tile 128x128 (operands cache resident)")
     cases["mm"] = mm
 
     def bmm():
-        a0, a1 = randn(16, 2048, 2048, std=0.02), randn(16, 2048, 2048, std=0.02)
-        out = torch.empty(16, 2048, 2048, dtype=bf, device=cuda)
-        return dict(fn=lambda: lh.batch_matmul(a0, a1, out, tile_m=256, tile_n=256),
-                    flop=2 * 16 * 2048 ** 3, bytes=3 * 16 * 2048 * 2048 * 2, bound="mfma",
+        nb = 3 * 16 * 2048 * 2048 * 2
+        n = copies(nb)
+        sets = [(randn(16, 2048, 2048, std=0.02), randn(16, 2048, 2048, std=0.02),
+                 torch.empty(16, 2048, 2048, dtype=bf, device=cuda)) for _ in range(n)]
+        return dict(fn=lambda i: lh.batch_matmul(*sets[i % n], tile_m=256, tile_n=256),
+                    flop=2 * 16 * 2048 ** 3, bytes=nb, bound="mfma", sets=n,
                     desc="bmm 16x2048^3 bf16, tile 256x256")
     cases["bmm"] = bmm
 
     def splitk():
-        a, b = randn(512, 16384, std=0.02), randn(16384, 512, std=0.02)
-        out = torch.empty(512, 512, dtype=bf, device=cuda)
-        parts = torch.empty(16, 512, 512, dtype=torch.float32, device=cuda)
-        return dict(fn=lambda: lh.split_k_matmul_gather(a, b, out, parts, tile_m=64, tile_n=64,
-                                                        tile_k=1024),
-                    flop=2 * 512 * 512 * 16384,
-                    bytes=(512 * 16384 * 2) * 2 + 16 * 512 * 512 * 4 * 2 + 512 * 512 * 2,
-                    bound="hbm", desc="split-K 512x512x16384, 16 slabs, fp32 partials")
+        nb = (512 * 16384 * 2) * 2 + 16 * 512 * 512 * 4 * 2 + 512 * 512 * 2
+        n = copies(nb)
+        sets = [(randn(512, 16384, std=0.02), randn(16384, 512, std=0.02),
+                 torch.empty(512, 512, dtype=bf, device=cuda),
+                 torch.empty(16, 512, 512, dtype=torch.float32, device=cuda)) for _ in range(n)]
+        return dict(fn=lambda i: lh.split_k_matmul_gather(*sets[i % n], tile_m=64, tile_n=64,
+                                                          tile_k=1024),
+                    flop=2 * 512 * 512 * 16384, bytes=nb, bound="hbm", sets=n,
+                    desc="split-K 512x512x16384, 16 slabs, fp32 partials")
     cases["split_k"] = splitk
 
     def flashattn():
         BH, S, D = 128, 4096, 128
-        k, v, q = randn(BH, D, S), randn(BH, S, D), randn(BH, S, D)
-        out = torch.empty(BH, S, D, dtype=bf, device=cuda)
-        return dict(fn=lambda: lh.attention(k, v, q, out, causal=True, tile_m=128, tile_n=64),
-                    flop=4 * BH * S * S * D // 2, bytes=4 * BH * S * D * 2, bound="mfma",
+        nb = 4 * BH * S * D * 2
+        n = min(2, copies(nb))
+        sets = [(randn(BH, D, S), randn(BH, S, D), randn(BH, S, D),
+                 torch.empty(BH, S, D, dtype=bf, device=cuda)) for _ in range(n)]
+        return dict(fn=lambda i: lh.attention(*sets[i % n], causal=True, tile_m=128, tile_n=64),
+                    flop=4 * BH * S * S * D // 2, bytes=nb, bound="mfma", sets=n,
                     desc="flashattn fwd B4 H32 S4096 D128 causal")
     cases["flashattn"] = flashattn
 
     def decode():
         B, H, D, S = 32, 32, 128, 8192
-        k, v, q = randn(B, D, S), randn(B, S, D), randn(B, H, D)
-        out = torch.empty(B, H, D, dtype=bf, device=cuda)
-        ws = torch.empty(lh.flash_decode_workspace_bytes(B, H, D, S, 512), dtype=torch.uint8,
-                         device=cuda)
-        return dict(fn=lambda: lh.flash_decode(k, v, q, out, ws, tile_s=512, tile_n=128),
-                    flop=4 * B * H * S * D, bytes=2 * B * S * D * 2 + 2 * B * H * D * 2,
-                    bound="hbm", desc="mqa_decode B32 H32/1KV D128 S8192, tile_s 512")
+        nb = 2 * B * S * D * 2 + 2 * B * H * D * 2
+        n = copies(nb)
+        sets = [(randn(B, D, S), randn(B, S, D), randn(B, H, D),
+                 torch.empty(B, H, D, dtype=bf, device=cuda),
+                 lh.flash_decode_workspace(B, H, D, S, 1024, cuda)) for _ in range(n)]
+        return dict(fn=lambda i: lh.flash_decode(*sets[i % n], tile_s=1024, tile_n=128),
+                    flop=4 * B * H * S * D, bytes=nb, bound="hbm", sets=n,
+                    desc="mqa_decode B32 H32/1KV D128 S8192, tile_s 1024")
     cases["mqa_decode"] = decode
 
     def mamba():
         b, L, H, P, N, Q = 4, 4096, 32, 64, 128, 256
         nc = L // Q
-        x = randn(b, H, L, P)
-        C = randn(b, 1, L, N)
-        cb = randn(b, nc, 1, Q, Q)
-        dt = torch.nn.functional.softplus(torch.randn(b, H, nc, Q, generator=g, device=cuda))
-        A = -torch.exp(torch.rand(H, generator=g, device=cuda))
-        dA = torch.cumsum(dt * A[None, :, None, None], dim=-1)
-        Dh = torch.randn(H, generator=g, device=cuda)
-        prev = torch.randn(b, nc, H, N, P, generator=g, device=cuda)
-        out = torch.empty(b, H, L, P, dtype=bf, device=cuda)
-        nbytes = (cb.numel() + x.numel() + C.numel() + out.numel()) * 2 + \
-            (dt.numel() + dA.numel() + prev.numel() + Dh.numel()) * 4
+
+        def one():
+            x = randn(b, H, L, P)
+            C = randn(b, 1, L, N)
+            cb = randn(b, nc, 1, Q, Q)
+            dt = torch.nn.functional.softplus(torch.randn(b, H, nc, Q, generator=g, device=cuda))
+            A = -torch.exp(torch.rand(H, generator=g, device=cuda))
+            dA = torch.cumsum(dt * A[None, :, None, None], dim=-1)
+            Dh = torch.randn(H, generator=g, device=cuda)
+            prev = torch.randn(b, nc, H, N, P, generator=g, device=cuda)
+            out = torch.empty(b, H, L, P, dtype=bf, device=cuda)
+            return (cb, x, dt, dA, C, Dh, prev, out)
+        first = one()
+        nb = sum(t.numel() * t.element_size() for t in first)
+        n = copies(nb)
+        sets = [first] + [one() for _ in range(n - 1)]
         flop = 2 * b * H * L * N * P + b * H * nc * Q * Q * P + 2 * b * H * L * P
-        return dict(fn=lambda: lh.helion_mamba2_chunk_scan_kernel(
-            cb, x, dt, dA, C, Dh, prev, out, tile_m=256, tile_n=64, tile_k=64),
-            flop=flop, bytes=nbytes, bound="hbm",
+        return dict(fn=lambda i: lh.helion_mamba2_chunk_scan_kernel(
+            *sets[i % n], tile_m=256, tile_n=64, tile_k=64),
+            flop=flop, bytes=nb, bound="hbm", sets=n,
             desc="mamba chunk_scan b4 L4096 h32 P64 N128 g1 Q256")
     cases["mamba_chunk_scan"] = mamba
     return cases
@@ -183,10 +193,10 @@ def report(case, ms):
     if case["bound"] == "mfma":
         frac = tflops / PEAK_BF16_TFLOPS
     else:
-        # attainable: min(peak, AI * BW); bandwidth-bound configs report GB/s
         frac = gbs / PEAK_HBM_GBS
     return {"desc": case["desc"], "ms": round(ms, 5), "tflops": round(tflops, 2),
-            "gbs": round(gbs, 1), "bound": case["bound"], "roofline_frac": round(frac, 4)}
+            "gbs": round(gbs, 1), "bound": case["bound"], "roofline_frac": round(frac, 4),
+            "input_copies": case["sets"]}
 
 
 def cpu_baseline(torch, a0, a1, budget_s=12.0):
@@ -229,15 +239,20 @@ def main():
 
     cases = make_cases(torch, lh)
     head = cases["bmm"]()
-    for _ in range(args.warmup):
-        head["fn"]()
+    for i in range(args.warmup):
+        head["fn"](i)
     torch.cuda.synchronize()
+    s = torch.cuda.current_stream()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
-    durs = time_calls(torch, head["fn"], args.steps)
+    ev0.record(s)
+    for i in range(args.steps):
+        head["fn"](i)
+    ev1.record(s)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     ms_step = elapsed / args.steps * 1e3
-    ms_kernel = sum(durs) / len(durs)
+    ms_kernel = ev0.elapsed_time(ev1) / args.steps   # GPU time per launch (one kernel per call)
     value = head["flop"] / (ms_step / 1e3) / 1e12
     achieved = head["flop"] / (ms_kernel / 1e3) / 1e12
     print(f"# bmm: {ms_step:.4f} ms/step wall, {ms_kernel:.4f} ms/launch (events)",
@@ -280,14 +295,12 @@ def main():
 
     if args.kernels != "none":
         names = list(cases) if args.kernels == "all" else args.kernels.split(",")
-        flush = Flusher(torch)
         table = {}
         for name in names:
             case = cases[name]()
-            for _ in range(2):
-                case["fn"]()
-            torch.cuda.synchronize()
-            ms = median(time_calls(torch, case["fn"], args.iters, flush))
+            for i in range(2):
+                case["fn"](i)
+            ms = time_back_to_back(torch, case["fn"], args.iters)
             table[name] = report(case, ms)
             print(f"# {name}: {table[name]}", file=sys.stderr, flush=True)
             del case

@@ -90,19 +90,20 @@ int loom_hip_attention(const void* k, const void* v, const void* q, void* out, i
                        int64_t tile_b, int64_t tile_m, int64_t tile_n, void* stream, char* err,
                        size_t errlen);
 
-/* Bytes of the gathered split-KV partials of loom_hip_flash_decode: lse
- * [ns, B, H] fp32 at offset 0, then o [ns, B, H, D] fp32 at offset
- * align256(ns*B*H*4), ns = ceil(S / tile_s)
- * (examples/mqa_decode/IR/00_from_helion_frontend.mlir:139-146). */
+/* Bytes of loom_hip_flash_decode's workspace, the gathered split-KV
+ * partials (examples/mqa_decode/IR/00_from_helion_frontend.mlir:139-146):
+ * lse [ns, B, H] fp32 at offset 0, then o [ns, B, H, D] fp32 at offset
+ * align256(ns*B*H*4); ns = ceil(S / tile_s). */
 size_t loom_hip_flash_decode_workspace_bytes(int64_t B, int64_t H, int64_t D, int64_t S,
                                              int64_t tile_s);
 
 /* @flash_decode -- examples/mqa_decode/IR/00_from_helion_frontend.mlir:6
  *   (k: memref<BxDxS>, v: memref<BxSxD>, q: memref<BxHxD>, out: memref<BxHxD>)
  * H query heads share one KV head.  Split s covers keys
- * [s*tile_s, (s+1)*tile_s); its (lse_s, o_s) land in the workspace and the
- * split-0 combine writes out.  tile_b (<= B) and tile_n (<= S) are validated
- * and do not change the result.  D = 64 or 128, H <= 32. */
+ * [s*tile_s, (s+1)*tile_s); its (lse_s, o_s) land in the workspace, then a
+ * second kernel performs the split-0 combine into out.  tile_b (<= B) and
+ * tile_n (<= S) are validated and do not change the result.  D = 64 or 128,
+ * H <= 32. */
 int loom_hip_flash_decode(const void* k, const void* v, const void* q, void* out,
                           void* workspace, size_t workspace_bytes, int64_t B, int64_t H,
                           int64_t D, int64_t S, float scale, int64_t tile_b, int64_t tile_s,

@@ -37,8 +37,15 @@ LOOM_DEV uint32_t f2bf(float f) {
   return u >> 16;
 }
 
-// two fp32 -> one dword holding (lo = bf16(a), hi = bf16(b))
-LOOM_DEV uint32_t pack_bf16x2(float a, float b) { return f2bf(a) | (f2bf(b) << 16); }
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// two fp32 -> one dword holding (lo = bf16(a), hi = bf16(b)): gfx950's
+// v_cvt_pk_bf16_f32, round to nearest even (the same bits as f2bf for every
+// non-NaN input)
+LOOM_DEV uint32_t pack_bf16x2(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
+}
 
 // D[16x16] += A[16x32] . B[32x16]; lane l supplies row (A) / column (B)
 // l % 16 and eight consecutive k of group l / 16; D lands as rows
@@ -49,9 +56,10 @@ LOOM_DEV f32x4_t mfma16(const u32x4_t& a, const u32x4_t& b, const f32x4_t& c) {
 }
 
 // Pack the low (pack_lo) or high (pack_hi) 16-bit halves of two dwords:
-// result low half from x, high half from y.
-LOOM_DEV uint32_t pack_lo(uint32_t x, uint32_t y) { return (x & 0xffffu) | (y << 16); }
-LOOM_DEV uint32_t pack_hi(uint32_t x, uint32_t y) { return (x >> 16) | (y & 0xffff0000u); }
+// result low half from x, high half from y.  One v_perm_b32 each: the
+// selector picks bytes of the 64-bit value {y, x} (x = bytes 0-3).
+LOOM_DEV uint32_t pack_lo(uint32_t x, uint32_t y) { return __builtin_amdgcn_perm(y, x, 0x05040100u); }
+LOOM_DEV uint32_t pack_hi(uint32_t x, uint32_t y) { return __builtin_amdgcn_perm(y, x, 0x07060302u); }
 
 // 8x8 transpose of 16-bit elements held as 8 rows of u32x4 (row r = eight
 // consecutive columns).  Output column c = eight consecutive rows.
@@ -111,3 +119,34 @@ static inline int loom_check_launch(char* err, size_t errlen, const char* what) 
 
 static inline int64_t cdiv64(int64_t a, int64_t b) { return (a + b - 1) / b; }
 static inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// ---------------------------------------------------------------------------
+// raw buffer loads: range-checked by the hardware against `bytes` (reads past
+// the end return zeros and issue no memory request), so guarded loads need
+// no branch
+// ---------------------------------------------------------------------------
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+LOOM_DEV rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+}
+LOOM_DEV u32x4_t buf_load16(rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+LOOM_DEV u32x2_t buf_load8(rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
+}
+LOOM_DEV uint32_t buf_load2(rsrc_t r, uint32_t off) {
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+}
+
+LOOM_DEV float wave_max(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m));
+  return v;
+}
+LOOM_DEV float wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
+  return v;
+}

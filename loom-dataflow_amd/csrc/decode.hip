@@ -31,7 +31,7 @@
 namespace {
 
 constexpr int kWaves = 4;
-constexpr int kBlockKeys = 128;   // keys per wave step: 16 lanes x 8 keys
+constexpr int kBlockKeys = 64;    // keys per wave block: 16 lanes x 4 keys
 
 struct DecodeParams {
   const uint16_t* k;
@@ -39,24 +39,80 @@ struct DecodeParams {
   const uint16_t* q;
   float* lse;  // [ns, B, H]
   float* o;    // [ns, B, H, D]
+  uint16_t* out;
   int B, H, S, tile_s, ns;
   float c2;    // scale * log2(e)
 };
 
-template <int VEC>
-struct VRow;
-template <>
-struct VRow<8> { typedef u32x4_t T; };
-template <>
-struct VRow<4> { typedef u32x2_t T; };
+// Split-0 combine of the reference (:147-199), one wave per (b, head):
+// lane s < 64 holds lse_s, M = max_s lse_s and den = sum_s exp(lse_s - M)
+// are wave reductions, then every lane accumulates out[d] = sum_s w_s o_s[d]
+// (w_s = exp(lse_s - M) / den, ascending s) for its D/64 values of d with
+// eight splits' loads in flight at a time.  Splits beyond 64 are taken in
+// chunks of 64.
+template <int D>
+__global__ void __launch_bounds__(256) decode_combine_kernel(DecodeParams p) {
+  constexpr int DPL = D / 64;  // d values per lane
+  const int lane = threadIdx.x & 63;
+  const int64_t BH = (int64_t)p.B * p.H;
+  const int64_t bh = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (bh >= BH) return;
+  const int ns = p.ns;
+  float M = -INFINITY;
+  for (int s = lane; s < ns; s += 64) M = fmaxf(M, p.lse[s * BH + bh]);
+  M = wave_max(M);
+  float den = 0.f;
+  for (int s = lane; s < ns; s += 64) den += expf(p.lse[s * BH + bh] - M);
+  den = wave_sum(den);
+  float acc[DPL];
+#pragma unroll
+  for (int i = 0; i < DPL; ++i) acc[i] = 0.f;
+  for (int c0 = 0; c0 < ns; c0 += 64) {
+    const int sl = c0 + lane;
+    const float wl = sl < ns ? expf(p.lse[sl * BH + bh] - M) / den : 0.f;
+    const int cn = min(64, ns - c0);
+    for (int u0 = 0; u0 < cn; u0 += 8) {
+      float v[8][DPL];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int s = c0 + min(u0 + u, cn - 1);  // clamped: weight 0 past the end
+        const float* src = p.o + (s * BH + bh) * D + lane * DPL;
+#pragma unroll
+        for (int i = 0; i < DPL; ++i) v[u][i] = src[i];
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const float w = u0 + u < cn ? __shfl(wl, u0 + u) : 0.f;
+#pragma unroll
+        for (int i = 0; i < DPL; ++i) acc[i] += v[u][i] * w;
+      }
+    }
+  }
+  uint16_t* dst = p.out + bh * D + lane * DPL;
+  if constexpr (DPL == 2)
+    *reinterpret_cast<uint32_t*>(dst) = pack_bf16x2(acc[0], acc[1]);
+  else
+    dst[0] = (uint16_t)f2bf(acc[0]);
+}
 
-// D = head dim (64 or 128), HT = head tiles of 16, ALIGNED = S and tile_s
-// are multiples of 8 (16-byte K chunks never straddle the split end).
+// D = head dim (64 or 128), HT = head tiles of 16, ALIGNED = S is a
+// multiple of 4 (8-byte K chunks start on 8-byte boundaries).
+//
+// Each wave walks its 64-key blocks as NSTEPS load steps of eight loads:
+// DSTEPS steps of K (eight d rows x 4 keys per lane, 8-byte loads) then two
+// steps of V (eight keys x VEC d per lane).  Loads run one step ahead of the
+// math through a two-slot register ring, continuing into the wave's next
+// block; with two waves per SIMD the other wave's math covers the rest of
+// the latency.  All loads are raw buffer loads: anything past the tensor
+// reads as zero, and keys past the split end are masked to -inf before the
+// softmax (so their V rows are multiplied by exactly 0).
 template <int D, int HT, bool ALIGNED>
 __global__ void __launch_bounds__(64 * kWaves) decode_split_kernel(DecodeParams p) {
   constexpr int VEC = D / 16;     // d values per lane per V row, also # of d tiles
   constexpr int DSTEPS = D / 32;  // 32-deep MFMA steps over d
-  typedef typename VRow<VEC>::T vrow_t;
+  constexpr int NSTEPS = DSTEPS + 2;
+  constexpr int R = 2;            // ring slots
+  static_assert(NSTEPS % R == 0, "ring must divide the step count");
   constexpr int HP = HT * 16;     // padded head count
   constexpr int ACC_STRIDE = D + 1;
   __shared__ float sm_m[kWaves][HP];
@@ -69,21 +125,58 @@ __global__ void __launch_bounds__(64 * kWaves) decode_split_kernel(DecodeParams 
   const int H = p.H, S = p.S;
   const int s0 = split * p.tile_s;
   const int s1 = min(S, s0 + p.tile_s);
+  const int nblk = (s1 - s0 + kBlockKeys - 1) / kBlockKeys;
 
-  const uint16_t* __restrict__ kb = p.k + (int64_t)b * D * S;
-  const uint16_t* __restrict__ vb = p.v + (int64_t)b * S * D;
+  const rsrc_t krs = make_rsrc(p.k + (int64_t)b * D * S, (uint32_t)(D * S * 2));
+  const rsrc_t vrs = make_rsrc(p.v + (int64_t)b * S * D, (uint32_t)(S * D * 2));
   const uint16_t* __restrict__ qb = p.q + (int64_t)b * H * D;
 
-  // Q^T operand: lane holds q[h = r + 16 ht][32 ds + 8 g .. +7]
-  u32x4_t qf[DSTEPS][HT];
-#pragma unroll
-  for (int ht = 0; ht < HT; ++ht) {
-    const int h = r + 16 * ht;
-#pragma unroll
-    for (int ds = 0; ds < DSTEPS; ++ds)
-      qf[ds][ht] = h < H ? *reinterpret_cast<const u32x4_t*>(qb + (int64_t)h * D + ds * 32 + g * 8)
-                         : u32x4_t{0u, 0u, 0u, 0u};
+  // Q^T operands, shared by the waves through LDS: slot [ds][ht][lane]
+  // holds q[h = r + 16 ht][32 ds + 8 g .. +7]
+  __shared__ u32x4_t sm_q[DSTEPS][HT][64];
+  for (int e = threadIdx.x; e < DSTEPS * HT * 64; e += 64 * kWaves) {
+    const int ln = e & 63, ht = (e >> 6) % HT, ds = (e >> 6) / HT;
+    const int h = (ln & 15) + 16 * ht;
+    sm_q[ds][ht][ln] = h < H ? *reinterpret_cast<const u32x4_t*>(qb + (int64_t)h * D + ds * 32 +
+                                                                  (ln >> 4) * 8)
+                             : u32x4_t{0u, 0u, 0u, 0u};
   }
+  __syncthreads();
+
+  // ---- loads of step `st` of the block starting at key `base`
+  auto issue = [&](int base, int st, u32x4_t (&buf)[8]) {
+    if (st < DSTEPS) {
+      // K rows d = 32 st + 8 g + e, keys base + 4 r .. +3
+      const uint32_t off = ((uint32_t)(st * 32 + g * 8) * S + base + r * 4) * 2;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t o = off + (uint32_t)(e * S) * 2;
+        if constexpr (ALIGNED) {
+          const u32x2_t w = buf_load8(krs, o);
+          buf[e] = u32x4_t{w[0], w[1], 0u, 0u};
+        } else {
+          uint32_t h[4];
+#pragma unroll
+          for (int x = 0; x < 4; ++x) h[x] = buf_load2(krs, o + 2 * x);
+          buf[e] = u32x4_t{h[0] | (h[1] << 16), h[2] | (h[3] << 16), 0u, 0u};
+        }
+      }
+    } else {
+      // V rows for 32-key step c: slot t holds key base + 16 g + 4 (t%4) + 2c + t/4
+      const int c = st - DSTEPS;
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        const int key = base + 16 * g + 4 * (t & 3) + 2 * c + (t >> 2);
+        const uint32_t o = ((uint32_t)key * D + r * VEC) * 2;
+        if constexpr (VEC == 8) {
+          buf[t] = buf_load16(vrs, o);
+        } else {
+          const u32x2_t w = buf_load8(vrs, o);
+          buf[t] = u32x4_t{w[0], w[1], 0u, 0u};
+        }
+      }
+    }
+  };
 
   float m_run[HT], l_run[HT];
   f32x4_t ot[VEC][HT];
@@ -95,108 +188,107 @@ __global__ void __launch_bounds__(64 * kWaves) decode_split_kernel(DecodeParams 
     for (int u = 0; u < VEC; ++u) ot[u][ht] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   }
 
-  for (int base = s0 + wave * kBlockKeys; base < s1; base += kWaves * kBlockKeys) {
-    // ---- S^T = K^T Q^T over the block's 128 keys
-    f32x4_t st[8][HT];
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-#pragma unroll
-      for (int ht = 0; ht < HT; ++ht) st[j][ht] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    const int key0 = base + r * 8;  // this lane's 8 keys: key0 .. key0+7
-#pragma unroll
-    for (int ds = 0; ds < DSTEPS; ++ds) {
-      u32x4_t kr[8], kt[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const uint16_t* row = kb + (int64_t)(ds * 32 + g * 8 + e) * S;
-        if constexpr (ALIGNED) {
-          kr[e] = key0 < s1 ? *reinterpret_cast<const u32x4_t*>(row + key0)
-                            : u32x4_t{0u, 0u, 0u, 0u};
-        } else {
-          uint32_t h[8];
-#pragma unroll
-          for (int x = 0; x < 8; ++x) h[x] = key0 + x < s1 ? (uint32_t)row[key0 + x] : 0u;
-          kr[e] = u32x4_t{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
-                          h[6] | (h[7] << 16)};
-        }
-      }
-      transpose8x8(kr, kt);  // kt[j] = d values 32ds+8g..+7 of key key0 + j
-#pragma unroll
-      for (int j = 0; j < 8; ++j)
-#pragma unroll
-        for (int ht = 0; ht < HT; ++ht) st[j][ht] = mfma16(kt[j], qf[ds][ht], st[j][ht]);
-    }
+  u32x4_t ring[R][8];
+  if (wave < nblk) issue(s0 + wave * kBlockKeys, 0, ring[0]);
 
-    // ---- online softmax (log2 domain).  st[j][ht][i] is the score of key
-    // base + 8*(4g+i) + j for head r + 16 ht.
-    float alpha[HT];
+  for (int bi = wave; bi < nblk; bi += kWaves) {
+    const int base = s0 + bi * kBlockKeys;
+    const bool has_next = bi + kWaves < nblk;
+    const int next_base = base + kWaves * kBlockKeys;
+    f32x4_t st_acc[4][HT];
 #pragma unroll
-    for (int ht = 0; ht < HT; ++ht) {
-      float mx = -INFINITY;
+    for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int key = base + 8 * (4 * g + i) + j;
-          float t = st[j][ht][i] * p.c2;
-          if (key >= s1) t = -INFINITY;
-          st[j][ht][i] = t;
-          mx = fmaxf(mx, t);
-        }
-      mx = fmaxf(mx, __shfl_xor(mx, 16));
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float m_new = fmaxf(m_run[ht], mx);
-      alpha[ht] = fast_exp2(m_run[ht] - m_new);
-      m_run[ht] = m_new;
-      float ls = 0.f;
-#pragma unroll
-      for (int j = 0; j < 8; ++j)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float pv = fast_exp2(st[j][ht][i] - m_new);
-          st[j][ht][i] = pv;
-          ls += pv;
-        }
-      l_run[ht] = l_run[ht] * alpha[ht] + ls;
-#pragma unroll
-      for (int u = 0; u < VEC; ++u) ot[u][ht] *= alpha[ht];
-    }
+      for (int ht = 0; ht < HT; ++ht) st_acc[j][ht] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-    // ---- O^T += V^T P^T, 32 keys per MFMA step (tiles j0 = 2c, j1 = 2c+1)
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int j0 = 2 * c, j1 = 2 * c + 1;
-      u32x4_t pf[HT];
+    for (int st = 0; st < NSTEPS; ++st) {
+      // prefetch the next step (the next block's first step at the end)
+      if (st + 1 < NSTEPS)
+        issue(base, st + 1, ring[(st + 1) % R]);
+      else if (has_next)
+        issue(next_base, 0, ring[(st + 1) % R]);
+
+      u32x4_t (&cur)[8] = ring[st % R];
+      if (st < DSTEPS) {
+        // ---- S^T += K^T Q^T for d rows 32 st .. +31; kt[j] = d values
+        // 32st+8g..+7 of key base + 4r + j (8x4 transpose of 16-bit values)
+        u32x4_t kt[4];
 #pragma unroll
-      for (int ht = 0; ht < HT; ++ht)
-        pf[ht] = u32x4_t{pack_bf16x2(st[j0][ht][0], st[j0][ht][1]),
-                         pack_bf16x2(st[j0][ht][2], st[j0][ht][3]),
-                         pack_bf16x2(st[j1][ht][0], st[j1][ht][1]),
-                         pack_bf16x2(st[j1][ht][2], st[j1][ht][3])};
-      // k slot t of group g: key base + 8*(4g + t%4) + (t<4 ? j0 : j1)
-      vrow_t vr[8];
+        for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int t = 0; t < 8; ++t) {
-        const int key = base + 8 * (4 * g + (t & 3)) + (t < 4 ? j0 : j1);
-        if (key < s1)
-          vr[t] = *reinterpret_cast<const vrow_t*>(vb + (int64_t)key * D + r * VEC);
-        else
-          vr[t] = vrow_t{};
+          for (int i = 0; i < 4; ++i) {
+            const uint32_t x = cur[2 * i][j / 2], y = cur[2 * i + 1][j / 2];
+            kt[j][i] = (j & 1) ? pack_hi(x, y) : pack_lo(x, y);
+          }
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int ht = 0; ht < HT; ++ht) st_acc[j][ht] = mfma16(kt[j], sm_q[st][ht][lane], st_acc[j][ht]);
       }
-      // transpose: va[u] = V[key_t][VEC*r + u] for t = 0..7
-      u32x4_t va[VEC];
+      if (st == DSTEPS - 1) {
+        // ---- online softmax (log2 domain); st_acc[j][ht][i] is the score of
+        // key base + 16 g + 4 i + j for head r + 16 ht
+        if (base + kBlockKeys > s1) {  // keys past the split end: -inf
 #pragma unroll
-      for (int u = 0; u < VEC; ++u) {
+          for (int ht = 0; ht < HT; ++ht)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const uint32_t x = vr[2 * i][u / 2], y = vr[2 * i + 1][u / 2];
-          va[u][i] = (u & 1) ? pack_hi(x, y) : pack_lo(x, y);
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+              for (int i = 0; i < 4; ++i)
+                if (base + 16 * g + 4 * i + j >= s1) st_acc[j][ht][i] = -INFINITY;
+        }
+#pragma unroll
+        for (int ht = 0; ht < HT; ++ht) {
+          // max of the raw scores; scale > 0 commutes with max
+          float mx = -INFINITY;
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) mx = fmaxf(mx, st_acc[j][ht][i]);
+          mx = fmaxf(mx, __shfl_xor(mx, 16));
+          mx = fmaxf(mx, __shfl_xor(mx, 32));
+          const float m_new = fmaxf(m_run[ht], mx * p.c2);
+          const float alpha = fast_exp2(m_run[ht] - m_new);
+          m_run[ht] = m_new;
+          float ls = 0.f;
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const float pv = fast_exp2(__builtin_fmaf(st_acc[j][ht][i], p.c2, -m_new));
+              st_acc[j][ht][i] = pv;
+              ls += pv;
+            }
+          l_run[ht] = l_run[ht] * alpha + ls;
+#pragma unroll
+          for (int u = 0; u < VEC; ++u) ot[u][ht] *= alpha;
         }
       }
+      if (st >= DSTEPS) {
+        // ---- O^T += V^T P^T over keys of tiles j0 = 2c, j1 = 2c + 1
+        const int c = st - DSTEPS, j0 = 2 * c, j1 = 2 * c + 1;
+        u32x4_t pf[HT];
 #pragma unroll
-      for (int u = 0; u < VEC; ++u)
+        for (int ht = 0; ht < HT; ++ht)
+          pf[ht] = u32x4_t{pack_bf16x2(st_acc[j0][ht][0], st_acc[j0][ht][1]),
+                           pack_bf16x2(st_acc[j0][ht][2], st_acc[j0][ht][3]),
+                           pack_bf16x2(st_acc[j1][ht][0], st_acc[j1][ht][1]),
+                           pack_bf16x2(st_acc[j1][ht][2], st_acc[j1][ht][3])};
+        // transpose: va[u] = V[key_t][VEC r + u] for slots t = 0..7
+        u32x4_t va[VEC];
 #pragma unroll
-        for (int ht = 0; ht < HT; ++ht) ot[u][ht] = mfma16(va[u], pf[ht], ot[u][ht]);
+        for (int u = 0; u < VEC; ++u)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const uint32_t x = cur[2 * i][u / 2], y = cur[2 * i + 1][u / 2];
+            va[u][i] = (u & 1) ? pack_hi(x, y) : pack_lo(x, y);
+          }
+#pragma unroll
+        for (int u = 0; u < VEC; ++u)
+#pragma unroll
+          for (int ht = 0; ht < HT; ++ht) ot[u][ht] = mfma16(va[u], pf[ht], ot[u][ht]);
+      }
     }
   }
 
@@ -236,26 +328,7 @@ __global__ void __launch_bounds__(64 * kWaves) decode_split_kernel(DecodeParams 
     p.o[(row0 + h) * D + d] = o / L;
     if (d == 0) p.lse[row0 + h] = logf(L) + M * 0.69314718055994530942f;
   }
-}
 
-// Split-0 combine of the reference (:147-199), one workgroup per (b, head).
-__global__ void __launch_bounds__(128) decode_combine_kernel(const float* __restrict__ lse,
-                                                             const float* __restrict__ o,
-                                                             uint16_t* __restrict__ out,
-                                                             int BH, int D, int ns) {
-  const int bh = blockIdx.x;
-  float M = -INFINITY;
-  for (int s = 0; s < ns; ++s) M = fmaxf(M, lse[(int64_t)s * BH + bh]);
-  float den = 0.f;
-  for (int s = 0; s < ns; ++s) den += expf(lse[(int64_t)s * BH + bh] - M);
-  for (int d = threadIdx.x; d < D; d += blockDim.x) {
-    float acc = 0.f;
-    for (int s = 0; s < ns; ++s) {
-      const float w = expf(lse[(int64_t)s * BH + bh] - M) / den;
-      acc += o[((int64_t)s * BH + bh) * D + d] * w;
-    }
-    out[(int64_t)bh * D + d] = (uint16_t)f2bf(acc);
-  }
 }
 
 template <int D, int HT>
@@ -268,6 +341,9 @@ void launch_split(const DecodeParams& p, bool aligned, hipStream_t st) {
 }
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+
+
 
 }  // namespace
 
@@ -299,8 +375,8 @@ int loom_hip_flash_decode(const void* k, const void* v, const void* q, void* out
   if (H > 32)
     return loom_fail(err, errlen, LOOM_EUNSUP, "flash_decode: at most 32 query heads (got %lld)",
                      (long long)H);
-  if (S > (1ll << 30) || B > 65535)
-    return loom_fail(err, errlen, LOOM_EINVAL, "flash_decode: S or B too large");
+  if (S * D * 2 > 0x7fffffffll || B > 65535)
+    return loom_fail(err, errlen, LOOM_EINVAL, "flash_decode: S*D or B too large");
   if (!aligned16(k) || !aligned16(v) || !aligned16(q))
     return loom_fail(err, errlen, LOOM_EINVAL, "flash_decode: tensors must be 16-byte aligned");
   const int64_t ns = cdiv64(S, tile_s);
@@ -314,15 +390,16 @@ int loom_hip_flash_decode(const void* k, const void* v, const void* q, void* out
   p.v = static_cast<const uint16_t*>(v);
   p.q = static_cast<const uint16_t*>(q);
   p.lse = static_cast<float*>(workspace);
-  p.o = reinterpret_cast<float*>(static_cast<char*>(workspace) +
-                                 align256((size_t)ns * B * H * sizeof(float)));
+  const size_t lse_bytes = align256((size_t)ns * B * H * sizeof(float));
+  p.o = reinterpret_cast<float*>(static_cast<char*>(workspace) + lse_bytes);
+  p.out = static_cast<uint16_t*>(out);
   p.B = (int)B;
   p.H = (int)H;
   p.S = (int)S;
   p.tile_s = (int)tile_s;
   p.ns = (int)ns;
   p.c2 = scale * 1.4426950408889634f;
-  const bool al = S % 8 == 0 && tile_s % 8 == 0;
+  const bool al = S % 4 == 0;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (D == 128) {
     if (H > 16) launch_split<128, 2>(p, al, st); else launch_split<128, 1>(p, al, st);
@@ -331,8 +408,11 @@ int loom_hip_flash_decode(const void* k, const void* v, const void* q, void* out
   }
   int rc = loom_check_launch(err, errlen, "flash_decode (split)");
   if (rc) return rc;
-  hipLaunchKernelGGL(decode_combine_kernel, dim3((unsigned)(B * H)), dim3(128), 0, st, p.lse, p.o,
-                     static_cast<uint16_t*>(out), (int)(B * H), (int)D, (int)ns);
+  const dim3 cgrid((unsigned)cdiv64(B * H, 4)), cblock(256);
+  if (D == 128)
+    hipLaunchKernelGGL(decode_combine_kernel<128>, cgrid, cblock, 0, st, p);
+  else
+    hipLaunchKernelGGL(decode_combine_kernel<64>, cgrid, cblock, 0, st, p);
   return loom_check_launch(err, errlen, "flash_decode (combine)");
 }
 

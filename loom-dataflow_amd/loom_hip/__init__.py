@@ -181,7 +181,13 @@ def flash_decode_workspace_bytes(B, H, D, S, tile_s) -> int:
     return int(_lib.loom_hip_flash_decode_workspace_bytes(B, H, D, S, tile_s))
 
 
-def flash_decode(k, v, q, out=None, workspace=None, *, scale=None, tile_b=1, tile_s=512,
+def flash_decode_workspace(B, H, D, S, tile_s, device):
+    """A flash_decode workspace (uint8 tensor) for these extents and tile_s."""
+    return torch.empty(max(flash_decode_workspace_bytes(B, H, D, S, tile_s), 4),
+                       dtype=torch.uint8, device=device)
+
+
+def flash_decode(k, v, q, out=None, workspace=None, *, scale=None, tile_b=1, tile_s=1024,
                  tile_n=128, return_partials=False):
     """@flash_decode (examples/mqa_decode/IR/00_from_helion_frontend.mlir:6).
 
@@ -195,9 +201,8 @@ def flash_decode(k, v, q, out=None, workspace=None, *, scale=None, tile_b=1, til
         scale = 1.0 / math.sqrt(D)
     if out is None:
         out = torch.empty((B, H, D), dtype=_bf16, device=q.device)
-    nbytes = flash_decode_workspace_bytes(B, H, D, S, tile_s)
     if workspace is None:
-        workspace = torch.empty(max(nbytes, 4), dtype=torch.uint8, device=q.device)
+        workspace = flash_decode_workspace(B, H, D, S, tile_s, q.device)
     if workspace.device != q.device or workspace.dtype != torch.uint8 or \
             not workspace.is_contiguous():
         raise ValueError("flash_decode: workspace must be a contiguous uint8 tensor")
