@@ -127,8 +127,16 @@ static inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t
 // ---------------------------------------------------------------------------
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
 
+// The descriptor must be wave-uniform; readfirstlane states that to the
+// compiler, which otherwise may keep it in VGPRs and wrap every buffer
+// instruction in a waterfall loop.
 LOOM_DEV rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+  const uint64_t v = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  void* ub = reinterpret_cast<void*>(((uint64_t)hi << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(ub, 0, (int)__builtin_amdgcn_readfirstlane(bytes),
+                                           0x00020000);
 }
 LOOM_DEV u32x4_t buf_load16(rsrc_t r, uint32_t off) {
   return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
@@ -149,4 +157,53 @@ LOOM_DEV float wave_sum(float v) {
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
   return v;
+}
+
+// ---------------------------------------------------------------------------
+// gfx950 LDS DMA and transpose reads
+// ---------------------------------------------------------------------------
+typedef __attribute__((address_space(3))) char lds_char_t;
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+
+// 16 bytes per lane from global memory straight into LDS
+// (global_load_lds_dwordx4): lane l's data lands at lds + 16 l, where lds
+// must be the same for the whole wave.  No range check: callers clamp.
+// Issued from inline assembly so the compiler does not track it: its LDS-DMA
+// tracking holds only a few loads in flight and beyond that waits for all of
+// them before any LDS read.  Callers therefore order it themselves with
+// LOOM_WAIT_VMCNT + barrier_nofence before reading the destination.  M0 holds
+// the LDS address; one wait state separates the M0 write from its use.
+LOOM_DEV uint32_t lds_addr(const lds_char_t* p) {
+  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)p);
+}
+LOOM_DEV void dma_load16(const void* g, uint32_t lds) {
+  asm volatile(
+      "s_mov_b32 m0, %1\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %0, off"
+      :
+      : "v"(g), "s"(lds)
+      : "memory", "m0");
+}
+
+// ds_read_b64_tr_b16: in each 16-lane group, lanes 4a..4a+3 address the four
+// 8-byte pieces of row a of a 4x16 matrix of 16-bit values; lane j receives
+// column j, (row0[j], row1[j], row2[j], row3[j]).
+LOOM_DEV u32x2_t lds_read_tr16(const lds_char_t* p) {
+  return __builtin_bit_cast(
+      u32x2_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                   (__attribute__((address_space(3))) s16x4_t*)(p)));
+}
+
+// s_waitcnt vmcnt(n), leaving LDS and export counters alone
+#define LOOM_WAIT_VMCNT(n) \
+  __builtin_amdgcn_s_waitcnt(((n) & 15) | ((((n) >> 4) & 3) << 14) | 0x0F70)
+
+// Workgroup barrier without the memory fence __syncthreads() adds (the fence
+// would force every outstanding load, LDS DMA included, to complete).  The
+// empty asm keeps the compiler from moving memory accesses across it.
+LOOM_DEV void barrier_nofence() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
 }

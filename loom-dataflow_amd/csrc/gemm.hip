@@ -222,6 +222,208 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_bf16_kernel(GemmParams p) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// 256x256 tile, LDS-DMA pipeline.  Four waves, each owning a 128x128 block of
+// C.  Per stage, A [256][BK] and B [BK][256] are copied global -> LDS by
+// buffer_load ... lds (no staging registers, range-checked against each
+// operand's extent), NS stages deep.  B stays in its [k][n] layout: the MFMA
+// operand with eight consecutive k per lane comes from two ds_read_b64_tr_b16.
+// The MFMA computes C^T tiles (B^T as the row operand, A^T as the column
+// operand), so each lane ends with four consecutive columns of one row of C:
+// 8-byte (bf16) or 16-byte (fp32) stores straight from registers.
+// Swizzles (16-byte chunk index XOR a function of the row, a_swz / b_swz)
+// keep the operand reads free of bank conflicts; the DMA writes are linear
+// 1 KB blocks per instruction.
+// Each stage buffer is its own __shared__ array and the main loop is unrolled
+// by NS, so the compiler can tell a stage being read from the stages whose DMA
+// is still in flight and only waits for the one it needs.
+// ---------------------------------------------------------------------------
+// A rows hold BK/8 16-byte chunks.  BK 32: the 16 lanes that read one chunk
+// column from 16 consecutive rows must land in distinct 16-byte bank slots
+// whether the LDS serves 8 lanes over 128 bytes or 16 lanes over 256 bytes
+// per cycle: with m = row bits (m3 m2 m1 m0) the XOR term
+// (m2^m1, m3^m1) is a bijection of (m3, m2) for fixed (m1, m0) and of
+// (m2, m1) for fixed (m3, m0).
+template <int BK>
+LOOM_DEV int a_swz(int row) {
+  if constexpr (BK == 64) {
+    return row & 7;
+  } else {
+    const int m1 = (row >> 1) & 1, m2 = (row >> 2) & 1, m3 = (row >> 3) & 1;
+    return ((m2 ^ m1) << 1) | (m3 ^ m1);
+  }
+}
+// B rows hold 32 chunks; a transposed read covers 4 consecutive k rows x 32
+// bytes per 16 lanes: 2 (k & 3) separates those rows, and 8 ((k >> 3) & 1)
+// separates the next 16 lanes' rows (k + 8) within a 256-byte window.
+LOOM_DEV int b_swz(int k) { return (2 * (k & 3)) ^ (8 * ((k >> 3) & 1)); }
+
+template <int BK, int NS, bool OUT_F32>
+__global__ void __launch_bounds__(256) gemm_dma_kernel(GemmParams p) {
+  constexpr int BM = 256, BN = 256;
+  constexpr int A_BYTES = BM * BK * 2, B_BYTES = BK * BN * 2;
+  constexpr int A_ROWS_PER_I = 1024 / (BK * 2);   // A rows per DMA instruction
+  constexpr int A_CPR = BK / 8;                   // 16-byte chunks per A row
+  constexpr int A_INSTR = A_BYTES / 1024 / 4;     // per wave per stage
+  constexpr int B_INSTR = B_BYTES / 1024 / 4;
+  constexpr int LPW = A_INSTR + B_INSTR;          // DMA instructions per wave per stage
+  static_assert(NS >= 2 && NS <= 4, "2..4 stages");
+  static_assert(LPW * (NS - 2) <= 63, "vmcnt range");
+  __shared__ __attribute__((aligned(1024))) char sA0[A_BYTES], sB0[B_BYTES];
+  __shared__ __attribute__((aligned(1024))) char sA1[A_BYTES], sB1[B_BYTES];
+  __shared__ __attribute__((aligned(1024))) char sA2[NS > 2 ? A_BYTES : 16], sB2[NS > 2 ? B_BYTES : 16];
+  __shared__ __attribute__((aligned(1024))) char sA3[NS > 3 ? A_BYTES : 16], sB3[NS > 3 ? B_BYTES : 16];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  // wave-uniform by construction; readfirstlane lets the compiler know (the
+  // LDS destination of a DMA load lives in M0)
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+  // ---- which tile, which z (XCD-contiguous, grouped by 8 tile rows)
+  const int nblocks = p.tiles_m * p.tiles_n * p.nz;
+  const int bid = xcd_remap(blockIdx.x, nblocks);
+  const int per_z = p.tiles_m * p.tiles_n;
+  const int z = bid / per_z;
+  const int t = bid - z * per_z;
+  constexpr int GM = 8;
+  const int group = t / (GM * p.tiles_n);
+  const int first_m = group * GM;
+  const int gsz = min(p.tiles_m - first_m, GM);
+  const int tin = t - group * GM * p.tiles_n;
+  const int64_t m0 = (int64_t)(first_m + tin % gsz) * BM;
+  const int64_t n0 = (int64_t)(tin / gsz) * BN;
+
+  const uint16_t* A = p.A;
+  const uint16_t* B = p.B;
+  int64_t kb = 0, ke = p.k_total;
+  if (p.split) {
+    kb = (int64_t)z * p.k_slab;
+    ke = min(p.k_total, kb + p.k_slab);
+  } else {
+    A += (int64_t)z * p.za;
+    B += (int64_t)z * p.zb;
+  }
+
+  auto stageA = [&](int s) -> lds_char_t* {
+    if (s == 0) return (lds_char_t*)sA0;
+    if (s == 1) return (lds_char_t*)sA1;
+    if (s == 2) return (lds_char_t*)sA2;
+    return (lds_char_t*)sA3;
+  };
+  auto stageB = [&](int s) -> lds_char_t* {
+    if (s == 0) return (lds_char_t*)sB0;
+    if (s == 1) return (lds_char_t*)sB1;
+    if (s == 2) return (lds_char_t*)sB2;
+    return (lds_char_t*)sB3;
+  };
+
+  // ---- DMA one stage: this wave's A_INSTR + B_INSTR 1 KB blocks
+  auto issue = [&](int s, int64_t k0) {
+    const uint32_t la = lds_addr(stageA(s));
+    const uint32_t lb = lds_addr(stageB(s));
+#pragma unroll
+    for (int i = 0; i < A_INSTR; ++i) {
+      const int j = wave * A_INSTR + i;
+      const int row = j * A_ROWS_PER_I + lane / A_CPR;
+      const int c = (lane % A_CPR) ^ a_swz<BK>(row);
+      const int64_t gm = min<int64_t>(m0 + row, p.M - 1);
+      dma_load16(A + gm * p.lda + k0 + c * 8, la + j * 1024);
+    }
+#pragma unroll
+    for (int i = 0; i < B_INSTR; ++i) {
+      const int j = wave * B_INSTR + i;
+      const int row = j * 2 + lane / 32;
+      const int c = (lane % 32) ^ b_swz(row);
+      const int64_t gn = min<int64_t>(n0 + c * 8, p.N - 8);
+      dma_load16(B + (k0 + row) * p.ldb + gn, lb + j * 1024);
+    }
+  };
+
+  const int wm = wave & 1, wn = wave >> 1;
+  const int lr = lane & 15, lg = lane >> 4;
+  f32x4_t acc[8][8];  // [n tile][m tile]
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  auto compute = [&](int s) {
+    const lds_char_t* la = stageA(s);
+    const lds_char_t* lb = stageB(s);
+#pragma unroll
+    for (int ks = 0; ks < BK / 32; ++ks) {
+      u32x4_t af[8];
+#pragma unroll
+      for (int tm = 0; tm < 8; ++tm) {
+        // column operand A^T: lane holds A[m][32 ks + 8 lg .. +7], m = tile row lr
+        const int m = wm * 128 + tm * 16 + lr;
+        const int ch = (ks * 4 + lg) ^ a_swz<BK>(m);
+        af[tm] = *(const __attribute__((address_space(3))) u32x4_t*)(la + m * (BK * 2) + ch * 16);
+      }
+#pragma unroll
+      for (int tn = 0; tn < 8; ++tn) {
+        // row operand B^T: lane holds B[32 ks + 8 lg .. +7][n], n = tile col lr
+        const int nb = wn * 128 + tn * 16;
+        const int a = lr >> 2, c4 = lr & 3;
+        const int k0r = ks * 32 + lg * 8 + a;          // & 3 == a
+        const int ch = ((nb >> 3) + (c4 >> 1)) ^ b_swz(k0r);
+        const lds_char_t* q = lb + k0r * 512 + ch * 16 + (c4 & 1) * 8;
+        const u32x2_t lo = lds_read_tr16(q);
+        const u32x2_t hi = lds_read_tr16(q + 4 * 512);
+        const u32x4_t bf = u32x4_t{lo[0], lo[1], hi[0], hi[1]};
+#pragma unroll
+        for (int tm = 0; tm < 8; ++tm) acc[tn][tm] = mfma16(bf, af[tm], acc[tn][tm]);
+      }
+    }
+  };
+
+  const int nk = ke > kb ? (int)((ke - kb) / BK) : 0;  // K range is a multiple of BK
+#pragma unroll
+  for (int s = 0; s < NS - 1; ++s)
+    if (s < nk) issue(s, kb + (int64_t)s * BK);
+
+  for (int it0 = 0; it0 < nk; it0 += NS) {
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const int it = it0 + s;
+      if (it < nk) {
+        // my DMA for stage `it` is done once at most the younger stages'
+        // loads are outstanding; the barrier makes everyone's visible and
+        // frees the buffer read in the previous iteration
+        const int younger = min(NS - 2, nk - 1 - it);
+        if (younger >= 2) LOOM_WAIT_VMCNT(2 * LPW);
+        else if (younger == 1) LOOM_WAIT_VMCNT(LPW);
+        else LOOM_WAIT_VMCNT(0);
+        barrier_nofence();
+        if (it + NS - 1 < nk) issue((s + NS - 1) % NS, kb + (int64_t)(it + NS - 1) * BK);
+        compute(s);
+      }
+    }
+  }
+
+  // ---- epilogue: acc[tn][tm][i] = C[m][n + i], m = tile row, n = 4 lg.
+  // The scheduling fences keep the compiler from pulling all 256 accumulators
+  // into VGPRs at once (which would set the kernel's VGPR budget).
+#pragma unroll
+  for (int tm = 0; tm < 8; ++tm) {
+    __builtin_amdgcn_sched_barrier(0);
+    const int64_t row = m0 + wm * 128 + tm * 16 + lr;
+    if (row >= p.M) continue;
+#pragma unroll
+    for (int tn = 0; tn < 8; ++tn) {
+      const int64_t col = n0 + wn * 128 + tn * 16 + lg * 4;
+      if (col >= p.N) continue;
+      const f32x4_t v = acc[tn][tm];
+      if constexpr (OUT_F32)
+        *reinterpret_cast<f32x4_t*>(static_cast<float*>(p.C) + (int64_t)z * p.zc + row * p.ldc + col) = v;
+      else
+        *reinterpret_cast<u32x2_t*>(static_cast<uint16_t*>(p.C) + (int64_t)z * p.zc + row * p.ldc + col) =
+            u32x2_t{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+    }
+  }
+}
+
 // out[e] = bf16( sum_{s ascending} G[s][e] ) -- the split-0 reduction of
 // examples/split_k_mm_gather/IR/00_from_helion_frontend.mlir:34-51.
 __global__ void __launch_bounds__(256) splitk_reduce_vec4(const float* __restrict__ G,
@@ -276,12 +478,31 @@ bool tile_supported(int64_t tm, int64_t tn) {
   return (tm == 64 && tn == 64) || (tm == 128 && tn == 128) || (tm == 256 && tn == 256);
 }
 
+// Depth of the DMA pipeline of the 256x256 kernel: BK-deep stages, NS of them.
+#ifndef LOOM_GEMM_DMA_BK
+#define LOOM_GEMM_DMA_BK 32
+#endif
+#ifndef LOOM_GEMM_DMA_NS
+#define LOOM_GEMM_DMA_NS 4
+#endif
+
 hipError_t launch_gemm(GemmParams p, int64_t tile_m, int64_t tile_n, bool aligned, bool out_f32,
                        hipStream_t st) {
   p.tiles_m = (int)cdiv64(p.M, tile_m);
   p.tiles_n = (int)cdiv64(p.N, tile_n);
   if (tile_m == 64) return launch_tile<64, 64, 1, 2>(p, aligned, out_f32, st);
   if (tile_m == 128) return launch_tile<128, 128, 2, 2>(p, aligned, out_f32, st);
+  // 256x256: the LDS-DMA kernel needs whole BK steps in every K range
+  constexpr int BK = LOOM_GEMM_DMA_BK, NS = LOOM_GEMM_DMA_NS;
+  const bool dma = aligned && p.k_total % BK == 0 && (!p.split || p.k_slab % BK == 0);
+  if (dma) {
+    const dim3 grid((unsigned)((int64_t)p.tiles_m * p.tiles_n * p.nz)), block(256);
+    if (out_f32)
+      hipLaunchKernelGGL((gemm_dma_kernel<BK, NS, true>), grid, block, 0, st, p);
+    else
+      hipLaunchKernelGGL((gemm_dma_kernel<BK, NS, false>), grid, block, 0, st, p);
+    return hipGetLastError();
+  }
   return launch_tile<256, 256, 2, 4>(p, aligned, out_f32, st);
 }
 
