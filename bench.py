@@ -141,9 +141,9 @@ def make_cases(torch, lh):
         n = min(2, copies(nb))
         sets = [(randn(BH, D, S), randn(BH, S, D), randn(BH, S, D),
                  torch.empty(BH, S, D, dtype=bf, device=cuda)) for _ in range(n)]
-        return dict(fn=lambda i: lh.attention(*sets[i % n], causal=True, tile_m=128, tile_n=64),
+        return dict(fn=lambda i: lh.attention(*sets[i % n], causal=True, tile_m=192, tile_n=64),
                     flop=4 * BH * S * S * D // 2, bytes=nb, bound="mfma", sets=n,
-                    desc="flashattn fwd B4 H32 S4096 D128 causal")
+                    desc="flashattn fwd B4 H32 S4096 D128 causal, tile_m 192")
     cases["flashattn"] = flashattn
 
     def decode():

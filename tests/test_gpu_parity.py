@@ -164,7 +164,7 @@ def test_split_k_baseline_float(lh):
 
 # ---------------------------------------------------------------- attention
 
-@pytest.mark.parametrize("tile_m", [64, 128])
+@pytest.mark.parametrize("tile_m", [64, 128, 192, 256])
 @pytest.mark.parametrize("name", ["attention_noncausal", "attention_causal"])
 def test_attention_golden(lh, golden, name, tile_m):
     g = golden(name)
@@ -199,8 +199,9 @@ def test_attention_vs_oracle_mid(lh):
     k, v, q = rng_bf16(rng, (BH, D, S)), rng_bf16(rng, (BH, S, D)), rng_bf16(rng, (BH, S, D))
     for causal in (False, True):
         ref = from_bf16(oracle.attention(k, v, q, 1 / math.sqrt(D), causal, 1, 64, 64))
-        got = from_bf16(host(lh.attention(dev(k), dev(v), dev(q), causal=causal)))
-        assert_close(got, ref, **ATTN_TOL, what=f"attention S=1000 causal={causal}")
+        for tm in (64, 192, 256):
+            got = from_bf16(host(lh.attention(dev(k), dev(v), dev(q), causal=causal, tile_m=tm)))
+            assert_close(got, ref, **ATTN_TOL, what=f"attention S=1000 causal={causal} tile_m={tm}")
 
 
 def test_attention_baseline_heads(lh):
@@ -210,7 +211,7 @@ def test_attention_baseline_heads(lh):
     k = torch.randn(BH, D, S, device="cuda").to(torch.bfloat16)
     v = torch.randn(BH, S, D, device="cuda").to(torch.bfloat16)
     q = torch.randn(BH, S, D, device="cuda").to(torch.bfloat16)
-    out = host(lh.attention(k, v, q, causal=True, tile_m=128, tile_n=64))
+    out = host(lh.attention(k, v, q, causal=True, tile_m=192, tile_n=64))
     assert np.isfinite(from_bf16(out)).all()
     for h in (0, 77, 127):
         ref = oracle.attention(host(k[h:h + 1]), host(v[h:h + 1]), host(q[h:h + 1]),
