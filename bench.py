@@ -277,7 +277,7 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                     "traffic": traffic_for("gemm_bf16_kernel_256x256")},
+                     "traffic": traffic_for("gemm_dma_kernel<32,4,false>")},
     }
     a0_a1 = None
     if not args.no_cpu:

@@ -27,8 +27,10 @@
 //     summed over a 256-long chunk exceeds the 2e-2 output tolerance);
 //   - 16-row m tiles are dealt to the waves in a snake order so the causal
 //     triangle costs every wave the same;
-//   - the bf16 output tile is staged in LDS (over pT) and written with
-//     16-byte stores.
+//   - the MFMAs compute out^T tiles, so each lane holds four consecutive
+//     columns of one output row: the exp(dA[m]) scale is one factor per lane
+//     and results are stored as 8-byte writes straight from registers;
+//   - D x is folded into the diagonal of W (W[m, m] += D[h]).
 #include "common.h"
 
 namespace {
@@ -57,8 +59,8 @@ __global__ void __launch_bounds__(64 * kWaves) mamba_chunk_scan_kernel(MambaPara
   constexpr int XROW = kQmax / 8;   // 16-byte chunks per xT row
   constexpr int PROW = kNmax / 8;   // 16-byte chunks per pT row
   __shared__ u32x4_t xT[kPT * XROW];          // [p][k]
-  __shared__ u32x4_t pT[2][kPT * PROW];       // hi, lo: [p][n]; reused for the output tile
-  __shared__ float s_dA[kQmax], s_dt[kQmax];
+  __shared__ u32x4_t pT[2][kPT * PROW];       // hi, lo: [p][n]
+  __shared__ __attribute__((aligned(16))) float s_dA[kQmax], s_dt[kQmax], s_U[kQmax];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -88,182 +90,213 @@ __global__ void __launch_bounds__(64 * kWaves) mamba_chunk_scan_kernel(MambaPara
   const float* __restrict__ pvg = p.prevT + ((int64_t)(b * p.nc + c) * H + h) * N * P;
   const int64_t sidx = ((int64_t)(b * H + h) * p.nc + c) * Q;
 
-  // ---- stage dA, dt
-  for (int i = tid; i < Q; i += 64 * kWaves) {
-    s_dA[i] = p.dA[sidx + i] * 1.4426950408889634f;  // log2 domain
-    s_dt[i] = p.dt[sidx + i];
+  // ---- staging: every global load first, then conversions and LDS stores.
+  // One 8x8 block of x per thread (k-chunk fastest; k rounded up to the
+  // 32-deep MFMA step, rows past the chunk zero-filled), one 8x8 block of
+  // prevT for the first nch*pch threads, one dA and dt value per thread.
+  const int kch = ((mend + 31) / 32) * 4, pch = TN / 8;
+  const int nch = ((N + 31) / 32) * 4;
+  const bool do_x = tid < kch * pch, do_p = tid < nch * pch;
+  const int x_kc = tid % kch, x_pc = tid / kch;
+  const int p_nc = tid % nch, p_pc = tid / nch;
+  u32x4_t xr[8];
+  f32x4_t pr[8][2];
+  float dA_v = 0.f, dt_v = 0.f, dA_e = 0.f;
+  if (tid < Q) {
+    dA_v = p.dA[sidx + tid];
+    dt_v = p.dt[sidx + tid];
+    dA_e = p.dA[sidx + min(tid | 31, Q - 1)];  // last key of tid's 32-key block
   }
-  // ---- stage xT[p][k] for k < mend (8x8 blocks, k-chunk fastest)
-  {
-    // rounded up to the 32-deep MFMA step: chunks past mend are zero-filled
-    const int kch = ((mend + 31) / 32) * 4, pch = TN / 8;
-    for (int blk = tid; blk < kch * pch; blk += 64 * kWaves) {
-      const int kc = blk % kch, pc = blk / kch;
-      const int pg = p0 + pc * 8;
-      u32x4_t rows[8], tr[8];
+  if (do_x) {
+    const int pg = p0 + x_pc * 8;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int k = kc * 8 + e;
-        rows[e] = (k < Q && pg < P) ? *reinterpret_cast<const u32x4_t*>(xg + (int64_t)k * P + pg)
-                                    : u32x4_t{0u, 0u, 0u, 0u};
-      }
-      transpose8x8(rows, tr);
+    for (int e = 0; e < 8; ++e) {
+      const int k = x_kc * 8 + e;
+      xr[e] = (k < Q && pg < P) ? *reinterpret_cast<const u32x4_t*>(xg + (int64_t)k * P + pg)
+                                : u32x4_t{0u, 0u, 0u, 0u};
+    }
+  }
+  if (do_p) {
+    const int pg = p0 + p_pc * 8;
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int pp = pc * 8 + u;  // pp & 7 == u
-        xT[pp * XROW + (kc ^ u)] = tr[u];
+    for (int e = 0; e < 8; ++e) {
+      const int n = p_nc * 8 + e;
+      if (n < N && pg < P) {
+        pr[e][0] = *reinterpret_cast<const f32x4_t*>(pvg + (int64_t)n * P + pg);
+        pr[e][1] = *reinterpret_cast<const f32x4_t*>(pvg + (int64_t)n * P + pg + 4);
+      } else {
+        pr[e][0] = pr[e][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
       }
     }
   }
-  // ---- stage pT[p][n] = prevT[n][p] split into bf16 hi + lo
-  {
-    const int nch = ((N + 31) / 32) * 4, pch = TN / 8;
-    for (int blk = tid; blk < nch * pch; blk += 64 * kWaves) {
-      const int nc8 = blk % nch, pc = blk / nch;
-      const int pg = p0 + pc * 8;
-      u32x4_t hi[8], lo[8], thi[8], tlo[8];
+  if (tid < Q) {
+    constexpr float kLog2e = 1.4426950408889634f;
+    s_dA[tid] = dA_v * kLog2e;  // log2 domain
+    s_dt[tid] = dt_v;
+    // U[k] = exp2(dA[k_e] - dA[k]) dt[k], k_e = last key of k's 32-key block:
+    // the k-dependent factor of W on blocks that lie wholly below a row
+    s_U[tid] = fast_exp2((dA_e - dA_v) * kLog2e) * dt_v;
+  }
+  if (do_x) {
+    u32x4_t tr[8];
+    transpose8x8(xr, tr);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int n = nc8 * 8 + e;
-        f32x4_t a{0.f, 0.f, 0.f, 0.f}, bq{0.f, 0.f, 0.f, 0.f};
-        if (n < N && pg < P) {
-          a = *reinterpret_cast<const f32x4_t*>(pvg + (int64_t)n * P + pg);
-          bq = *reinterpret_cast<const f32x4_t*>(pvg + (int64_t)n * P + pg + 4);
-        }
-        float v[8] = {a[0], a[1], a[2], a[3], bq[0], bq[1], bq[2], bq[3]};
-        uint32_t hb[8], lb[8];
+    for (int u = 0; u < 8; ++u) xT[(x_pc * 8 + u) * XROW + (x_kc ^ u)] = tr[u];  // row & 7 == u
+  }
+  if (do_p) {
+    // prevT split into bf16 hi + lo (the state term keeps ~16 mantissa bits)
+    u32x4_t hi[8], lo[8], thi[8], tlo[8];
 #pragma unroll
-        for (int z = 0; z < 8; ++z) {
-          hb[z] = f2bf(v[z]);
-          lb[z] = f2bf(v[z] - bf2f(hb[z]));
-        }
-        hi[e] = u32x4_t{hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16), hb[4] | (hb[5] << 16),
-                        hb[6] | (hb[7] << 16)};
-        lo[e] = u32x4_t{lb[0] | (lb[1] << 16), lb[2] | (lb[3] << 16), lb[4] | (lb[5] << 16),
-                        lb[6] | (lb[7] << 16)};
+    for (int e = 0; e < 8; ++e) {
+      const float v[8] = {pr[e][0][0], pr[e][0][1], pr[e][0][2], pr[e][0][3],
+                          pr[e][1][0], pr[e][1][1], pr[e][1][2], pr[e][1][3]};
+#pragma unroll
+      for (int z = 0; z < 4; ++z) {
+        const uint32_t hw = pack_bf16x2(v[2 * z], v[2 * z + 1]);
+        hi[e][z] = hw;
+        lo[e][z] = pack_bf16x2(v[2 * z] - bf2f_lo(hw), v[2 * z + 1] - bf2f_hi(hw));
       }
-      transpose8x8(hi, thi);
-      transpose8x8(lo, tlo);
+    }
+    transpose8x8(hi, thi);
+    transpose8x8(lo, tlo);
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int pp = pc * 8 + u;
-        pT[0][pp * PROW + (nc8 ^ u)] = thi[u];
-        pT[1][pp * PROW + (nc8 ^ u)] = tlo[u];
-      }
+    for (int u = 0; u < 8; ++u) {
+      const int pp = p_pc * 8 + u;
+      pT[0][pp * PROW + (p_nc ^ u)] = thi[u];
+      pT[1][pp * PROW + (p_nc ^ u)] = tlo[u];
     }
   }
   __syncthreads();
 
   const float Dh = p.Dh[h];
   const int nmt16 = (mend - m0 + 15) / 16;  // 16-row tiles of this workgroup
-  const int nsteps_n = (N + 31) / 32;
   constexpr int MAXT = kQmax / 16 / kWaves;  // tiles per wave at most
+  constexpr int NSN = kNmax / 32;            // state-term steps at most
+  constexpr int NKS = kQmax / 32;            // intra-chunk steps at most
   // snake deal of 16-row tiles: slot ti of wave w is tile 4 ti + (w or 3 - w)
   auto tile_of = [&](int ti) {
     return kWaves * ti + ((ti & 1) ? (kWaves - 1 - wave) : wave);
   };
-  f32x4_t acc[MAXT][PT];
+  // C and cb rows come straight from global memory as MFMA operands.  A
+  // tile's loads are issued while the previous tile computes (two register
+  // sets); buffer loads read rows past the chunk as zeros.
+  const rsrc_t rC = make_rsrc(Cg, (uint32_t)(Q * N * 2));
+  const rsrc_t rCB = make_rsrc(cbg, (uint32_t)(Q * Q * 2));
+  struct Rows {
+    u32x4_t c[NSN];
+    u32x4_t cb[NKS];
+  };
+  auto fetch = [&](int ti, Rows& rw) {
+    const int mrow0 = m0 + 16 * tile_of(ti);
+    const int am = mrow0 + rr;
+    const int kend = min(mrow0 + 16, Q);
+#pragma unroll
+    for (int ns = 0; ns < NSN; ++ns)
+      if (ns * 32 < N) rw.c[ns] = buf_load16(rC, (uint32_t)(am * N + ns * 32 + g4 * 8) * 2);
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks)
+      if (ks * 32 < kend) rw.cb[ks] = buf_load16(rCB, (uint32_t)(am * Q + ks * 32 + g4 * 8) * 2);
+  };
+
+  // The MFMAs compute out^T tiles (x^T / prevT^T as the row operand, W / C
+  // as the column operand): lane (rr, g4) of tile (ti, pt) accumulates
+  // out[m = mrow0 + rr][p = 16 pt + 4 g4 + i], four consecutive columns.
+  uint16_t* og = p.out + ((int64_t)(b * H + h) * L + (int64_t)c * Q) * P;
+  Rows rowbuf[2];
+  if (tile_of(0) < nmt16) fetch(0, rowbuf[0]);
 #pragma unroll
   for (int ti = 0; ti < MAXT; ++ti) {
     if (tile_of(ti) >= nmt16) continue;
+    if (ti + 1 < MAXT && tile_of(ti + 1) < nmt16) fetch(ti + 1, rowbuf[(ti + 1) & 1]);
+    const Rows& rw = rowbuf[ti & 1];
     const int mrow0 = m0 + 16 * tile_of(ti);
-    const int am = mrow0 + rr;  // this lane's A-operand row
+    const int am = mrow0 + rr;  // this lane's output row
+    f32x4_t acc[PT];
 #pragma unroll
-    for (int pt = 0; pt < PT; ++pt) acc[ti][pt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int pt = 0; pt < PT; ++pt) acc[pt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
     // ---- state term: C[m, :] . prevT[:, p] (hi + lo), then * exp(dA[m])
-    for (int ns = 0; ns < nsteps_n; ++ns) {
-      const int n = ns * 32 + g4 * 8;
-      const u32x4_t a = (am < Q && n < N)
-                            ? *reinterpret_cast<const u32x4_t*>(Cg + (int64_t)am * N + n)
-                            : u32x4_t{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int ns = 0; ns < NSN; ++ns) {
+      if (ns * 32 >= N) continue;  // pT is staged (zero-padded) only up to N rounded to 32
 #pragma unroll
       for (int pt = 0; pt < PT; ++pt) {
         const int pp = pt * 16 + rr;
         const int ch = (ns * 4 + g4) ^ (pp & 7);
-        acc[ti][pt] = mfma16(a, pT[0][pp * PROW + ch], acc[ti][pt]);
-        acc[ti][pt] = mfma16(a, pT[1][pp * PROW + ch], acc[ti][pt]);
+        acc[pt] = mfma16(pT[0][pp * PROW + ch], rw.c[ns], acc[pt]);
+        acc[pt] = mfma16(pT[1][pp * PROW + ch], rw.c[ns], acc[pt]);
       }
     }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int m = mrow0 + 4 * g4 + i;
-      const float e = m < Q ? fast_exp2(s_dA[m]) : 0.f;
-#pragma unroll
-      for (int pt = 0; pt < PT; ++pt) acc[ti][pt][i] *= e;
-    }
-
-    // ---- intra-chunk term: W[m, k] . x[k, p] for k <= m
     const float dAm = am < Q ? s_dA[am] : 0.f;
-    const int kend = min(mrow0 + 16, Q);
-    for (int k0 = 0; k0 < kend; k0 += 32) {
-      const int kb = k0 + g4 * 8;
-      u32x4_t cbv = (am < Q && kb < Q)
-                        ? *reinterpret_cast<const u32x4_t*>(cbg + (int64_t)am * Q + kb)
-                        : u32x4_t{0u, 0u, 0u, 0u};
-      // W in fp32, split into bf16 hi + lo so the product keeps ~16 bits
-      uint32_t whi[8], wlo[8];
+    const float em = am < Q ? fast_exp2(dAm) : 0.f;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int k = kb + e;
-        const uint32_t word = cbv[e >> 1];
-        const float cbf = (e & 1) ? bf2f_hi(word) : bf2f_lo(word);
-        float wv = 0.f;
-        if (k <= am && k < Q) wv = cbf * fast_exp2(dAm - s_dA[k]) * s_dt[k];
-        whi[e] = f2bf(wv);
-        wlo[e] = f2bf(wv - bf2f(whi[e]));
+    for (int pt = 0; pt < PT; ++pt) acc[pt] *= em;
+
+    // ---- intra-chunk term: W[m, k] . x[k, p] for k <= m, with the skip
+    // connection folded into the diagonal: W[m, m] += D[h].  A 32-key block
+    // that ends below the tile's first row uses the factored form
+    //   W = cb[m, k] * U[k] * exp2(dA[m] - dA[k_e])   (both exponents <= 0);
+    // the block(s) reaching the diagonal use exp2(dA[m] - dA[k]) per element,
+    // masked to k <= m.
+    const int kend = min(mrow0 + 16, Q);
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+      if (ks * 32 >= kend) continue;
+      const int kb = ks * 32 + g4 * 8;
+      float wv[8];
+      if (ks * 32 + 31 < mrow0) {
+        const f32x4_t u0 = *reinterpret_cast<const f32x4_t*>(s_U + kb);
+        const f32x4_t u1 = *reinterpret_cast<const f32x4_t*>(s_U + kb + 4);
+        const float vm = fast_exp2(dAm - s_dA[ks * 32 + 31]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const uint32_t word = rw.cb[ks][e >> 1];
+          const float cbf = (e & 1) ? bf2f_hi(word) : bf2f_lo(word);
+          wv[e] = cbf * (e < 4 ? u0[e] : u1[e - 4]) * vm;
+        }
+      } else {
+        const f32x4_t dA0 = *reinterpret_cast<const f32x4_t*>(s_dA + kb);
+        const f32x4_t dA1 = *reinterpret_cast<const f32x4_t*>(s_dA + kb + 4);
+        const f32x4_t dt0 = *reinterpret_cast<const f32x4_t*>(s_dt + kb);
+        const f32x4_t dt1 = *reinterpret_cast<const f32x4_t*>(s_dt + kb + 4);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int k = kb + e;
+          const uint32_t word = rw.cb[ks][e >> 1];
+          const float cbf = (e & 1) ? bf2f_hi(word) : bf2f_lo(word);
+          const float dAk = e < 4 ? dA0[e] : dA1[e - 4];
+          const float dtk = e < 4 ? dt0[e] : dt1[e - 4];
+          float w = (k <= am && k < Q) ? cbf * fast_exp2(dAm - dAk) * dtk : 0.f;
+          if (k == am) w += Dh;
+          wv[e] = w;
+        }
       }
-      const u32x4_t ahi{whi[0] | (whi[1] << 16), whi[2] | (whi[3] << 16),
-                        whi[4] | (whi[5] << 16), whi[6] | (whi[7] << 16)};
-      const u32x4_t alo{wlo[0] | (wlo[1] << 16), wlo[2] | (wlo[3] << 16),
-                        wlo[4] | (wlo[5] << 16), wlo[6] | (wlo[7] << 16)};
+      u32x4_t ahi, alo;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t hw = pack_bf16x2(wv[2 * i], wv[2 * i + 1]);
+        ahi[i] = hw;
+        alo[i] = pack_bf16x2(wv[2 * i] - bf2f_lo(hw), wv[2 * i + 1] - bf2f_hi(hw));
+      }
 #pragma unroll
       for (int pt = 0; pt < PT; ++pt) {
         const int pp = pt * 16 + rr;
-        const u32x4_t xb = xT[pp * XROW + (((k0 >> 3) + g4) ^ (pp & 7))];
-        acc[ti][pt] = mfma16(ahi, xb, acc[ti][pt]);
-        acc[ti][pt] = mfma16(alo, xb, acc[ti][pt]);
+        const u32x4_t xb = xT[pp * XROW + ((ks * 4 + g4) ^ (pp & 7))];
+        acc[pt] = mfma16(xb, ahi, acc[pt]);
+        acc[pt] = mfma16(xb, alo, acc[pt]);
       }
     }
 
-    // ---- skip connection D * x[m, p]
+    // ---- store: four consecutive columns per lane (8 bytes)
+    if (am < mend) {
 #pragma unroll
-    for (int pt = 0; pt < PT; ++pt) {
-      const int pp = pt * 16 + rr;
-      const uint16_t* xrow = reinterpret_cast<const uint16_t*>(xT + pp * XROW);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int m = mrow0 + 4 * g4 + i;
-        if (m < Q) {
-          const int off = (((m >> 3) ^ (pp & 7)) << 3) + (m & 7);
-          acc[ti][pt][i] += Dh * bf2f(xrow[off]);
-        }
+      for (int pt = 0; pt < PT; ++pt) {
+        const int pg = p0 + pt * 16 + 4 * g4;
+        if (pg < P)
+          *reinterpret_cast<u32x2_t*>(og + (int64_t)am * P + pg) =
+              u32x2_t{pack_bf16x2(acc[pt][0], acc[pt][1]), pack_bf16x2(acc[pt][2], acc[pt][3])};
       }
     }
-  }
-  __syncthreads();  // pT is dead from here: reuse it for the output tile
-
-  // ---- output tile -> LDS [m - m0][p] (row = TN bf16), then 16-byte stores
-  uint16_t* ot = reinterpret_cast<uint16_t*>(&pT[0][0]);
-#pragma unroll
-  for (int ti = 0; ti < MAXT; ++ti) {
-    if (tile_of(ti) >= nmt16) continue;
-    const int lrow0 = 16 * tile_of(ti);
-#pragma unroll
-    for (int pt = 0; pt < PT; ++pt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        ot[(lrow0 + 4 * g4 + i) * TN + pt * 16 + rr] = (uint16_t)f2bf(acc[ti][pt][i]);
-  }
-  __syncthreads();
-  uint16_t* og = p.out + ((int64_t)(b * H + h) * L + (int64_t)c * Q) * P;
-  const int rows = mend - m0, cch = TN / 8;
-  for (int e = tid; e < rows * cch; e += 64 * kWaves) {
-    const int r = e / cch, cc = e % cch;
-    const int pg = p0 + cc * 8;
-    if (pg < P)
-      *reinterpret_cast<u32x4_t*>(og + (int64_t)(m0 + r) * P + pg) =
-          *reinterpret_cast<const u32x4_t*>(ot + r * TN + cc * 8);
   }
 }
 
