@@ -211,9 +211,14 @@ __global__ void __launch_bounds__(64 * kWaves) mamba_chunk_scan_kernel(MambaPara
     const Rows& rw = rowbuf[ti & 1];
     const int mrow0 = m0 + 16 * tile_of(ti);
     const int am = mrow0 + rr;  // this lane's output row
-    f32x4_t acc[PT];
+    // state and intra-chunk terms accumulate separately and meet only at the
+    // store, so no VALU touches an accumulator between MFMAs
+    f32x4_t acc_s[PT], acc[PT];
 #pragma unroll
-    for (int pt = 0; pt < PT; ++pt) acc[pt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int pt = 0; pt < PT; ++pt) {
+      acc_s[pt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      acc[pt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    }
 
     // ---- state term: C[m, :] . prevT[:, p] (hi + lo), then * exp(dA[m])
 #pragma unroll
@@ -223,14 +228,12 @@ __global__ void __launch_bounds__(64 * kWaves) mamba_chunk_scan_kernel(MambaPara
       for (int pt = 0; pt < PT; ++pt) {
         const int pp = pt * 16 + rr;
         const int ch = (ns * 4 + g4) ^ (pp & 7);
-        acc[pt] = mfma16(pT[0][pp * PROW + ch], rw.c[ns], acc[pt]);
-        acc[pt] = mfma16(pT[1][pp * PROW + ch], rw.c[ns], acc[pt]);
+        acc_s[pt] = mfma16(pT[0][pp * PROW + ch], rw.c[ns], acc_s[pt]);
+        acc_s[pt] = mfma16(pT[1][pp * PROW + ch], rw.c[ns], acc_s[pt]);
       }
     }
     const float dAm = am < Q ? s_dA[am] : 0.f;
     const float em = am < Q ? fast_exp2(dAm) : 0.f;
-#pragma unroll
-    for (int pt = 0; pt < PT; ++pt) acc[pt] *= em;
 
     // ---- intra-chunk term: W[m, k] . x[k, p] for k <= m, with the skip
     // connection folded into the diagonal: W[m, m] += D[h].  A 32-key block
@@ -292,9 +295,10 @@ __global__ void __launch_bounds__(64 * kWaves) mamba_chunk_scan_kernel(MambaPara
 #pragma unroll
       for (int pt = 0; pt < PT; ++pt) {
         const int pg = p0 + pt * 16 + 4 * g4;
+        const f32x4_t o = acc_s[pt] * em + acc[pt];
         if (pg < P)
           *reinterpret_cast<u32x2_t*>(og + (int64_t)am * P + pg) =
-              u32x2_t{pack_bf16x2(acc[pt][0], acc[pt][1]), pack_bf16x2(acc[pt][2], acc[pt][3])};
+              u32x2_t{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
       }
     }
   }
