@@ -37,6 +37,22 @@
 extern "C" {
 #endif
 
+/* Return codes of every entry point. */
+#define LOOM_HIP_OK 0
+#define LOOM_HIP_EINVAL 1 /* shapes, tiles, pointers, JSON or workspace rejected */
+#define LOOM_HIP_EUNSUP 2 /* legal in the reference, not built for gfx950 */
+#define LOOM_HIP_EHIP 3   /* HIP runtime error */
+
+/* Slots of the tiles[] array loom_hip_parse_variant fills (-1 = unbound). */
+#define LOOM_HIP_TILE_B 0
+#define LOOM_HIP_TILE_M 1
+#define LOOM_HIP_TILE_N 2
+#define LOOM_HIP_TILE_K 3
+#define LOOM_HIP_TILE_S 4
+#define LOOM_HIP_TILE_H 5
+#define LOOM_HIP_TILE_C 6
+#define LOOM_HIP_NTILES 7
+
 /* Library version string ("loom_hip <major>.<minor>.<patch> gfx950").
  * Counterpart of the pybind module's __version__
  * (lib/pipeline/src/loom_pybind.cpp:17-20). */
@@ -82,9 +98,9 @@ int loom_hip_split_k_matmul_gather(const void* a, const void* b, void* out, void
  * Flash-attention forward with online softmax; `scale` multiplies q.k (the
  * reference hard-codes the f16 constant 0.08837890625 at :10); `causal`
  * (not in the reference; needs Sq == Skv) hides key j from query i < j.
- * tile_m (64 or 128) is the workgroup's query tile; tile_b (<= BH) and
- * tile_n (<= Skv, the online-softmax step) are validated, the kernel steps
- * KV in 64-key LDS blocks.  D = 64 or 128, Skv a multiple of 8. */
+ * tile_m (64, 128, 192 or 256) is the workgroup's query tile; tile_b (<= BH)
+ * and tile_n (<= Skv, the online-softmax step) are validated, the kernel
+ * streams KV in 64-key LDS blocks.  D = 64 or 128, Skv a multiple of 8. */
 int loom_hip_attention(const void* k, const void* v, const void* q, void* out, int64_t BH,
                        int64_t Sq, int64_t Skv, int64_t D, float scale, int causal,
                        int64_t tile_b, int64_t tile_m, int64_t tile_n, void* stream, char* err,
@@ -124,6 +140,50 @@ int loom_hip_helion_mamba2_chunk_scan_kernel(
     int64_t nheads, int64_t ngroups, int64_t chunk_size, int64_t headdim, int64_t dstate,
     int64_t tile_b, int64_t tile_h, int64_t tile_c, int64_t tile_m, int64_t tile_n,
     int64_t tile_k, void* stream, char* err, size_t errlen);
+
+/* ---- materialization contract and by-name dispatch ---------------------- */
+
+/* Variant names the materialization pipeline emits for `funcs` under the
+ * solver's block-size JSON, written to out[0..outlen) one per line in
+ * emission order.  Follows run_materialization's input contract
+ * (lib/pipeline/src/loom_materialization_pipeline.cpp:81-192): the root is an
+ * object mapping a function name to a binding object {"sym": int}, a
+ * non-empty array of binding objects, or null (UNSAT: no variant);
+ * "__loom_candidate_order__" is an array of names that orders the functions
+ * (unranked ones last); "ALL" binds every function without an entry of its
+ * own and replaces the candidate order (:251-270).  An empty string selects
+ * the placeholder solver (lib/passes/loom-opt/src/materialize.cpp:56-65) over
+ * each example function's symbols.  Names are <func> + "__<sym><value>" in
+ * sorted symbol order, "__combo<i>" added on a clash (materialize.cpp:39-53,
+ * 253-262).  Rejections carry the reference's messages. */
+int loom_hip_materialize_variants(const char* block_sizes_json, const char* const* funcs,
+                                  int nfuncs, char* out, size_t outlen, char* err,
+                                  size_t errlen);
+
+/* Splits a materialized variant name into its function name (the text
+ * before the first "__") and the tile_* values its suffix binds
+ * (tiles[LOOM_HIP_TILE_*], -1 where unbound).  Other "__" tokens (mapping
+ * variants such as "__d0i0_d1i0", "__combo<i>") are skipped.  Inverse of the
+ * naming in materialize.cpp:39-53. */
+int loom_hip_parse_variant(const char* variant, char* func, size_t funclen, int64_t* tiles,
+                           char* err, size_t errlen);
+
+/* Launches the kernel a materialized variant names: the step a gfx950
+ * backend performs where the reference hands materialized IR to its TT
+ * lowering (lib/pipeline/src/loom_materialization_pipeline.cpp:307-313).
+ * `tensors` are the function's memref arguments in IR order; `dims` its
+ * extents in the order of the matching entry point above:
+ *   matmul (3 tensors) M,N,K | batch_matmul (3) B,M,N,K |
+ *   split_k_matmul_gather (3) M,N,K (workspace = partials) |
+ *   attention (4) BH,Sq,Skv,D (scale, causal used) |
+ *   flash_decode (4) B,H,D,S (scale used; workspace as for that call) |
+ *   helion_mamba2_chunk_scan_kernel (8) batch,nchunks,nheads,ngroups,
+ *   chunk_size,headdim,dstate.
+ * Every tile symbol the entry point takes must be bound by the name.
+ * Unknown functions return LOOM_HIP_EUNSUP. */
+int loom_hip_dispatch(const char* variant, void* const* tensors, int ntensors,
+                      const int64_t* dims, int ndims, float scale, int causal, void* workspace,
+                      size_t workspace_bytes, void* stream, char* err, size_t errlen);
 
 #ifdef __cplusplus
 }

@@ -1,11 +1,631 @@
-// abi.cpp -- library-wide C ABI entry points (version string).
+// abi.cpp -- library-wide C ABI: version, the materialization contract of the
+// reference (block-size JSON -> variant names, variant name -> tile values)
+// and the by-name dispatcher a backend seam calls.
 //
-// The kernels' entry points live next to their kernels (gemm.hip,
-// attention.hip, decode.hip, mamba.hip); this file holds what belongs to the
-// library as a whole.  The version string is the counterpart of the
-// reference pybind module's __version__ (lib/pipeline/src/loom_pybind.cpp:19).
+// Reference behaviour mirrored here:
+//   - block-size JSON (lib/pipeline/src/loom_materialization_pipeline.cpp:
+//     81-192): a top-level object; each key names a function and maps to a
+//     binding object {"sym": int, ...}, a non-empty array of such objects, or
+//     null (UNSAT: the function is skipped); "__loom_candidate_order__" maps
+//     to an array of strings; symbol values must be integers; "ALL" expands
+//     to every function that has no binding of its own (:251-270);
+//   - variant names (lib/passes/loom-opt/src/materialize.cpp:39-53,253-262):
+//     <function> + "__<sym><value>" for every bound symbol in sorted symbol
+//     order, with "__combo<i>" appended while a name is already taken;
+//   - error reporting as (code, message), the pipeline's "(error, result)"
+//     convention (lib/pipeline/__init__.py:97-98).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cctype>
+#include <cerrno>
+#include <cstdlib>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <set>
+#include <string>
+#include <utility>
+#include <vector>
+
 #include "../../include/loom_hip.h"
 
-#define LOOM_HIP_VERSION_STRING "loom_hip 0.1.0 gfx950"
+#define LOOM_HIP_VERSION_STRING "loom_hip 0.2.0 gfx950"
 
-extern "C" const char* loom_hip_version(void) { return LOOM_HIP_VERSION_STRING; }
+namespace {
+
+int fail(char* err, size_t errlen, int code, const char* fmt, ...) {
+  if (err && errlen) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(err, errlen, fmt, ap);
+    va_end(ap);
+  }
+  return code;
+}
+
+// ---------------------------------------------------------------------------
+// Minimal JSON reader: objects (key order kept), arrays, strings, numbers
+// (integer-valued or not), true/false/null.
+// ---------------------------------------------------------------------------
+struct JVal {
+  enum Kind { Null, Bool, Int, Real, Str, Arr, Obj } kind = Null;
+  bool b = false;
+  long long i = 0;
+  std::string s;
+  std::vector<JVal> arr;
+  std::vector<std::pair<std::string, JVal>> obj;
+};
+
+struct JParser {
+  const char* p;
+  const char* end;
+  std::string err;
+
+  void ws() {
+    while (p < end && (*p == ' ' || *p == '\t' || *p == '\n' || *p == '\r')) ++p;
+  }
+  bool bad(const char* what) {
+    if (err.empty()) err = what;
+    return false;
+  }
+  bool lit(const char* w) {
+    const size_t n = strlen(w);
+    if ((size_t)(end - p) < n || strncmp(p, w, n) != 0) return false;
+    p += n;
+    return true;
+  }
+  bool str(std::string& out) {
+    if (p >= end || *p != '"') return bad("expected a string");
+    ++p;
+    out.clear();
+    while (p < end && *p != '"') {
+      char c = *p++;
+      if (c == '\\') {
+        if (p >= end) return bad("unterminated escape");
+        const char e = *p++;
+        switch (e) {
+          case '"': out += '"'; break;
+          case '\\': out += '\\'; break;
+          case '/': out += '/'; break;
+          case 'b': out += '\b'; break;
+          case 'f': out += '\f'; break;
+          case 'n': out += '\n'; break;
+          case 'r': out += '\r'; break;
+          case 't': out += '\t'; break;
+          case 'u': {
+            if (end - p < 4) return bad("short \\u escape");
+            unsigned v = 0;
+            for (int k = 0; k < 4; ++k) {
+              const char h = *p++;
+              v <<= 4;
+              if (h >= '0' && h <= '9') v |= h - '0';
+              else if (h >= 'a' && h <= 'f') v |= h - 'a' + 10;
+              else if (h >= 'A' && h <= 'F') v |= h - 'A' + 10;
+              else return bad("bad \\u escape");
+            }
+            if (v < 0x80) {
+              out += (char)v;
+            } else if (v < 0x800) {
+              out += (char)(0xC0 | (v >> 6));
+              out += (char)(0x80 | (v & 0x3F));
+            } else {
+              out += (char)(0xE0 | (v >> 12));
+              out += (char)(0x80 | ((v >> 6) & 0x3F));
+              out += (char)(0x80 | (v & 0x3F));
+            }
+            break;
+          }
+          default: return bad("bad escape");
+        }
+      } else {
+        out += c;
+      }
+    }
+    if (p >= end) return bad("unterminated string");
+    ++p;
+    return true;
+  }
+  bool num(JVal& v) {
+    const char* s = p;
+    if (p < end && *p == '-') ++p;
+    if (p >= end || !isdigit((unsigned char)*p)) return bad("bad number");
+    while (p < end && isdigit((unsigned char)*p)) ++p;
+    bool real = false;
+    if (p < end && *p == '.') {
+      real = true;
+      ++p;
+      if (p >= end || !isdigit((unsigned char)*p)) return bad("bad number");
+      while (p < end && isdigit((unsigned char)*p)) ++p;
+    }
+    if (p < end && (*p == 'e' || *p == 'E')) {
+      real = true;
+      ++p;
+      if (p < end && (*p == '+' || *p == '-')) ++p;
+      if (p >= end || !isdigit((unsigned char)*p)) return bad("bad number");
+      while (p < end && isdigit((unsigned char)*p)) ++p;
+    }
+    const std::string t(s, p);
+    if (!real) {
+      errno = 0;
+      char* e = nullptr;
+      const long long x = strtoll(t.c_str(), &e, 10);
+      if (errno == ERANGE) return bad("integer out of range");
+      v.kind = JVal::Int;
+      v.i = x;
+      return true;
+    }
+    // a real number that happens to be integral (e.g. 64.0) is still an
+    // integer value, as llvm::json::Value::getAsInteger accepts it
+    const double d = strtod(t.c_str(), nullptr);
+    if (d == (double)(long long)d && d > -9.2e18 && d < 9.2e18) {
+      v.kind = JVal::Int;
+      v.i = (long long)d;
+    } else {
+      v.kind = JVal::Real;
+    }
+    return true;
+  }
+  bool value(JVal& v, int depth) {
+    if (depth > 64) return bad("nesting too deep");
+    ws();
+    if (p >= end) return bad("unexpected end of input");
+    const char c = *p;
+    if (c == '{') {
+      ++p;
+      v.kind = JVal::Obj;
+      ws();
+      if (p < end && *p == '}') {
+        ++p;
+        return true;
+      }
+      for (;;) {
+        ws();
+        std::string k;
+        if (!str(k)) return false;
+        ws();
+        if (p >= end || *p != ':') return bad("expected ':'");
+        ++p;
+        JVal child;
+        if (!value(child, depth + 1)) return false;
+        v.obj.emplace_back(std::move(k), std::move(child));
+        ws();
+        if (p < end && *p == ',') {
+          ++p;
+          continue;
+        }
+        if (p < end && *p == '}') {
+          ++p;
+          return true;
+        }
+        return bad("expected ',' or '}'");
+      }
+    }
+    if (c == '[') {
+      ++p;
+      v.kind = JVal::Arr;
+      ws();
+      if (p < end && *p == ']') {
+        ++p;
+        return true;
+      }
+      for (;;) {
+        JVal child;
+        if (!value(child, depth + 1)) return false;
+        v.arr.push_back(std::move(child));
+        ws();
+        if (p < end && *p == ',') {
+          ++p;
+          continue;
+        }
+        if (p < end && *p == ']') {
+          ++p;
+          return true;
+        }
+        return bad("expected ',' or ']'");
+      }
+    }
+    if (c == '"') {
+      v.kind = JVal::Str;
+      return str(v.s);
+    }
+    if (lit("true")) {
+      v.kind = JVal::Bool;
+      v.b = true;
+      return true;
+    }
+    if (lit("false")) {
+      v.kind = JVal::Bool;
+      return true;
+    }
+    if (lit("null")) {
+      v.kind = JVal::Null;
+      return true;
+    }
+    return num(v);
+  }
+};
+
+bool parse_json(const std::string& text, JVal& root, std::string& err) {
+  JParser jp{text.data(), text.data() + text.size(), {}};
+  if (!jp.value(root, 0)) {
+    err = jp.err;
+    return false;
+  }
+  jp.ws();
+  if (jp.p != jp.end) {
+    err = "trailing characters after the JSON value";
+    return false;
+  }
+  return true;
+}
+
+// ---------------------------------------------------------------------------
+// Block-size map (function -> bindings), as the materialization pipeline
+// builds it.
+// ---------------------------------------------------------------------------
+typedef std::map<std::string, long long> Binding;  // sorted by symbol name
+
+struct BlockSizes {
+  std::vector<std::pair<std::string, std::vector<Binding>>> funcs;  // key order
+  std::vector<std::string> candidate_order;
+  bool has_all = false;
+  std::vector<Binding> all;
+};
+
+bool parse_symbol_map(const std::string& fkey, const JVal& obj, Binding& out, std::string& err) {
+  for (const auto& kv : obj.obj) {
+    if (kv.second.kind != JVal::Int) {
+      err = "Value for symbol '" + kv.first + "' in '" + fkey + "' must be an integer";
+      return false;
+    }
+    out[kv.first] = kv.second.i;
+  }
+  return true;
+}
+
+bool parse_binding_list(const std::string& fkey, const JVal& v, std::vector<Binding>& out,
+                        std::string& err) {
+  if (v.kind == JVal::Obj) {
+    Binding b;
+    if (!parse_symbol_map(fkey, v, b, err)) return false;
+    out.push_back(std::move(b));
+    return true;
+  }
+  if (v.kind == JVal::Arr) {
+    if (v.arr.empty()) {
+      err = "Value for key '" + fkey + "' must not be an empty array";
+      return false;
+    }
+    for (size_t i = 0; i < v.arr.size(); ++i) {
+      if (v.arr[i].kind != JVal::Obj) {
+        err = "Value for key '" + fkey + "' at index " + std::to_string(i) +
+              " must be a JSON object";
+        return false;
+      }
+      Binding b;
+      if (!parse_symbol_map(fkey, v.arr[i], b, err)) return false;
+      out.push_back(std::move(b));
+    }
+    return true;
+  }
+  err = "Value for key '" + fkey + "' must be a JSON object, array of objects, or null";
+  return false;
+}
+
+bool parse_block_sizes(const std::string& text, BlockSizes& bs, std::string& err) {
+  if (text.empty()) return true;  // the reference then uses its placeholder solver
+  JVal root;
+  std::string perr;
+  if (!parse_json(text, root, perr)) {
+    err = "Failed to parse block_sizes_json: " + perr;
+    return false;
+  }
+  if (root.kind != JVal::Obj) {
+    err = "block_sizes_json must be a JSON object at the top level";
+    return false;
+  }
+  for (const auto& kv : root.obj) {
+    const std::string& fkey = kv.first;
+    if (fkey == "__loom_candidate_order__") {
+      if (kv.second.kind != JVal::Arr) {
+        err = "Value for '__loom_candidate_order__' must be an array";
+        return false;
+      }
+      for (const auto& n : kv.second.arr) {
+        if (n.kind != JVal::Str) {
+          err = "Entries in '__loom_candidate_order__' must be strings";
+          return false;
+        }
+        bs.candidate_order.push_back(n.s);
+      }
+      continue;
+    }
+    if (kv.second.kind == JVal::Null) continue;  // UNSAT: no variant emitted
+    std::vector<Binding> bl;
+    if (!parse_binding_list(fkey, kv.second, bl, err)) return false;
+    if (fkey == "ALL") {
+      bs.has_all = true;
+      bs.all = std::move(bl);
+      continue;
+    }
+    bool replaced = false;
+    for (auto& f : bs.funcs)
+      if (f.first == fkey) {
+        f.second = bl;
+        replaced = true;
+      }
+    if (!replaced) bs.funcs.emplace_back(fkey, std::move(bl));
+  }
+  return true;
+}
+
+std::string suffix_of(const Binding& b) {
+  std::string s;
+  for (const auto& kv : b) s += "__" + kv.first + std::to_string(kv.second);
+  return s;
+}
+
+// ---------------------------------------------------------------------------
+// Tile symbols the kernels know, and variant-name parsing
+// ---------------------------------------------------------------------------
+const char* const kTileNames[LOOM_HIP_NTILES] = {"tile_b", "tile_m", "tile_n", "tile_k",
+                                                 "tile_s", "tile_h", "tile_c"};
+
+int tile_index(const std::string& sym) {
+  for (int i = 0; i < LOOM_HIP_NTILES; ++i)
+    if (sym == kTileNames[i]) return i;
+  return -1;
+}
+
+const char* const kFunctions[] = {"matmul", "batch_matmul", "split_k_matmul_gather",
+                                  "attention", "flash_decode",
+                                  "helion_mamba2_chunk_scan_kernel"};
+
+bool known_function(const std::string& f) {
+  for (const char* k : kFunctions)
+    if (f == k) return true;
+  return false;
+}
+
+// "<func>[__<mapping>...]__tile_k64__tile_m128[__comboN]" -> func, tiles.
+// Tokens are the "__"-separated pieces after the function name; a token that
+// starts with "tile_" and ends in digits binds that symbol, others (mapping
+// variants, combo indices) are ignored.
+int parse_variant(const std::string& name, std::string& func, int64_t* tiles,
+                  std::string& err) {
+  for (int i = 0; i < LOOM_HIP_NTILES; ++i) tiles[i] = -1;
+  const size_t first = name.find("__");
+  func = name.substr(0, first);
+  if (func.empty()) {
+    err = "variant name '" + name + "' has no function name";
+    return LOOM_HIP_EINVAL;
+  }
+  size_t pos = first;
+  while (pos != std::string::npos) {
+    pos += 2;
+    const size_t next = name.find("__", pos);
+    const std::string tok = name.substr(pos, next == std::string::npos ? std::string::npos
+                                                                         : next - pos);
+    pos = next;
+    if (tok.compare(0, 5, "tile_") != 0) continue;
+    size_t d = tok.size();
+    while (d > 0 && isdigit((unsigned char)tok[d - 1])) --d;
+    if (d == tok.size()) {
+      err = "variant token '" + tok + "' carries no value";
+      return LOOM_HIP_EINVAL;
+    }
+    const std::string sym = tok.substr(0, d);
+    const int ti = tile_index(sym);
+    if (ti < 0) {
+      err = "variant token '" + tok + "' names an unknown block-size symbol";
+      return LOOM_HIP_EINVAL;
+    }
+    if (tok.size() - d > 12) {
+      err = "variant token '" + tok + "' value out of range";
+      return LOOM_HIP_EINVAL;
+    }
+    tiles[ti] = atoll(tok.c_str() + d);
+  }
+  return LOOM_HIP_OK;
+}
+
+// loom.sym symbols of each example function in order of first appearance
+// (examples/*/IR/00_from_helion_frontend.mlir), which is the order the
+// placeholder solver zips its candidate tuple with.
+const std::vector<std::string>* known_symbols(const std::string& f) {
+  static const std::map<std::string, std::vector<std::string>> table = {
+      {"matmul", {"tile_m", "tile_n", "tile_k"}},
+      {"batch_matmul", {"tile_b", "tile_m", "tile_n", "tile_k"}},
+      {"split_k_matmul_gather", {"tile_m", "tile_n", "tile_k"}},
+      {"attention", {"tile_b", "tile_m", "tile_n"}},
+      {"flash_decode", {"tile_b", "tile_s", "tile_n"}},
+      {"helion_mamba2_chunk_scan_kernel",
+       {"tile_m", "tile_n", "tile_k", "tile_c", "tile_b", "tile_h"}},
+  };
+  auto it = table.find(f);
+  return it == table.end() ? nullptr : &it->second;
+}
+
+// Placeholder solver of lib/passes/loom-opt/src/materialize.cpp:56-65: one
+// candidate, {64,64,512} for three symbols, {64,32,64,8,1,4} for six, else 64
+// for every symbol.
+Binding placeholder_binding(const std::vector<std::string>& syms) {
+  std::vector<long long> vals(syms.size(), 64);
+  if (syms.size() == 3) vals = {64, 64, 512};
+  if (syms.size() == 6) vals = {64, 32, 64, 8, 1, 4};
+  Binding b;
+  for (size_t i = 0; i < syms.size(); ++i) b[syms[i]] = vals[i];
+  return b;
+}
+
+int need_tiles(const std::string& func, const int64_t* tiles, std::initializer_list<int> which,
+               char* err, size_t errlen) {
+  for (int i : which)
+    if (tiles[i] < 0)
+      return fail(err, errlen, LOOM_HIP_EINVAL, "dispatch: variant of %s lacks %s", func.c_str(),
+                  kTileNames[i]);
+  return LOOM_HIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* loom_hip_version(void) { return LOOM_HIP_VERSION_STRING; }
+
+int loom_hip_materialize_variants(const char* block_sizes_json, const char* const* funcs,
+                                  int nfuncs, char* out, size_t outlen, char* err,
+                                  size_t errlen) {
+  if (!block_sizes_json || (nfuncs > 0 && !funcs) || nfuncs < 0)
+    return fail(err, errlen, LOOM_HIP_EINVAL, "materialize_variants: null argument");
+  for (int i = 0; i < nfuncs; ++i)
+    if (!funcs[i]) return fail(err, errlen, LOOM_HIP_EINVAL, "materialize_variants: null name");
+  BlockSizes bs;
+  std::string perr;
+  if (!parse_block_sizes(block_sizes_json, bs, perr))
+    return fail(err, errlen, LOOM_HIP_EINVAL, "%s", perr.c_str());
+  const bool external = block_sizes_json[0] != '\0';
+
+  std::vector<std::string> order(funcs, funcs + nfuncs);
+  if (external) {
+    // "ALL": every listed function without its own binding, in list order;
+    // it replaces the candidate order by exactly those functions
+    if (bs.has_all) {
+      bs.candidate_order.clear();
+      for (const auto& f : order) {
+        bool have = false;
+        for (const auto& e : bs.funcs) have |= e.first == f;
+        if (!have) {
+          bs.funcs.emplace_back(f, bs.all);
+          bs.candidate_order.push_back(f);
+        }
+      }
+    }
+    // stable sort by candidate rank; unranked functions keep list order last
+    std::map<std::string, size_t> rank;
+    for (size_t r = 0; r < bs.candidate_order.size(); ++r) rank[bs.candidate_order[r]] = r;
+    auto rank_of = [&](const std::string& f) {
+      auto it = rank.find(f);
+      return it == rank.end() ? rank.size() : it->second;
+    };
+    std::stable_sort(order.begin(), order.end(), [&](const std::string& a, const std::string& b) {
+      return rank_of(a) < rank_of(b);
+    });
+  }
+
+  std::string names;
+  for (const auto& f : order) {
+    std::vector<Binding> bl;
+    if (external) {
+      for (const auto& e : bs.funcs)
+        if (e.first == f) bl = e.second;
+    } else {
+      // mapping variants ("matmul__x8_y1y8__...") carry their base's symbols
+      const std::vector<std::string>* syms = known_symbols(f.substr(0, f.find("__")));
+      if (!syms || syms->empty()) continue;  // symbols unknown: nothing to bind
+      bl.push_back(placeholder_binding(*syms));
+    }
+    std::set<std::string> used;  // names are unique per function's module
+    for (size_t bi = 0; bi < bl.size(); ++bi) {
+      std::string n = f + suffix_of(bl[bi]);
+      if (used.count(n)) {
+        const std::string base = n;
+        unsigned combo = (unsigned)bi;
+        do {
+          ++combo;
+          n = base + "__combo" + std::to_string(combo);
+        } while (used.count(n));
+      }
+      used.insert(n);
+      names += n;
+      names += '\n';
+    }
+  }
+  if (!out || outlen <= names.size())
+    return fail(err, errlen, LOOM_HIP_EINVAL,
+                "materialize_variants: output buffer needs %zu bytes", names.size() + 1);
+  memcpy(out, names.c_str(), names.size() + 1);
+  if (err && errlen) err[0] = '\0';
+  return LOOM_HIP_OK;
+}
+
+int loom_hip_parse_variant(const char* variant, char* func, size_t funclen, int64_t* tiles,
+                           char* err, size_t errlen) {
+  if (!variant || !tiles)
+    return fail(err, errlen, LOOM_HIP_EINVAL, "parse_variant: null argument");
+  std::string f, perr;
+  const int rc = parse_variant(variant, f, tiles, perr);
+  if (rc) return fail(err, errlen, rc, "%s", perr.c_str());
+  if (func) {
+    if (funclen <= f.size())
+      return fail(err, errlen, LOOM_HIP_EINVAL, "parse_variant: function buffer too small");
+    memcpy(func, f.c_str(), f.size() + 1);
+  }
+  if (err && errlen) err[0] = '\0';
+  return LOOM_HIP_OK;
+}
+
+int loom_hip_dispatch(const char* variant, void* const* tensors, int ntensors,
+                      const int64_t* dims, int ndims, float scale, int causal,
+                      void* workspace, size_t workspace_bytes, void* stream, char* err,
+                      size_t errlen) {
+  if (!variant || (ntensors > 0 && !tensors) || (ndims > 0 && !dims))
+    return fail(err, errlen, LOOM_HIP_EINVAL, "dispatch: null argument");
+  std::string f, perr;
+  int64_t t[LOOM_HIP_NTILES];
+  int rc = parse_variant(variant, f, t, perr);
+  if (rc) return fail(err, errlen, rc, "dispatch: %s", perr.c_str());
+  if (!known_function(f))
+    return fail(err, errlen, LOOM_HIP_EUNSUP, "dispatch: no gfx950 kernel for function '%s'",
+                f.c_str());
+  auto shape = [&](int nt, int nd) {
+    if (ntensors != nt || ndims != nd)
+      return fail(err, errlen, LOOM_HIP_EINVAL,
+                  "dispatch: %s takes %d tensors and %d extents (got %d and %d)", f.c_str(), nt,
+                  nd, ntensors, ndims);
+    return (int)LOOM_HIP_OK;
+  };
+  if (f == "matmul") {
+    if ((rc = shape(3, 3)) || (rc = need_tiles(f, t, {1, 2, 3}, err, errlen))) return rc;
+    return loom_hip_matmul(tensors[0], tensors[1], tensors[2], dims[0], dims[1], dims[2],
+                           t[LOOM_HIP_TILE_M], t[LOOM_HIP_TILE_N], t[LOOM_HIP_TILE_K], stream,
+                           err, errlen);
+  }
+  if (f == "batch_matmul") {
+    if ((rc = shape(3, 4)) || (rc = need_tiles(f, t, {0, 1, 2, 3}, err, errlen))) return rc;
+    return loom_hip_batch_matmul(tensors[0], tensors[1], tensors[2], dims[0], dims[1], dims[2],
+                                 dims[3], t[LOOM_HIP_TILE_B], t[LOOM_HIP_TILE_M],
+                                 t[LOOM_HIP_TILE_N], t[LOOM_HIP_TILE_K], stream, err, errlen);
+  }
+  if (f == "split_k_matmul_gather") {
+    if ((rc = shape(3, 3)) || (rc = need_tiles(f, t, {1, 2, 3}, err, errlen))) return rc;
+    return loom_hip_split_k_matmul_gather(tensors[0], tensors[1], tensors[2], workspace,
+                                          workspace_bytes, dims[0], dims[1], dims[2],
+                                          t[LOOM_HIP_TILE_M], t[LOOM_HIP_TILE_N],
+                                          t[LOOM_HIP_TILE_K], stream, err, errlen);
+  }
+  if (f == "attention") {
+    if ((rc = shape(4, 4)) || (rc = need_tiles(f, t, {0, 1, 2}, err, errlen))) return rc;
+    return loom_hip_attention(tensors[0], tensors[1], tensors[2], tensors[3], dims[0], dims[1],
+                              dims[2], dims[3], scale, causal, t[LOOM_HIP_TILE_B],
+                              t[LOOM_HIP_TILE_M], t[LOOM_HIP_TILE_N], stream, err, errlen);
+  }
+  if (f == "flash_decode") {
+    if ((rc = shape(4, 4)) || (rc = need_tiles(f, t, {0, 2, 4}, err, errlen))) return rc;
+    return loom_hip_flash_decode(tensors[0], tensors[1], tensors[2], tensors[3], workspace,
+                                 workspace_bytes, dims[0], dims[1], dims[2], dims[3], scale,
+                                 t[LOOM_HIP_TILE_B], t[LOOM_HIP_TILE_S], t[LOOM_HIP_TILE_N],
+                                 stream, err, errlen);
+  }
+  // helion_mamba2_chunk_scan_kernel
+  if ((rc = shape(8, 7)) || (rc = need_tiles(f, t, {0, 1, 2, 3, 5, 6}, err, errlen))) return rc;
+  return loom_hip_helion_mamba2_chunk_scan_kernel(
+      tensors[0], tensors[1], tensors[2], tensors[3], tensors[4], tensors[5], tensors[6],
+      tensors[7], dims[0], dims[1], dims[2], dims[3], dims[4], dims[5], dims[6],
+      t[LOOM_HIP_TILE_B], t[LOOM_HIP_TILE_H], t[LOOM_HIP_TILE_C], t[LOOM_HIP_TILE_M],
+      t[LOOM_HIP_TILE_N], t[LOOM_HIP_TILE_K], stream, err, errlen);
+}
+
+}  // extern "C"

@@ -54,9 +54,24 @@ _lib.loom_hip_split_k_workspace_bytes.restype = _sz
 _lib.loom_hip_flash_decode_workspace_bytes.argtypes = [_i64] * 5
 _lib.loom_hip_flash_decode_workspace_bytes.restype = _sz
 _lib.loom_hip_version.restype = ctypes.c_char_p
+_lib.loom_hip_materialize_variants.argtypes = [ctypes.c_char_p, ctypes.POINTER(ctypes.c_char_p),
+                                               ctypes.c_int, ctypes.c_char_p, _sz, *_ERR]
+_lib.loom_hip_materialize_variants.restype = ctypes.c_int
+_lib.loom_hip_parse_variant.argtypes = [ctypes.c_char_p, ctypes.c_char_p, _sz,
+                                        ctypes.POINTER(_i64), *_ERR]
+_lib.loom_hip_parse_variant.restype = ctypes.c_int
+_lib.loom_hip_dispatch.argtypes = [ctypes.c_char_p, ctypes.POINTER(_vp), ctypes.c_int,
+                                   ctypes.POINTER(_i64), ctypes.c_int, _f32, ctypes.c_int,
+                                   _vp, _sz, _vp, *_ERR]
+_lib.loom_hip_dispatch.restype = ctypes.c_int
 
 EXPORTED = tuple(_SIGS) + ("loom_hip_split_k_workspace_bytes",
-                           "loom_hip_flash_decode_workspace_bytes", "loom_hip_version")
+                           "loom_hip_flash_decode_workspace_bytes", "loom_hip_version",
+                           "loom_hip_materialize_variants", "loom_hip_parse_variant",
+                           "loom_hip_dispatch")
+
+#: block-size symbols in the slot order of loom_hip_parse_variant's tiles[]
+TILE_SYMBOLS = ("tile_b", "tile_m", "tile_n", "tile_k", "tile_s", "tile_h", "tile_c")
 
 __version__ = _lib.loom_hip_version().decode()
 
@@ -240,3 +255,102 @@ def helion_mamba2_chunk_scan_kernel(cb, x, dt, dA_cumsum, C, D, prev_states_T, o
           _need(out, "out", _bf16, 4), b, nc, H, G, Q, P, N, tile_b, tile_h, tile_c,
           tile_m, tile_n, tile_k, _stream(x))
     return out
+
+
+# ---------------------------------------------------------------------------
+# materialization contract and by-name dispatch
+# (lib/pipeline/src/loom_materialization_pipeline.cpp:81-192,251-270,
+#  lib/passes/loom-opt/src/materialize.cpp:39-65,253-262)
+# ---------------------------------------------------------------------------
+
+FUNCTIONS = ("matmul", "batch_matmul", "split_k_matmul_gather", "attention", "flash_decode",
+             "helion_mamba2_chunk_scan_kernel")
+
+
+def materialize_variants(block_sizes_json: str, funcs=FUNCTIONS) -> list:
+    """Variant names run_materialization emits for ``funcs`` under the
+    solver's block-size JSON (``""`` = placeholder solver), in emission order.
+    A rejected JSON raises ``RuntimeError`` with the reference's message."""
+    names = [f.encode() for f in funcs]
+    arr = (ctypes.c_char_p * max(len(names), 1))(*names)
+    js = block_sizes_json.encode()
+    cap = 4096 + 64 * len(js)
+    while True:
+        out = ctypes.create_string_buffer(cap)
+        err = ctypes.create_string_buffer(512)
+        rc = _lib.loom_hip_materialize_variants(js, arr, len(names), out, cap, err, len(err))
+        if rc == 0:
+            return [n for n in out.value.decode().split("\n") if n]
+        msg = err.value.decode(errors="replace")
+        if "output buffer needs" in msg:
+            cap = int(msg.rsplit(" ", 2)[-2]) + 1
+            continue
+        raise LoomHipError("loom_hip_materialize_variants", rc, msg)
+
+
+def parse_variant(name: str):
+    """``"matmul__tile_k64__tile_m128__tile_n128"`` -> ``("matmul",
+    {"tile_k": 64, "tile_m": 128, "tile_n": 128})``."""
+    func = ctypes.create_string_buffer(len(name) + 1)
+    tiles = (_i64 * len(TILE_SYMBOLS))()
+    err = ctypes.create_string_buffer(512)
+    rc = _lib.loom_hip_parse_variant(name.encode(), func, len(func), tiles, err, len(err))
+    if rc != 0:
+        raise LoomHipError("loom_hip_parse_variant", rc, err.value.decode(errors="replace"))
+    return func.value.decode(), {s: int(t) for s, t in zip(TILE_SYMBOLS, tiles) if t >= 0}
+
+
+def _dims_of(func: str, tensors):
+    if func in ("matmul", "split_k_matmul_gather"):
+        (M, K), N = tensors[0].shape, tensors[1].shape[1]
+        return [M, N, K]
+    if func == "batch_matmul":
+        (B, M, K), N = tensors[0].shape, tensors[1].shape[2]
+        return [B, M, N, K]
+    if func == "attention":
+        BH, D, Skv = tensors[0].shape
+        return [BH, tensors[2].shape[1], Skv, D]
+    if func == "flash_decode":
+        B, D, S = tensors[0].shape
+        return [B, tensors[2].shape[1], D, S]
+    if func == "helion_mamba2_chunk_scan_kernel":
+        b, nc, G, Q, _ = tensors[0].shape
+        _, H, _, P = tensors[1].shape
+        return [b, nc, H, G, Q, P, tensors[4].shape[-1]]
+    raise LoomHipError("loom_hip_dispatch", 2, f"no gfx950 kernel for function '{func}'")
+
+
+def dispatch(variant: str, *tensors, workspace=None, scale=None, causal=False):
+    """Runs the kernel a materialized variant name selects on ``tensors``
+    (the function's memref arguments in IR order, outputs included) through
+    ``loom_hip_dispatch``.  split_k_matmul_gather and flash_decode allocate
+    their workspace when none is given; it is returned with the output."""
+    func, tiles = parse_variant(variant)
+    dims = _dims_of(func, tensors)
+    ptrs = []
+    for i, t in enumerate(tensors):
+        if not isinstance(t, torch.Tensor) or t.device.type != "cuda" or not t.is_contiguous():
+            raise ValueError(f"dispatch: tensor {i} must be a contiguous ROCm tensor")
+        ptrs.append(t.data_ptr())
+    dev = tensors[0].device
+    if workspace is None and func == "split_k_matmul_gather" and "tile_k" in tiles:
+        M, N, K = dims
+        workspace = torch.empty(max(split_k_workspace_bytes(M, N, K, tiles["tile_k"]), 4),
+                                dtype=torch.uint8, device=dev)
+    if workspace is None and func == "flash_decode" and "tile_s" in tiles:
+        B, H, D, S = dims
+        workspace = flash_decode_workspace(B, H, D, S, tiles["tile_s"], dev)
+    if scale is None:
+        d = dims[3] if func in ("attention",) else dims[2] if func == "flash_decode" else 1
+        scale = 1.0 / math.sqrt(d)
+    tarr = (_vp * max(len(ptrs), 1))(*ptrs)
+    darr = (_i64 * max(len(dims), 1))(*dims)
+    ws_ptr = workspace.data_ptr() if workspace is not None else None
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    err = ctypes.create_string_buffer(512)
+    rc = _lib.loom_hip_dispatch(variant.encode(), tarr, len(ptrs), darr, len(dims),
+                                float(scale), int(bool(causal)), ws_ptr, ws_bytes,
+                                _stream(tensors[0]), err, len(err))
+    if rc != 0:
+        raise LoomHipError("loom_hip_dispatch", rc, err.value.decode(errors="replace"))
+    return tensors[-1], workspace
