@@ -29,9 +29,6 @@
 
 namespace {
 
-constexpr int kKB = 64;       // keys per block
-constexpr int kWaves = 4;
-
 struct AttnParams {
   const uint16_t* k;
   const uint16_t* v;
@@ -40,216 +37,6 @@ struct AttnParams {
   int BH, Sq, Skv, causal, nqt;
   float c2;  // scale * log2(e)
 };
-
-// K^T row swizzle: distinct for the 8 keys {0..3, 8..11} (+4) read together
-LOOM_DEV int kswz(int key) { return (key & 3) | (((key >> 3) & 1) << 2); }
-
-template <int D, int QT>
-__global__ void __launch_bounds__(64 * kWaves) attention_kernel(AttnParams p) {
-  constexpr int BQ = 16 * QT * kWaves;     // queries per workgroup
-  constexpr int DCH = D / 8;               // 16-byte chunks per Ks row
-  constexpr int KCH = kKB / 8;             // 16-byte chunks per Vt row
-  constexpr int DSTEPS = D / 32;
-  constexpr int DT = D / 16;               // O^T tiles over d
-  constexpr int NBLK = KCH * DCH;          // 8x8 blocks per K (and per V) tile
-  static_assert(2 * NBLK <= 64 * kWaves, "one 8x8 block per copying thread");
-  constexpr int KS_UNITS = kKB * DCH, VT_UNITS = D * KCH;
-  constexpr int STAGE = KS_UNITS + VT_UNITS;
-  __shared__ u32x4_t lds[2 * STAGE];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
-  const int rr = lane & 15, g = lane >> 4;
-
-  // heaviest (last) query tiles first; consecutive ids walk over (b, h)
-  const int L = blockIdx.x;
-  const int qtile = p.nqt - 1 - L / p.BH;
-  const int bh = L % p.BH;
-  const int q0 = qtile * BQ;
-  const int Sq = p.Sq, Skv = p.Skv;
-
-  const uint16_t* __restrict__ kg = p.k + (int64_t)bh * D * Skv;
-  const uint16_t* __restrict__ vg = p.v + (int64_t)bh * Skv * D;
-  const uint16_t* __restrict__ qg = p.q + (int64_t)bh * Sq * D;
-
-  // ---- Q^T operand: lane holds q[qrow = q0 + 16*(QT*wave + qt) + rr][32 ds + 8 g ..]
-  const int wq0 = q0 + 16 * QT * wave;
-  u32x4_t qf[DSTEPS][QT];
-#pragma unroll
-  for (int qt = 0; qt < QT; ++qt) {
-    const int qrow = wq0 + 16 * qt + rr;
-#pragma unroll
-    for (int ds = 0; ds < DSTEPS; ++ds)
-      qf[ds][qt] = qrow < Sq
-                       ? *reinterpret_cast<const u32x4_t*>(qg + (int64_t)qrow * D + ds * 32 + g * 8)
-                       : u32x4_t{0u, 0u, 0u, 0u};
-  }
-
-  // ---- copy roles: threads [0, NBLK) stage K blocks, [NBLK, 2 NBLK) V blocks
-  const bool kcopy = tid < NBLK;
-  const bool vcopy = !kcopy && tid < 2 * NBLK;
-  const int ct = kcopy ? tid : tid - NBLK;
-  // K: d-chunk fastest (conflict-free Ks stores); V: key-chunk fastest
-  const int k_dc = ct % DCH, k_kc = ct / DCH;
-  const int v_kc = ct % KCH, v_dc = ct / KCH;
-  u32x4_t cr[8];
-
-  auto load_block = [&](int kv0) {
-    if (kcopy) {
-      const int key = kv0 + k_kc * 8;
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        cr[e] = key < Skv ? *reinterpret_cast<const u32x4_t*>(kg + (int64_t)(k_dc * 8 + e) * Skv + key)
-                          : u32x4_t{0u, 0u, 0u, 0u};
-    } else if (vcopy) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int key = kv0 + v_kc * 8 + e;
-        cr[e] = key < Skv ? *reinterpret_cast<const u32x4_t*>(vg + (int64_t)key * D + v_dc * 8)
-                          : u32x4_t{0u, 0u, 0u, 0u};
-      }
-    }
-  };
-  auto store_block = [&](int stage) {
-    u32x4_t tr[8];
-    if (kcopy) {
-      transpose8x8(cr, tr);  // tr[j] = d chunk k_dc of key 8 k_kc + j
-      u32x4_t* ks = lds + stage * STAGE;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int key = k_kc * 8 + j;
-        ks[key * DCH + (k_dc ^ kswz(key))] = tr[j];
-      }
-    } else if (vcopy) {
-      transpose8x8(cr, tr);  // tr[u] = keys 8 v_kc .. +7 of d = 8 v_dc + u
-      u32x4_t* vt = lds + stage * STAGE + KS_UNITS;
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int d = v_dc * 8 + u;
-        vt[d * KCH + (v_kc ^ (d & 7))] = tr[u];
-      }
-    }
-  };
-
-  float m_run[QT], l_run[QT];
-  f32x4_t ot[DT][QT];
-#pragma unroll
-  for (int qt = 0; qt < QT; ++qt) {
-    m_run[qt] = -INFINITY;
-    l_run[qt] = 0.f;
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) ot[dt][qt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  }
-
-  const int kv_end = p.causal ? min(Skv, q0 + BQ) : Skv;
-  const int nblk = (kv_end + kKB - 1) / kKB;
-  if (nblk > 0) {
-    load_block(0);
-    store_block(0);
-  }
-  __syncthreads();
-
-  for (int bi = 0; bi < nblk; ++bi) {
-    const int kv0 = bi * kKB;
-    if (bi + 1 < nblk) load_block(kv0 + kKB);
-    const u32x4_t* ks = lds + (bi & 1) * STAGE;
-    const u32x4_t* vt = ks + KS_UNITS;
-    // a wave whose queries all precede the block sees only masked keys
-    const bool active = !p.causal || kv0 <= wq0 + 16 * QT - 1;
-    if (active) {
-      // ---- S^T = K Q^T: tile jt = 2 pp + hh, row rr -> key 32pp + 8(rr/4) + 4hh + rr%4
-      f32x4_t st[4][QT];
-#pragma unroll
-      for (int jt = 0; jt < 4; ++jt)
-#pragma unroll
-        for (int qt = 0; qt < QT; ++qt) st[jt][qt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ds = 0; ds < DSTEPS; ++ds) {
-#pragma unroll
-        for (int jt = 0; jt < 4; ++jt) {
-          const int key = 32 * (jt >> 1) + 8 * (rr >> 2) + 4 * (jt & 1) + (rr & 3);
-          const u32x4_t a = ks[key * DCH + ((ds * 4 + g) ^ kswz(key))];
-#pragma unroll
-          for (int qt = 0; qt < QT; ++qt) st[jt][qt] = mfma16(a, qf[ds][qt], st[jt][qt]);
-        }
-      }
-      // ---- online softmax; st[jt][qt][i] is key 32(jt/2) + 8g + 4(jt%2) + i
-#pragma unroll
-      for (int qt = 0; qt < QT; ++qt) {
-        const int qrow = wq0 + 16 * qt + rr;
-        float mx = -INFINITY;
-#pragma unroll
-        for (int jt = 0; jt < 4; ++jt)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int key = kv0 + 32 * (jt >> 1) + 8 * g + 4 * (jt & 1) + i;
-            float t = st[jt][qt][i] * p.c2;
-            if (key >= Skv || (p.causal && key > qrow)) t = -INFINITY;
-            st[jt][qt][i] = t;
-            mx = fmaxf(mx, t);
-          }
-        mx = fmaxf(mx, __shfl_xor(mx, 16));
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        const float m_new = fmaxf(m_run[qt], mx);
-        // a row with no visible key so far keeps m = -inf; guard the exps
-        const float m_use = m_new == -INFINITY ? 0.f : m_new;
-        const float alpha = fast_exp2(m_run[qt] - m_use);
-        m_run[qt] = m_new;
-        float ls = 0.f;
-#pragma unroll
-        for (int jt = 0; jt < 4; ++jt)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float pv = fast_exp2(st[jt][qt][i] - m_use);
-            st[jt][qt][i] = pv;
-            ls += pv;
-          }
-        l_run[qt] = l_run[qt] * alpha + ls;
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) ot[dt][qt] *= alpha;
-      }
-      // ---- O^T += V^T P^T over the two 32-key pairs
-#pragma unroll
-      for (int pp = 0; pp < 2; ++pp) {
-        u32x4_t pf[QT];
-#pragma unroll
-        for (int qt = 0; qt < QT; ++qt)
-          pf[qt] = u32x4_t{pack_bf16x2(st[2 * pp][qt][0], st[2 * pp][qt][1]),
-                           pack_bf16x2(st[2 * pp][qt][2], st[2 * pp][qt][3]),
-                           pack_bf16x2(st[2 * pp + 1][qt][0], st[2 * pp + 1][qt][1]),
-                           pack_bf16x2(st[2 * pp + 1][qt][2], st[2 * pp + 1][qt][3])};
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-          const int d = dt * 16 + rr;
-          const u32x4_t a = vt[d * KCH + ((4 * pp + g) ^ (d & 7))];
-#pragma unroll
-          for (int qt = 0; qt < QT; ++qt) ot[dt][qt] = mfma16(a, pf[qt], ot[dt][qt]);
-        }
-      }
-    }
-    if (bi + 1 < nblk) store_block((bi + 1) & 1);
-    __syncthreads();
-  }
-
-  // ---- out = acc / l; O^T[dt][qt][i] is d = 16 dt + 4 g + i of query row
-#pragma unroll
-  for (int qt = 0; qt < QT; ++qt) {
-    float l = l_run[qt];
-    l += __shfl_xor(l, 16);
-    l += __shfl_xor(l, 32);
-    const float inv = 1.f / l;
-    const int qrow = wq0 + 16 * qt + rr;
-    if (qrow < Sq) {
-      uint16_t* orow = p.out + ((int64_t)bh * Sq + qrow) * D;
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        const f32x4_t o = ot[dt][qt];
-        *reinterpret_cast<u32x2_t*>(orow + dt * 16 + 4 * g) =
-            u32x2_t{pack_bf16x2(o[0] * inv, o[1] * inv), pack_bf16x2(o[2] * inv, o[3] * inv)};
-      }
-    }
-  }
-}
 
 // ---------------------------------------------------------------------------
 // LDS-DMA variant: K and V blocks are copied global -> LDS unchanged
@@ -268,14 +55,15 @@ __global__ void __launch_bounds__(64 * kWaves) attention_kernel(AttnParams p) {
 // Ks rows (128 B) and Vs rows (2 D bytes) XOR their 16-byte chunk index with
 // 2 (row & 3), so a transposed read's four rows hit distinct banks.
 // ---------------------------------------------------------------------------
-template <int D, int QT>
-__global__ void __launch_bounds__(256) attention_dma_kernel(AttnParams p) {
+template <int D, int QT, int W>
+__global__ void __launch_bounds__(64 * W) attention_dma_kernel(AttnParams p) {
   constexpr int KB = 64;                        // keys per stage
   constexpr int NS = 4;                         // stages
-  constexpr int BQ = 16 * QT * 4;               // queries per workgroup
+  constexpr int BQ = 16 * QT * W;               // queries per workgroup
   constexpr int K_BYTES = D * KB * 2, V_BYTES = KB * D * 2;
-  constexpr int K_INSTR = K_BYTES / 1024 / 4;   // DMA instructions per wave per stage
-  constexpr int V_INSTR = V_BYTES / 1024 / 4;
+  constexpr int K_INSTR = K_BYTES / 1024 / W;   // DMA instructions per wave per stage
+  constexpr int V_INSTR = V_BYTES / 1024 / W;
+  static_assert(K_INSTR >= 1 && V_INSTR >= 1, "every wave issues K and V copies");
   constexpr int LPW = K_INSTR + V_INSTR;
   constexpr int VROW = D * 2;                   // Vs row bytes
   constexpr int V_ROWS_PER_I = 1024 / VROW;
@@ -335,23 +123,33 @@ __global__ void __launch_bounds__(256) attention_dma_kernel(AttnParams p) {
     }
   };
 
-  // ---- Q^T operands: lane holds q[q0w + 16 qt + r][32 ds + 8 g .. +7]
+  // ---- Q^T operands: lane holds q[q0w + 16 qt + r][32 ds + 8 g .. +7] times
+  // scale * log2(e), rounded to bf16, so scores come out in the log2 domain
   const int q0w = q0 + 16 * QT * wave;
   u32x4_t qf[DSTEPS][QT];
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
     const int qrow = min(q0w + 16 * qt + r, Sq - 1);
 #pragma unroll
-    for (int ds = 0; ds < DSTEPS; ++ds)
-      qf[ds][qt] = *reinterpret_cast<const u32x4_t*>(qg + (int64_t)qrow * D + ds * 32 + g * 8);
+    for (int ds = 0; ds < DSTEPS; ++ds) {
+      const u32x4_t raw =
+          *reinterpret_cast<const u32x4_t*>(qg + (int64_t)qrow * D + ds * 32 + g * 8);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        qf[ds][qt][e] = pack_bf16x2(__uint_as_float(raw[e] << 16) * p.c2,
+                                    __uint_as_float(raw[e] & 0xffff0000u) * p.c2);
+    }
   }
 
-  float m_run[QT], l_run[QT];
-  f32x4_t ot[DT][QT];
+  // running base m (log2 domain) per query row; O^T and the row sums l (an
+  // MFMA of P^T against ones: every row of that tile holds l) share it
+  float m_run[QT];
+  f32x4_t ot[DT][QT], lacc[QT];
+  const u32x4_t ones = u32x4_t{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
-    m_run[qt] = -INFINITY;
-    l_run[qt] = 0.f;
+    m_run[qt] = 0.f;
+    lacc[qt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) ot[dt][qt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   }
@@ -365,12 +163,12 @@ __global__ void __launch_bounds__(256) attention_dma_kernel(AttnParams p) {
     if (p.causal && kv0 > q0w + 16 * QT - 1) return;
     const lds_char_t* ks = stK(s);
     const lds_char_t* vs = stV(s);
-    // ---- S^T = K^T Q^T; st[jt][qt][i] = score of key kv0 + 16 jt + 4 g + i
+    // ---- S^T = K^T Q^T - m; st[jt][qt][i] = score of key kv0 + 16 jt + 4 g + i
     f32x4_t st[4][QT];
 #pragma unroll
     for (int jt = 0; jt < 4; ++jt)
 #pragma unroll
-      for (int qt = 0; qt < QT; ++qt) st[jt][qt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      for (int qt = 0; qt < QT; ++qt) st[jt][qt] = f32x4_t{-m_run[qt], -m_run[qt], -m_run[qt], -m_run[qt]};
 #pragma unroll
     for (int ds = 0; ds < DSTEPS; ++ds) {
 #pragma unroll
@@ -400,7 +198,12 @@ __global__ void __launch_bounds__(256) attention_dma_kernel(AttnParams p) {
           }
       }
     }
-    // ---- online softmax, log2 domain, lazy rescale
+    // ---- lazy online softmax.  P = 2^(s - m) directly while every score
+    // stays within 2^8 of the base; the first block, or a block that rises
+    // higher, moves m to the row maximum and rescales O and l (numerator and
+    // denominator share m, so the result does not depend on it)
+    float lmax[QT];
+    bool big = false;
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
       float mx = -INFINITY;
@@ -408,40 +211,45 @@ __global__ void __launch_bounds__(256) attention_dma_kernel(AttnParams p) {
       for (int jt = 0; jt < 4; ++jt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) mx = fmaxf(mx, st[jt][qt][i]);
-      mx = fmaxf(mx, __shfl_xor(mx, 16));
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float mblk = mx * p.c2;
-      if (__builtin_amdgcn_ballot_w64(mblk > m_run[qt] + 8.f) != 0) {
-        const float m_new = fmaxf(m_run[qt], mblk);
-        const float alpha = fast_exp2(m_run[qt] - m_new);   // 0 on the first visible block
-        m_run[qt] = m_new;
-        l_run[qt] *= alpha;
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) ot[dt][qt] *= alpha;
-      }
-      // rows that have seen no key keep m = -inf: exponentiate against 0
-      const float mb = m_run[qt] == -INFINITY ? 0.f : m_run[qt];
-      float ls = 0.f;
-#pragma unroll
-      for (int jt = 0; jt < 4; ++jt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float pv = fast_exp2(__builtin_fmaf(st[jt][qt][i], p.c2, -mb));
-          st[jt][qt][i] = pv;
-          ls += pv;
-        }
-      l_run[qt] += ls;
+      lmax[qt] = mx;
+      big |= mx > 8.f;
     }
-    // ---- O^T += V^T P^T, 32 keys (tiles j0 = 2 pp, j1 = 2 pp + 1) per step
+    const bool first = blk == 0;
+    if (first || __builtin_amdgcn_ballot_w64(big) != 0) {
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) {
+        float mx = lmax[qt];
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        // the first block sets m (O and l are still zero); later ones only raise it
+        const float shift = first ? (mx == -INFINITY ? 0.f : mx) : fmaxf(mx, 0.f);
+        if (!first) {
+          const float alpha = fast_exp2(-shift);
+          lacc[qt] *= alpha;
+#pragma unroll
+          for (int dt = 0; dt < DT; ++dt) ot[dt][qt] *= alpha;
+        }
+        m_run[qt] += shift;
+#pragma unroll
+        for (int jt = 0; jt < 4; ++jt) st[jt][qt] -= shift;
+      }
+    }
+    // ---- O^T += V^T P^T and l += ones . P^T, 32 keys (tiles 2 pp, 2 pp + 1) per step
 #pragma unroll
     for (int pp = 0; pp < 2; ++pp) {
       u32x4_t pf[QT];
 #pragma unroll
-      for (int qt = 0; qt < QT; ++qt)
-        pf[qt] = u32x4_t{pack_bf16x2(st[2 * pp][qt][0], st[2 * pp][qt][1]),
-                         pack_bf16x2(st[2 * pp][qt][2], st[2 * pp][qt][3]),
-                         pack_bf16x2(st[2 * pp + 1][qt][0], st[2 * pp + 1][qt][1]),
-                         pack_bf16x2(st[2 * pp + 1][qt][2], st[2 * pp + 1][qt][3])};
+      for (int qt = 0; qt < QT; ++qt) {
+        f32x4_t e0, e1;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          e0[i] = fast_exp2(st[2 * pp][qt][i]);
+          e1[i] = fast_exp2(st[2 * pp + 1][qt][i]);
+        }
+        pf[qt] = u32x4_t{pack_bf16x2(e0[0], e0[1]), pack_bf16x2(e0[2], e0[3]),
+                         pack_bf16x2(e1[0], e1[1]), pack_bf16x2(e1[2], e1[3])};
+        lacc[qt] = mfma16(ones, pf[qt], lacc[qt]);
+      }
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
         const int ch = (2 * dt + (c4 >> 1)) ^ (2 * a4);
@@ -480,10 +288,7 @@ __global__ void __launch_bounds__(256) attention_dma_kernel(AttnParams p) {
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
     __builtin_amdgcn_sched_barrier(0);
-    float l = l_run[qt];
-    l += __shfl_xor(l, 16);
-    l += __shfl_xor(l, 32);
-    const float inv = 1.f / l;
+    const float inv = 1.f / lacc[qt][0];
     const int qrow = q0w + 16 * qt + r;
     if (qrow < Sq) {
       uint16_t* orow = p.out + ((int64_t)bh * Sq + qrow) * D;
@@ -495,12 +300,6 @@ __global__ void __launch_bounds__(256) attention_dma_kernel(AttnParams p) {
       }
     }
   }
-}
-
-template <int D, int QT>
-void launch_attn(const AttnParams& p, hipStream_t st) {
-  hipLaunchKernelGGL((attention_kernel<D, QT>), dim3((unsigned)(p.BH * p.nqt)),
-                     dim3(64 * kWaves), 0, st, p);
 }
 
 }  // namespace
@@ -547,27 +346,19 @@ int loom_hip_attention(const void* k, const void* v, const void* q, void* out, i
   p.nqt = (int)cdiv64(Sq, tile_m);
   p.c2 = scale * 1.4426950408889634f;
   hipStream_t st = static_cast<hipStream_t>(stream);
-#ifdef LOOM_ATTN_LEGACY
-  if (D == 128) {
-    if (tile_m == 128) launch_attn<128, 2>(p, st); else launch_attn<128, 1>(p, st);
-  } else {
-    if (tile_m == 128) launch_attn<64, 2>(p, st); else launch_attn<64, 1>(p, st);
-  }
-#else
   {
-    const dim3 grid((unsigned)(p.BH * p.nqt)), block(256);
+    const dim3 grid((unsigned)(p.BH * p.nqt)), b4(256), b8(512);
     switch ((D == 128 ? 10 : 0) + (int)(tile_m / 64)) {
-      case 11: hipLaunchKernelGGL((attention_dma_kernel<128, 1>), grid, block, 0, st, p); break;
-      case 12: hipLaunchKernelGGL((attention_dma_kernel<128, 2>), grid, block, 0, st, p); break;
-      case 13: hipLaunchKernelGGL((attention_dma_kernel<128, 3>), grid, block, 0, st, p); break;
-      case 14: hipLaunchKernelGGL((attention_dma_kernel<128, 4>), grid, block, 0, st, p); break;
-      case 1: hipLaunchKernelGGL((attention_dma_kernel<64, 1>), grid, block, 0, st, p); break;
-      case 2: hipLaunchKernelGGL((attention_dma_kernel<64, 2>), grid, block, 0, st, p); break;
-      case 3: hipLaunchKernelGGL((attention_dma_kernel<64, 3>), grid, block, 0, st, p); break;
-      default: hipLaunchKernelGGL((attention_dma_kernel<64, 4>), grid, block, 0, st, p); break;
+      case 11: hipLaunchKernelGGL((attention_dma_kernel<128, 1, 4>), grid, b4, 0, st, p); break;
+      case 12: hipLaunchKernelGGL((attention_dma_kernel<128, 1, 8>), grid, b8, 0, st, p); break;
+      case 13: hipLaunchKernelGGL((attention_dma_kernel<128, 3, 4>), grid, b4, 0, st, p); break;
+      case 14: hipLaunchKernelGGL((attention_dma_kernel<128, 2, 8>), grid, b8, 0, st, p); break;
+      case 1: hipLaunchKernelGGL((attention_dma_kernel<64, 1, 4>), grid, b4, 0, st, p); break;
+      case 2: hipLaunchKernelGGL((attention_dma_kernel<64, 1, 8>), grid, b8, 0, st, p); break;
+      case 3: hipLaunchKernelGGL((attention_dma_kernel<64, 3, 4>), grid, b4, 0, st, p); break;
+      default: hipLaunchKernelGGL((attention_dma_kernel<64, 2, 8>), grid, b8, 0, st, p); break;
     }
   }
-#endif
   return loom_check_launch(err, errlen, "attention");
 }
 
