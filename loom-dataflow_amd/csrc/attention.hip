@@ -163,88 +163,91 @@ __global__ void __launch_bounds__(64 * W) attention_dma_kernel(AttnParams p) {
     if (p.causal && kv0 > q0w + 16 * QT - 1) return;
     const lds_char_t* ks = stK(s);
     const lds_char_t* vs = stV(s);
-    // ---- S^T = K^T Q^T - m; st[jt][qt][i] = score of key kv0 + 16 jt + 4 g + i
-    f32x4_t st[4][QT];
-#pragma unroll
-    for (int jt = 0; jt < 4; ++jt)
-#pragma unroll
-      for (int qt = 0; qt < QT; ++qt) st[jt][qt] = f32x4_t{-m_run[qt], -m_run[qt], -m_run[qt], -m_run[qt]};
-#pragma unroll
-    for (int ds = 0; ds < DSTEPS; ++ds) {
-#pragma unroll
-      for (int jt = 0; jt < 4; ++jt) {
-        const int d = ds * 32 + g * 8 + a4;                 // & 3 == a4
-        const int ch = (2 * jt + (c4 >> 1)) ^ (2 * a4);
-        const lds_char_t* q = ks + d * (KB * 2) + ch * 16 + (c4 & 1) * 8;
-        const u32x2_t lo = lds_read_tr16(q);
-        const u32x2_t hi = lds_read_tr16(q + 4 * (KB * 2));
-        const u32x4_t kf = u32x4_t{lo[0], lo[1], hi[0], hi[1]};
-#pragma unroll
-        for (int qt = 0; qt < QT; ++qt) st[jt][qt] = mfma16(kf, qf[ds][qt], st[jt][qt]);
-      }
-    }
-    // ---- masking (only blocks that reach past Skv or the diagonal)
     const bool edge = kv0 + KB > Skv || (p.causal && kv0 + KB - 1 > q0w);
-    if (edge) {
+    // two 32-key halves, each a softmax step of its own
 #pragma unroll
-      for (int qt = 0; qt < QT; ++qt) {
-        const int qrow = q0w + 16 * qt + r;
+    for (int h = 0; h < 2; ++h) {
+      // ---- S^T = K^T Q^T - m; st[j][qt][i] = score of key kv0 + 32 h + 16 j + 4 g + i
+      f32x4_t st[2][QT];
 #pragma unroll
-        for (int jt = 0; jt < 4; ++jt)
+      for (int j = 0; j < 2; ++j)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int key = kv0 + 16 * jt + 4 * g + i;
-            if (key >= Skv || (p.causal && key > qrow)) st[jt][qt][i] = -INFINITY;
-          }
-      }
-    }
-    // ---- lazy online softmax.  P = 2^(s - m) directly while every score
-    // stays within 2^8 of the base; the first block, or a block that rises
-    // higher, moves m to the row maximum and rescales O and l (numerator and
-    // denominator share m, so the result does not depend on it)
-    float lmax[QT];
-    bool big = false;
+        for (int qt = 0; qt < QT; ++qt)
+          st[j][qt] = f32x4_t{-m_run[qt], -m_run[qt], -m_run[qt], -m_run[qt]};
 #pragma unroll
-    for (int qt = 0; qt < QT; ++qt) {
-      float mx = -INFINITY;
+      for (int ds = 0; ds < DSTEPS; ++ds) {
 #pragma unroll
-      for (int jt = 0; jt < 4; ++jt)
+        for (int j = 0; j < 2; ++j) {
+          const int jt = 2 * h + j;
+          const int d = ds * 32 + g * 8 + a4;               // & 3 == a4
+          const int ch = (2 * jt + (c4 >> 1)) ^ (2 * a4);
+          const lds_char_t* q = ks + d * (KB * 2) + ch * 16 + (c4 & 1) * 8;
+          const u32x2_t lo = lds_read_tr16(q);
+          const u32x2_t hi = lds_read_tr16(q + 4 * (KB * 2));
+          const u32x4_t kf = u32x4_t{lo[0], lo[1], hi[0], hi[1]};
 #pragma unroll
-        for (int i = 0; i < 4; ++i) mx = fmaxf(mx, st[jt][qt][i]);
-      lmax[qt] = mx;
-      big |= mx > 8.f;
-    }
-    const bool first = blk == 0;
-    if (first || __builtin_amdgcn_ballot_w64(big) != 0) {
-#pragma unroll
-      for (int qt = 0; qt < QT; ++qt) {
-        float mx = lmax[qt];
-        mx = fmaxf(mx, __shfl_xor(mx, 16));
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        // the first block sets m (O and l are still zero); later ones only raise it
-        const float shift = first ? (mx == -INFINITY ? 0.f : mx) : fmaxf(mx, 0.f);
-        if (!first) {
-          const float alpha = fast_exp2(-shift);
-          lacc[qt] *= alpha;
-#pragma unroll
-          for (int dt = 0; dt < DT; ++dt) ot[dt][qt] *= alpha;
+          for (int qt = 0; qt < QT; ++qt) st[j][qt] = mfma16(kf, qf[ds][qt], st[j][qt]);
         }
-        m_run[qt] += shift;
-#pragma unroll
-        for (int jt = 0; jt < 4; ++jt) st[jt][qt] -= shift;
       }
-    }
-    // ---- O^T += V^T P^T and l += ones . P^T, 32 keys (tiles 2 pp, 2 pp + 1) per step
+      // ---- masking (only blocks that reach past Skv or the diagonal)
+      if (edge) {
 #pragma unroll
-    for (int pp = 0; pp < 2; ++pp) {
+        for (int qt = 0; qt < QT; ++qt) {
+          const int qrow = q0w + 16 * qt + r;
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int key = kv0 + 32 * h + 16 * j + 4 * g + i;
+              if (key >= Skv || (p.causal && key > qrow)) st[j][qt][i] = -INFINITY;
+            }
+        }
+      }
+      // ---- lazy online softmax.  P = 2^(s - m) directly while every score
+      // stays within 2^8 of the base; the first step, or a step that rises
+      // higher, moves m to the row maximum and rescales O and l (numerator
+      // and denominator share m, so the result does not depend on it)
+      float lmax[QT];
+      bool big = false;
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) mx = fmaxf(mx, st[j][qt][i]);
+        lmax[qt] = mx;
+        big |= mx > 8.f;
+      }
+      const bool first = blk == 0 && h == 0;
+      if (first || __builtin_amdgcn_ballot_w64(big) != 0) {
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) {
+          float mx = lmax[qt];
+          mx = fmaxf(mx, __shfl_xor(mx, 16));
+          mx = fmaxf(mx, __shfl_xor(mx, 32));
+          // the first step sets m (O and l are still zero); later ones only raise it
+          const float shift = first ? (mx == -INFINITY ? 0.f : mx) : fmaxf(mx, 0.f);
+          if (!first) {
+            const float alpha = fast_exp2(-shift);
+            lacc[qt] *= alpha;
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) ot[dt][qt] *= alpha;
+          }
+          m_run[qt] += shift;
+#pragma unroll
+          for (int j = 0; j < 2; ++j) st[j][qt] -= shift;
+        }
+      }
+      // ---- O^T += V^T P^T and l += ones . P^T over these 32 keys
       u32x4_t pf[QT];
 #pragma unroll
       for (int qt = 0; qt < QT; ++qt) {
         f32x4_t e0, e1;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          e0[i] = fast_exp2(st[2 * pp][qt][i]);
-          e1[i] = fast_exp2(st[2 * pp + 1][qt][i]);
+          e0[i] = fast_exp2(st[0][qt][i]);
+          e1[i] = fast_exp2(st[1][qt][i]);
         }
         pf[qt] = u32x4_t{pack_bf16x2(e0[0], e0[1]), pack_bf16x2(e0[2], e0[3]),
                          pack_bf16x2(e1[0], e1[1]), pack_bf16x2(e1[2], e1[3])};
@@ -253,10 +256,10 @@ __global__ void __launch_bounds__(64 * W) attention_dma_kernel(AttnParams p) {
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
         const int ch = (2 * dt + (c4 >> 1)) ^ (2 * a4);
-        const int k0r = 32 * pp + 4 * g + a4;               // & 3 == a4
+        const int k0r = 32 * h + 4 * g + a4;                // & 3 == a4
         const lds_char_t* q = vs + k0r * VROW + ch * 16 + (c4 & 1) * 8;
-        const u32x2_t lo = lds_read_tr16(q);                // keys 32pp + 4g + 0..3
-        const u32x2_t hi = lds_read_tr16(q + 16 * VROW);    // keys 32pp + 16 + 4g + 0..3
+        const u32x2_t lo = lds_read_tr16(q);                // keys 32h + 4g + 0..3
+        const u32x2_t hi = lds_read_tr16(q + 16 * VROW);    // keys 32h + 16 + 4g + 0..3
         const u32x4_t vf = u32x4_t{lo[0], lo[1], hi[0], hi[1]};
 #pragma unroll
         for (int qt = 0; qt < QT; ++qt) ot[dt][qt] = mfma16(vf, pf[qt], ot[dt][qt]);

@@ -198,6 +198,8 @@ LOOM_DEV u32x2_t lds_read_tr16(const lds_char_t* p) {
 // s_waitcnt vmcnt(n), leaving LDS and export counters alone
 #define LOOM_WAIT_VMCNT(n) \
   __builtin_amdgcn_s_waitcnt(((n) & 15) | ((((n) >> 4) & 3) << 14) | 0x0F70)
+// s_waitcnt lgkmcnt(0): this wave's LDS reads and writes have completed
+#define LOOM_WAIT_LGKM0() __builtin_amdgcn_s_waitcnt(0xC07F)
 
 // Workgroup barrier without the memory fence __syncthreads() adds (the fence
 // would force every outstanding load, LDS DMA included, to complete).  The
