@@ -141,6 +141,46 @@ int loom_hip_helion_mamba2_chunk_scan_kernel(
     int64_t tile_b, int64_t tile_h, int64_t tile_c, int64_t tile_m, int64_t tile_n,
     int64_t tile_k, void* stream, char* err, size_t errlen);
 
+/* ---- Mamba-2 SSD prologue --------------------------------------------------
+ * The chunk-scan example takes cb, dA_cumsum and prev_states_T ready-made
+ * (examples/mamba_chunk_scan/IR/00_from_helion_frontend.mlir:4); the
+ * reference repository has no code that produces them.  These entry points
+ * compute them on the GPU from raw Mamba-2 inputs, following the chunked SSD
+ * algorithm (Dao & Gu 2024): x [b,H,L,P] bf16, dt [b,H,L] fp32 (after
+ * softplus; the same memory as chunk_scan's dt [b,H,c,Q]), A [H] fp32,
+ * B and C [b,G,L,N] bf16, L = nchunks * chunk_size, head h reads group
+ * h / (H / G).  chunk_size, headdim and dstate are multiples of 16,
+ * chunk_size <= 256, headdim <= 256, dstate <= 128 (a multiple of 32 above
+ * 32; of 64 above 64 when headdim <= 128), and
+ * ceil32(chunk_size) * headdim * 2 <= 64 KiB. */
+
+/* dA_cumsum[b,h,c,q] = sum_{q' <= q} dt[b,h,c*Q+q'] * A[h] (fp32; a wave
+ * prefix scan, so the summation order differs from a serial loop). */
+int loom_hip_ssd_chunk_cumsum(const void* dt, const void* A, void* dA_cumsum, int64_t batch,
+                              int64_t nchunks, int64_t nheads, int64_t chunk_size, void* stream,
+                              char* err, size_t errlen);
+
+/* cb[b,c,g,i,j] = bf16(sum_n C[b,g,cQ+i,n] B[b,g,cQ+j,n]) for j <= i, else 0. */
+int loom_hip_ssd_bmm_chunk(const void* B, const void* C, void* cb, int64_t batch, int64_t nchunks,
+                           int64_t ngroups, int64_t chunk_size, int64_t dstate, void* stream,
+                           char* err, size_t errlen);
+
+/* prev_states_T [b,c,H,N,P] fp32: zero for c = 0, then
+ * prev(c) = exp(dA[c-1,Q-1]) prev(c-1) + sum_k B[k,n] exp(dA[c-1,Q-1] - dA[c-1,k]) dt[c-1,k] x[k,p]
+ * over the keys k of chunk c-1 (chunk states and state passing fused). */
+int loom_hip_ssd_chunk_state_passing(const void* x, const void* dt, const void* dA_cumsum,
+                                     const void* B, void* prev_states_T, int64_t batch,
+                                     int64_t nchunks, int64_t nheads, int64_t ngroups,
+                                     int64_t chunk_size, int64_t headdim, int64_t dstate,
+                                     void* stream, char* err, size_t errlen);
+
+/* All three stages in stream order: dA_cumsum, cb, prev_states_T. */
+int loom_hip_ssd_prologue(const void* x, const void* dt, const void* A, const void* B,
+                          const void* C, void* dA_cumsum, void* cb, void* prev_states_T,
+                          int64_t batch, int64_t nchunks, int64_t nheads, int64_t ngroups,
+                          int64_t chunk_size, int64_t headdim, int64_t dstate, void* stream,
+                          char* err, size_t errlen);
+
 /* ---- materialization contract and by-name dispatch ---------------------- */
 
 /* Variant names the materialization pipeline emits for `funcs` under the

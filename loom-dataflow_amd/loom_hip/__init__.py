@@ -44,6 +44,10 @@ _SIGS = {
     "loom_hip_flash_decode": [_vp] * 5 + [_sz] + [_i64] * 4 + [_f32] + [_i64] * 3
     + [_vp, *_ERR],
     "loom_hip_helion_mamba2_chunk_scan_kernel": [_vp] * 8 + [_i64] * 13 + [_vp, *_ERR],
+    "loom_hip_ssd_chunk_cumsum": [_vp] * 3 + [_i64] * 4 + [_vp, *_ERR],
+    "loom_hip_ssd_bmm_chunk": [_vp] * 3 + [_i64] * 5 + [_vp, *_ERR],
+    "loom_hip_ssd_chunk_state_passing": [_vp] * 5 + [_i64] * 7 + [_vp, *_ERR],
+    "loom_hip_ssd_prologue": [_vp] * 8 + [_i64] * 7 + [_vp, *_ERR],
 }
 for _name, _args in _SIGS.items():
     _fn = getattr(_lib, _name)
@@ -256,6 +260,36 @@ def helion_mamba2_chunk_scan_kernel(cb, x, dt, dA_cumsum, C, D, prev_states_T, o
           tile_m, tile_n, tile_k, _stream(x))
     return out
 
+
+# ---------------------------------------------------------------------------
+# Mamba-2 SSD prologue (raw x, dt, A, B, C -> chunk_scan's inputs)
+# ---------------------------------------------------------------------------
+
+def ssd_prologue(x, dt, A, B, C, chunk_size, *, dA_cumsum=None, cb=None, prev_states_T=None):
+    """x [b,H,L,P] bf16, dt [b,H,L] fp32 (post-softplus), A [H] fp32,
+    B, C [b,G,L,N] bf16 -> (dt [b,H,c,Q] (a view of dt), dA_cumsum [b,H,c,Q],
+    cb [b,c,G,Q,Q] bf16, prev_states_T [b,c,H,N,P] fp32)."""
+    b, H, L, P = x.shape
+    G, N = B.shape[1], B.shape[3]
+    Q = int(chunk_size)
+    if L % Q:
+        raise ValueError("ssd_prologue: L must be a multiple of chunk_size")
+    nc = L // Q
+    if tuple(dt.shape) != (b, H, L) or tuple(A.shape) != (H,) or tuple(B.shape) != (b, G, L, N) \
+            or tuple(C.shape) != (b, G, L, N):
+        raise ValueError("ssd_prologue: argument shapes disagree")
+    dev = x.device
+    if dA_cumsum is None:
+        dA_cumsum = torch.empty((b, H, nc, Q), dtype=_fp32, device=dev)
+    if cb is None:
+        cb = torch.empty((b, nc, G, Q, Q), dtype=_bf16, device=dev)
+    if prev_states_T is None:
+        prev_states_T = torch.empty((b, nc, H, N, P), dtype=_fp32, device=dev)
+    _call("loom_hip_ssd_prologue", _need(x, "x", _bf16, 4), _need(dt, "dt", _fp32, 3),
+          _need(A, "A", _fp32, 1), _need(B, "B", _bf16, 4), _need(C, "C", _bf16, 4),
+          _need(dA_cumsum, "dA_cumsum", _fp32, 4), _need(cb, "cb", _bf16, 5),
+          _need(prev_states_T, "prev_states_T", _fp32, 5), b, nc, H, G, Q, P, N, _stream(x))
+    return dt.view(b, H, nc, Q), dA_cumsum, cb, prev_states_T
 
 # ---------------------------------------------------------------------------
 # materialization contract and by-name dispatch

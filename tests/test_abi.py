@@ -116,3 +116,20 @@ def test_mamba_rejections(lh):
     rc, msg = _call(lh, "loom_hip_helion_mamba2_chunk_scan_kernel", *([FAKE] * 8),
                     1, 2, 6, 4, 64, 64, 128, 1, 1, 1, 64, 64, 64, None)
     assert rc == 1 and "ngroups" in msg
+
+
+def test_ssd_rejections(lh):
+    # x, dt, A, B, C, dA_cumsum, cb, prev_states_T | b, c, H, G, Q, P, N
+    rc, msg = _call(lh, "loom_hip_ssd_prologue", *([FAKE] * 8), 1, 2, 6, 4, 64, 64, 128, None)
+    assert rc == 1 and "ngroups" in msg
+    rc, msg = _call(lh, "loom_hip_ssd_prologue", *([FAKE] * 8), 1, 2, 4, 1, 8, 64, 128, None)
+    assert rc == 2 and "multiples of 16" in msg
+    rc, msg = _call(lh, "loom_hip_ssd_prologue", *([FAKE] * 8), 1, 2, 4, 1, 512, 64, 128, None)
+    assert rc == 2 and "chunk_size <= 256" in msg
+    rc, msg = _call(lh, "loom_hip_ssd_prologue", *([FAKE] * 8), 1, 2, 4, 1, 256, 160, 128, None)
+    assert rc == 2 and "LDS" in msg
+    rc, msg = _call(lh, "loom_hip_ssd_chunk_state_passing", None, *([FAKE] * 4),
+                    1, 2, 4, 1, 64, 64, 128, None)
+    assert rc == 1 and "null" in msg
+    rc, msg = _call(lh, "loom_hip_ssd_chunk_cumsum", FAKE, FAKE, FAKE, 1, 2, 4, 1024, None)
+    assert rc == 2 and "512" in msg

@@ -1,0 +1,109 @@
+"""GPU parity of the Mamba-2 SSD prologue (raw x, dt, A, B, C -> dA_cumsum,
+cb, prev_states_T) against the CPU oracle's mamba_prologue, and the whole
+chain (GPU prologue -> GPU chunk scan) against the sequential SSM
+recurrence of the golden fixture.
+
+Tolerances: dA_cumsum is an fp32 prefix sum in another association than the
+oracle's serial loop: |d| <= 1e-5 (1 + |ref|).  cb is an fp32 MFMA sum
+rounded to bf16: at most one bf16 rounding step apart, |d| <= 2^-7 |ref| +
+1e-5, and exactly zero above the diagonal.  prev_states_T accumulates in fp32 with w * B split into bf16 hi + lo
+(relative error ~2^-16 per term): |d| <= 1e-3 (|ref| + scale), scale = the
+tensor's largest magnitude times 1e-2.  The chain keeps the chunk-scan
+bar (2e-2 + 1e-2 |ref|; 3e-2 against the recurrence).
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from oracle import from_bf16
+from tests.conftest import assert_close
+from tests.test_gpu_parity import ATTN_TOL, dev, devf, host, rng_bf16
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def lh():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import loom_hip
+    return loom_hip
+
+
+def _raw_inputs(rng, b, H, G, L, P, N, dt_scale=1.0):
+    x = rng_bf16(rng, (b, H, L, P))
+    Bm = rng_bf16(rng, (b, G, L, N))
+    C = rng_bf16(rng, (b, G, L, N))
+    dt = (np.log1p(np.exp(rng.standard_normal((b, H, L)))) * dt_scale).astype(np.float32)
+    A = (-np.exp(rng.uniform(0, 1, H))).astype(np.float32)
+    return x, dt, A, Bm, C
+
+
+def _check_prologue(lh, x, dt, A, Bm, C, Q, what):
+    dt_v, dA, cb, prev = lh.ssd_prologue(dev(x), devf(dt), devf(A), dev(Bm), dev(C), Q)
+    torch.cuda.synchronize()
+    dt_o, dA_o, cb_o, prev_o = oracle.mamba_prologue(x, dt, A, Bm, C, Q)
+    np.testing.assert_array_equal(dt_v.cpu().numpy(), dt_o)
+    dA_g = dA.cpu().numpy()
+    assert np.all(np.abs(dA_g - dA_o) <= 1e-5 * (1 + np.abs(dA_o))), f"{what}: dA_cumsum"
+    cb_g, cb_r = from_bf16(host(cb)), from_bf16(cb_o)
+    bad = np.abs(cb_g - cb_r) > 2.0 ** -7 * np.abs(cb_r) + 1e-5
+    assert not bad.any(), (f"{what}: cb {int(bad.sum())} of {bad.size} beyond one bf16 step, max "
+                           f"err {float(np.abs(cb_g - cb_r).max()):.3e}")
+    # the masked upper triangle is exactly zero
+    Qn = cb_r.shape[-1]
+    assert not np.any(cb_g[..., np.triu_indices(Qn, 1)[0], np.triu_indices(Qn, 1)[1]])
+    prev_g = prev.cpu().numpy()
+    scale = 1e-2 * max(float(np.abs(prev_o).max()), 1e-30)
+    bad = np.abs(prev_g - prev_o) > 1e-3 * (np.abs(prev_o) + scale)
+    assert not bad.any(), (f"{what}: prev_states_T {int(bad.sum())} of {bad.size} off, max err "
+                           f"{float(np.abs(prev_g - prev_o).max()):.3e}")
+    return dt_v, dA, cb, prev
+
+
+def test_golden_chain_against_recurrence(lh, golden):
+    g = golden("mamba_small")
+    Q = int(g["chunk_size"])
+    dt_v, dA, cb, prev = _check_prologue(lh, g["x"], g["dt"], g["A"], g["B"], g["C"], Q, "golden")
+    out = lh.helion_mamba2_chunk_scan_kernel(cb, dev(g["x"]), dt_v.contiguous(), dA, dev(g["C"]),
+                                             devf(g["D"]), prev, tile_m=64, tile_n=16)
+    assert_close(from_bf16(host(out)), g["expected"], atol=3e-2, rtol=1e-2,
+                 what="GPU prologue + chunk scan vs recurrence")
+
+
+def test_baseline_chunk_shape(lh):
+    """BASELINE per-chunk shape: Q256, P64, N128, G1 (b1, 8 heads, 8 chunks)."""
+    rng = np.random.default_rng(41)
+    x, dt, A, Bm, C = _raw_inputs(rng, 1, 8, 1, 8 * 256, 64, 128)
+    dt_v, dA, cb, prev = _check_prologue(lh, x, dt, A, Bm, C, 256, "baseline shape")
+    # and the chain into the chunk scan, against the oracle's own chain
+    D = rng.standard_normal(8).astype(np.float32)
+    out = lh.helion_mamba2_chunk_scan_kernel(cb, dev(x), dt_v.contiguous(), dA, dev(C), devf(D),
+                                             prev, tile_m=256, tile_n=64)
+    _, dA_o, cb_o, prev_o = oracle.mamba_prologue(x, dt, A, Bm, C, 256)
+    ref = oracle.mamba_chunk_scan(cb_o, x, dt.reshape(1, 8, 8, 256), dA_o, C, D, prev_o, 64, 64, 64)
+    assert_close(from_bf16(host(out)), from_bf16(ref), **ATTN_TOL, what="baseline chain")
+
+
+def test_reference_example_shape(lh):
+    """The reference example's geometry: Q192, P160, N128, 4 groups (h/8)."""
+    rng = np.random.default_rng(42)
+    x, dt, A, Bm, C = _raw_inputs(rng, 1, 32, 4, 2 * 192, 160, 128)
+    _check_prologue(lh, x, dt, A, Bm, C, 192, "reference shape")
+
+
+def test_ragged_chunk_and_narrow_state(lh):
+    """Q = 48 (zero-filled to the 32-deep MFMA step), N = 32, P = 32, G = 2."""
+    rng = np.random.default_rng(43)
+    x, dt, A, Bm, C = _raw_inputs(rng, 2, 4, 2, 3 * 48, 32, 32)
+    _check_prologue(lh, x, dt, A, Bm, C, 48, "ragged")
+
+
+def test_zero_B_gives_zero_states(lh):
+    rng = np.random.default_rng(44)
+    x, dt, A, Bm, C = _raw_inputs(rng, 1, 2, 1, 4 * 64, 32, 64)
+    Bm[:] = 0
+    _, _, cb, prev = lh.ssd_prologue(dev(x), devf(dt), devf(A), dev(Bm), dev(C), 64)
+    assert not torch.any(cb.view(torch.int16) != 0)
+    assert not torch.any(prev != 0)
