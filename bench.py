@@ -141,9 +141,9 @@ def make_cases(torch, lh):
         n = min(2, copies(nb))
         sets = [(randn(BH, D, S), randn(BH, S, D), randn(BH, S, D),
                  torch.empty(BH, S, D, dtype=bf, device=cuda)) for _ in range(n)]
-        return dict(fn=lambda i: lh.attention(*sets[i % n], causal=True, tile_m=192, tile_n=64),
+        return dict(fn=lambda i: lh.attention(*sets[i % n], causal=True, tile_m=256, tile_n=64),
                     flop=4 * BH * S * S * D // 2, bytes=nb, bound="mfma", sets=n,
-                    desc="flashattn fwd B4 H32 S4096 D128 causal, tile_m 192")
+                    desc="flashattn fwd B4 H32 S4096 D128 causal, tile_m 256")
     cases["flashattn"] = flashattn
 
     def decode():
@@ -183,6 +183,33 @@ def make_cases(torch, lh):
             flop=flop, bytes=nb, bound="hbm", sets=n,
             desc="mamba chunk_scan b4 L4096 h32 P64 N128 g1 Q256")
     cases["mamba_chunk_scan"] = mamba
+
+    def ssd():
+        b, L, H, P, N, Q = 4, 4096, 32, 64, 128, 256
+        nc = L // Q
+
+        def one():
+            x = randn(b, H, L, P)
+            Bm, C = randn(b, 1, L, N), randn(b, 1, L, N)
+            dt = torch.nn.functional.softplus(torch.randn(b, H, L, generator=g, device=cuda))
+            A = -torch.exp(torch.rand(H, generator=g, device=cuda))
+            dA = torch.empty(b, H, nc, Q, dtype=torch.float32, device=cuda)
+            cb = torch.empty(b, nc, 1, Q, Q, dtype=bf, device=cuda)
+            prev = torch.empty(b, nc, H, N, P, dtype=torch.float32, device=cuda)
+            return (x, dt, A, Bm, C, dA, cb, prev)
+        first = one()
+        nb = sum(t.numel() * t.element_size() for t in first)
+        n = copies(nb)
+        sets = [first] + [one() for _ in range(n - 1)]
+
+        def fn(i):
+            x, dt, A, Bm, C, dA, cb, prev = sets[i % n]
+            lh.ssd_prologue(x, dt, A, Bm, C, Q, dA_cumsum=dA, cb=cb, prev_states_T=prev)
+        flop = b * nc * Q * Q * N + 2 * b * H * L * N * P
+        return dict(fn=fn, flop=flop, bytes=nb, bound="hbm", sets=n,
+                    desc="mamba SSD prologue (cumsum, cb, states + passing) b4 L4096 h32 P64 "
+                         "N128 g1 Q256")
+    cases["mamba_prologue"] = ssd
     return cases
 
 

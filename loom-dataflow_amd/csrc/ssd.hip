@@ -128,141 +128,224 @@ __global__ void __launch_bounds__(64) ssd_cb_kernel(const uint16_t* __restrict__
 // chunk states + state passing -> prev_states_T
 // ---------------------------------------------------------------------------
 constexpr int kSsdQmax = 256, kSsdPmax = 256, kSsdNB = 64, kSsdWaves = 8;
-constexpr int kSsdXBytes = 64 * 1024;        // x chunk [Qpad][P] bf16 at most
+constexpr int kSsdStageMax = 36 * 1024;      // bytes per pipeline stage
+constexpr int kSsdRing = 4 * kSsdStageMax;   // LDS for the stage ring
+constexpr int kSsdNSMax = 8;                 // stages at most
 
-template <int TPW>
-__global__ void __launch_bounds__(64 * kSsdWaves) ssd_state_kernel(
-    const uint16_t* __restrict__ x, const float* __restrict__ dt, const float* __restrict__ dA,
-    const uint16_t* __restrict__ Bm, float* __restrict__ prevT, int H, int G, int nc, int Q,
-    int P, int N, int nb) {
-  // LDS: x chunk [Qpad][P], B chunk [Qpad][nb] (bf16), w [Qpad]
-  __shared__ __attribute__((aligned(16))) uint16_t s_x[kSsdXBytes / 2];
-  __shared__ __attribute__((aligned(16))) uint16_t s_b[kSsdQmax * kSsdNB];
-  __shared__ __attribute__((aligned(16))) float s_w[kSsdQmax];
+// A chunk is processed in units of QS keys (QS divides Q; a chunk whose Q
+// is not a multiple of 32 is one unit zero-weighted up to QSP rows).  Unit u
+// lives in LDS stage u % NS: x rows [QSP][P] | B rows [QSP][nb] | dA, dt
+// (QSP floats each, 1 KB) | dA[c, Q-4 .. Q-1] of the unit's chunk (1 KB slot).
+struct SsdStateParams {
+  const uint16_t* x;
+  const float* dt;
+  const float* dA;
+  const uint16_t* B;
+  float* prevT;
+  int H, G, nc, Q, P, N, nb;
+  int QS, QSP, upc;          // keys per unit, LDS rows per unit, units per chunk
+  int xbytes, bbytes;        // per stage
+  int ninstr, lpw;           // DMA instructions per unit, per wave (padded)
+  int ns;                    // stages in the ring (3 .. 8)
+};
 
+// SHARED_PT: P / 16 divides the wave count, so all tiles of a wave share
+// one p tile and the w-scaled x operand is built once per k step.
+template <int TPW, bool SHARED_PT>
+__global__ void __launch_bounds__(64 * kSsdWaves) ssd_state_kernel(SsdStateParams p) {
+  __shared__ __attribute__((aligned(1024))) char smem[kSsdRing + 1024];
+  __shared__ __attribute__((aligned(16))) float s_w[2][128];  // w of units u, u+1 (by parity)
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = lane & 15, gq = lane >> 4, a4 = r >> 2, c4 = r & 3;
   const int bh = blockIdx.x, nblk = blockIdx.y;
-  const int b = bh / H, h = bh % H, g = h / (H / G);
+  const int H = p.H, Q = p.Q, P = p.P, N = p.N, nb = p.nb, nc = p.nc;
+  const int b = bh / H, h = bh % H, g = h / (H / p.G);
   const int n0 = nblk * nb;
-  const int L = nc * Q, Qpad = (Q + 31) & ~31;
-  const int XR = P * 2, BR = nb * 2;           // LDS row bytes
-  const int ptiles = P / 16, ntiles = nb / 16, tiles = ptiles * ntiles;
+  const int L = nc * Q;
+  const int XR = P * 2, BR = nb * 2;
+  const int stage_bytes = p.xbytes + p.bbytes + 2048;
+  const int xinstr = p.xbytes / 1024, binstr = p.bbytes / 1024;
+  const int ptiles = P / 16, tiles = ptiles * (nb / 16);
+  const int QS = p.QS, QSP = p.QSP, upc = p.upc, nu = nc * upc;
 
-  const uint16_t* xg = x + ((int64_t)bh * L) * P;
-  const uint16_t* bg = Bm + ((int64_t)(b * G + g) * L) * N + n0;
-  const float* dAg = dA + (int64_t)bh * nc * Q;
-  const float* dtg = dt + (int64_t)bh * nc * Q;
+  const uint16_t* xg = p.x + (int64_t)bh * L * P;
+  const uint16_t* bgp = p.B + (int64_t)(b * p.G + g) * L * N + n0;
+  const float* dAg = p.dA + (int64_t)bh * nc * Q;
+  const float* dtg = p.dt + (int64_t)bh * nc * Q;
+  lds_char_t* const sm = (lds_char_t*)smem;
+  const uint32_t scratch = lds_addr(sm + kSsdRing);
+  const int NS = p.ns;
 
-  // staging: x rows (P*2 bytes) and B rows (nb*2 bytes) of chunk c, 16 bytes a piece
-  const int xpieces = Qpad * P / 8, bpieces = Qpad * nb / 8;
-  constexpr int kMaxPieces = (kSsdXBytes / 16 + kSsdQmax * kSsdNB / 8) / (64 * kSsdWaves);
-  u32x4_t pre[kMaxPieces];
-  float wpre = 0.f;
-  auto load_chunk = [&](int c) {
-#pragma unroll
-    for (int u = 0; u < kMaxPieces; ++u) {
-      const int idx = tid + u * 64 * kSsdWaves;
-      u32x4_t v = u32x4_t{0u, 0u, 0u, 0u};
-      if (idx < xpieces) {
-        const int k = idx / (P / 8), pc = idx % (P / 8);
-        if (k < Q) v = *reinterpret_cast<const u32x4_t*>(xg + ((int64_t)c * Q + k) * P + pc * 8);
-      } else if (idx < xpieces + bpieces) {
-        const int j = idx - xpieces;
-        const int k = j / (nb / 8), nc8 = j % (nb / 8);
-        if (k < Q) v = *reinterpret_cast<const u32x4_t*>(bg + ((int64_t)c * Q + k) * N + nc8 * 8);
+  // ---- DMA of unit u into stage s; rows past the unit's keys are clamped
+  // (their weight is forced to zero)
+  auto issue = [&](int s, int u) {
+    const int c = u / upc, ko = (u % upc) * QS;
+    const int64_t key0 = (int64_t)c * Q + ko;   // first key of the unit within (b, h)
+    const uint32_t base = lds_addr(sm + s * stage_bytes);
+    for (int i = 0; i < p.lpw; ++i) {
+      const int j = wave + kSsdWaves * i;
+      if (j < xinstr) {
+        const int e = (j * 64 + lane) * 8;        // element offset in the [QSP][P] unit
+        const int k = min(e / P, QS - 1), col = e % P;
+        dma_load16(xg + (key0 + k) * P + col, base + j * 1024);
+      } else if (j < xinstr + binstr) {
+        const int idx = (j - xinstr) * 64 + lane;
+        const int k = min(idx / (nb / 8), QS - 1), col = (idx % (nb / 8)) * 8;
+        dma_load16(bgp + (key0 + k) * N + col, base + p.xbytes + (j - xinstr) * 1024);
+      } else if (j == xinstr + binstr) {
+        const int half = lane >> 5, k = min(4 * (lane & 31), QS - 4);
+        dma_load16((half ? dtg : dAg) + key0 + k, base + p.xbytes + p.bbytes);
+      } else if (j == xinstr + binstr + 1) {
+        dma_load16(dAg + (int64_t)c * Q + Q - 4, base + p.xbytes + p.bbytes + 1024);
+      } else {
+        dma_load16(xg, scratch);                  // padding: every wave issues lpw copies
       }
-      pre[u] = v;
-    }
-    wpre = 0.f;
-    if (tid < Q) {
-      const float last = dAg[(int64_t)c * Q + Q - 1];
-      wpre = expf(last - dAg[(int64_t)c * Q + tid]) * dtg[(int64_t)c * Q + tid];
     }
   };
-  auto store_chunk = [&]() {
-#pragma unroll
-    for (int u = 0; u < kMaxPieces; ++u) {
-      const int idx = tid + u * 64 * kSsdWaves;
-      if (idx < xpieces)
-        *reinterpret_cast<u32x4_t*>(&s_x[idx * 8]) = pre[u];
-      else if (idx < xpieces + bpieces)
-        *reinterpret_cast<u32x4_t*>(&s_b[(idx - xpieces) * 8]) = pre[u];
+  auto wait_units = [&](int younger, int stores) {
+    const int n = younger * p.lpw + stores;
+    switch (n) {
+      case 0: LOOM_WAIT_VMCNT(0); break;
+      case 1: LOOM_WAIT_VMCNT(1); break;
+      case 2: LOOM_WAIT_VMCNT(2); break;
+      case 3: LOOM_WAIT_VMCNT(3); break;
+      case 4: LOOM_WAIT_VMCNT(4); break;
+      case 5: LOOM_WAIT_VMCNT(5); break;
+      case 6: LOOM_WAIT_VMCNT(6); break;
+      case 7: LOOM_WAIT_VMCNT(7); break;
+      case 8: LOOM_WAIT_VMCNT(8); break;
+      case 9: LOOM_WAIT_VMCNT(9); break;
+      case 10: LOOM_WAIT_VMCNT(10); break;
+      case 11: LOOM_WAIT_VMCNT(11); break;
+      case 12: LOOM_WAIT_VMCNT(12); break;
+      case 13: LOOM_WAIT_VMCNT(13); break;
+      case 14: LOOM_WAIT_VMCNT(14); break;
+      case 15: LOOM_WAIT_VMCNT(15); break;
+      case 16: LOOM_WAIT_VMCNT(16); break;
+      case 17: LOOM_WAIT_VMCNT(17); break;
+      case 18: LOOM_WAIT_VMCNT(18); break;
+      case 19: LOOM_WAIT_VMCNT(19); break;
+      case 20: LOOM_WAIT_VMCNT(20); break;
+      case 21: LOOM_WAIT_VMCNT(21); break;
+      case 22: LOOM_WAIT_VMCNT(22); break;
+      case 23: LOOM_WAIT_VMCNT(23); break;
+      default: LOOM_WAIT_VMCNT(24); break;
     }
-    if (tid < Qpad) s_w[tid] = wpre;
   };
 
   // running prev_states^T tiles: tile t = wave + 8 u -> (pt, nt); lane holds
   // prev[n0 + 16 nt + r][16 pt + 4 gq + e]
   f32x4_t R[TPW];
 #pragma unroll
-  for (int u = 0; u < TPW; ++u) R[u] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-
-  load_chunk(0);
-  store_chunk();
-  __syncthreads();
-  for (int c = 0; c < nc; ++c) {
-    if (c + 1 < nc) load_chunk(c + 1);         // in flight during this chunk's MFMAs
-    // prev(c), then R = exp(dA[c, Q-1]) R + states(c)
-    const float decay = expf(dAg[(int64_t)c * Q + Q - 1]);
-    float* outc = prevT + (((int64_t)(b * nc + c) * H + h) * N + n0) * P;
-#pragma unroll
-    for (int u = 0; u < TPW; ++u) {
-      const int t = wave + kSsdWaves * u;
-      if (t < tiles) {
-        const int pt = t % ptiles, nt = t / ptiles;
-        *reinterpret_cast<f32x4_t*>(outc + (int64_t)(16 * nt + r) * P + 16 * pt + 4 * gq) = R[u];
-        R[u] *= decay;
-      }
+  for (int t = 0; t < TPW; ++t) R[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  // ---- w_c[k] = exp(dA[c, Q-1] - dA[c, k]) dt[c, k] of unit u (stage s)
+  // into s_w[u & 1], one key per thread; zero past the unit's keys
+  auto make_w = [&](int s, int u) {
+    const int ko = (u % upc) * QS;
+    if (tid < QSP) {
+      const float* dAs = reinterpret_cast<const float*>(smem + s * stage_bytes + p.xbytes + p.bbytes);
+      const float last = dAs[256 + 3];
+      float w = 0.f;
+      if (tid < QS && ko + tid < Q)
+        w = fast_exp2((last - dAs[tid]) * 1.4426950408889634f) * dAs[128 + tid];
+      s_w[u & 1][tid] = w;
     }
-    const char* xs = reinterpret_cast<const char*>(s_x);
-    const char* bs = reinterpret_cast<const char*>(s_b);
-    for (int ks = 0; ks < Qpad / 32; ++ks) {
-      const int k0 = 32 * ks + 4 * gq;          // rows k0 + a4 (lo) and + 16 (hi)
-      const f32x4_t w0 = *reinterpret_cast<const f32x4_t*>(&s_w[k0]);
-      const f32x4_t w1 = *reinterpret_cast<const f32x4_t*>(&s_w[k0 + 16]);
+  };
+
+  // x^T operand of p tile pt at k step ks, scaled by w and split into
+  // bf16 hi + lo (the products keep ~16 significant bits)
+  auto x_operand = [&](const lds_char_t* xs, const float* wv, int pt, int k0, u32x4_t& vh,
+                       u32x4_t& vl) {
+    const lds_char_t* qx = xs + (k0 + a4) * XR + (2 * pt + (c4 >> 1)) * 16 + (c4 & 1) * 8;
+    const u32x2_t xlo = lds_read_tr16(qx), xhi = lds_read_tr16(qx + 16 * XR);
+    const f32x4_t w0 = *reinterpret_cast<const f32x4_t*>(wv + k0);
+    const f32x4_t w1 = *reinterpret_cast<const f32x4_t*>(wv + k0 + 16);
+    const float v[8] = {bf2f_lo(xlo[0]) * w0[0], bf2f_hi(xlo[0]) * w0[1],
+                        bf2f_lo(xlo[1]) * w0[2], bf2f_hi(xlo[1]) * w0[3],
+                        bf2f_lo(xhi[0]) * w1[0], bf2f_hi(xhi[0]) * w1[1],
+                        bf2f_lo(xhi[1]) * w1[2], bf2f_hi(xhi[1]) * w1[3]};
 #pragma unroll
-      for (int u = 0; u < TPW; ++u) {
-        const int t = wave + kSsdWaves * u;
-        if (t < tiles) {
-          const int pt = t % ptiles, nt = t / ptiles;
-          // x^T operand: p = 16 pt + r, k in {k0..k0+3, k0+16..k0+19}
-          const lds_char_t* qx = (const lds_char_t*)(xs + (k0 + a4) * XR + (2 * pt + (c4 >> 1)) * 16 + (c4 & 1) * 8);
-          const u32x2_t xlo = lds_read_tr16(qx), xhi = lds_read_tr16(qx + 16 * XR);
-          const u32x4_t xf = u32x4_t{xlo[0], xlo[1], xhi[0], xhi[1]};
-          // (w B) operand: n = 16 nt + r, same k
-          const lds_char_t* qb = (const lds_char_t*)(bs + (k0 + a4) * BR + (2 * nt + (c4 >> 1)) * 16 + (c4 & 1) * 8);
-          const u32x2_t blo = lds_read_tr16(qb), bhi = lds_read_tr16(qb + 16 * BR);
-          const float v[8] = {bf2f_lo(blo[0]) * w0[0], bf2f_hi(blo[0]) * w0[1],
-                              bf2f_lo(blo[1]) * w0[2], bf2f_hi(blo[1]) * w0[3],
-                              bf2f_lo(bhi[0]) * w1[0], bf2f_hi(bhi[0]) * w1[1],
-                              bf2f_lo(bhi[1]) * w1[2], bf2f_hi(bhi[1]) * w1[3]};
-          u32x4_t hi, lo;
+    for (int e = 0; e < 4; ++e) {
+      vh[e] = pack_bf16x2(v[2 * e], v[2 * e + 1]);
+      vl[e] = pack_bf16x2(v[2 * e] - bf2f_lo(vh[e]), v[2 * e + 1] - bf2f_hi(vh[e]));
+    }
+  };
+
+  auto compute = [&](int s, int u) {
+    const int c = u / upc, part = u % upc;
+    const lds_char_t* xs = sm + s * stage_bytes;
+    const lds_char_t* bs = xs + p.xbytes;
+    const float* wv = s_w[u & 1];
+    if (part == 0) {
+      // prev(c) out, then R = exp(dA[c, Q-1]) R; states(c) accumulate below
+      const float* dAs = reinterpret_cast<const float*>(smem + s * stage_bytes + p.xbytes + p.bbytes);
+      const float decay = fast_exp2(dAs[256 + 3] * 1.4426950408889634f);
+      float* outc = p.prevT + (((int64_t)(b * nc + c) * H + h) * N + n0) * P;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            hi[e] = pack_bf16x2(v[2 * e], v[2 * e + 1]);
-            lo[e] = pack_bf16x2(v[2 * e] - bf2f_lo(hi[e]), v[2 * e + 1] - bf2f_hi(hi[e]));
-          }
-          R[u] = mfma16(xf, hi, R[u]);
-          R[u] = mfma16(xf, lo, R[u]);
+      for (int t = 0; t < TPW; ++t) {
+        const int tt = wave + kSsdWaves * t;
+        if (tt < tiles) {
+          const int pt = tt % ptiles, nt = tt / ptiles;
+          *reinterpret_cast<f32x4_t*>(outc + (int64_t)(16 * nt + r) * P + 16 * pt + 4 * gq) = R[t];
+          R[t] *= decay;
         }
       }
     }
-    __syncthreads();
-    if (c + 1 < nc) {
-      store_chunk();
-      __syncthreads();
+#pragma unroll 4
+    for (int ks = 0; ks < QSP / 32; ++ks) {
+      const int k0 = 32 * ks + 4 * gq;          // this lane's keys: k0 + 0..3, k0 + 16..19
+      u32x4_t xh, xl;
+      if (SHARED_PT && wave < tiles) x_operand(xs, wv, wave % ptiles, k0, xh, xl);
+#pragma unroll
+      for (int t = 0; t < TPW; ++t) {
+        const int tt = wave + kSsdWaves * t;
+        if (tt < tiles) {
+          const int pt = tt % ptiles, nt = tt / ptiles;
+          if (!SHARED_PT) x_operand(xs, wv, pt, k0, xh, xl);
+          // B operand: n = 16 nt + r, same keys
+          const lds_char_t* qb = bs + (k0 + a4) * BR + (2 * nt + (c4 >> 1)) * 16 + (c4 & 1) * 8;
+          const u32x2_t blo = lds_read_tr16(qb), bhi = lds_read_tr16(qb + 16 * BR);
+          const u32x4_t bf = u32x4_t{blo[0], blo[1], bhi[0], bhi[1]};
+          R[t] = mfma16(xh, bf, R[t]);
+          R[t] = mfma16(xl, bf, R[t]);
+        }
+      }
     }
+  };
+
+  // ---- pipeline: units issued NS-1 ahead.  Iteration u waits for units u
+  // and u+1, so w of unit u+1 can be built (into the other s_w buffer) while
+  // unit u computes; the barrier of iteration u+1 publishes it.  The DMA
+  // after the barrier of iteration u reuses the stage of unit u-1, finished
+  // before that barrier.  prev stores issued by compute(u) are younger than
+  // the DMAs in flight, so the next wait leaves them outstanding too.
+  const int nst = min(TPW, max(0, (tiles - wave + kSsdWaves - 1) / kSsdWaves));
+  for (int u = 0; u < NS - 1 && u < nu; ++u) issue(u, u);
+  wait_units(min(NS - 2, nu - 1), 0);
+  barrier_nofence();
+  make_w(0, 0);
+  int stores = 0;
+  for (int u = 0; u < nu; ++u) {
+    wait_units(max(0, min(NS - 3, nu - 2 - u)), stores);
+    LOOM_WAIT_LGKM0();                        // s_w writes visible after the barrier
+    barrier_nofence();
+    if (u + NS - 1 < nu) issue((u + NS - 1) % NS, u + NS - 1);
+    if (u + 1 < nu) make_w((u + 1) % NS, u + 1);
+    compute(u % NS, u);
+    stores = (u % upc == 0) ? nst : 0;
   }
 }
 
 template <int TPW>
-void launch_state(const uint16_t* x, const float* dt, const float* dA, const uint16_t* Bm,
-                  float* prevT, int Bb, int H, int G, int nc, int Q, int P, int N, int nb,
-                  hipStream_t st) {
-  hipLaunchKernelGGL((ssd_state_kernel<TPW>), dim3((unsigned)(Bb * H), (unsigned)(N / nb)),
-                     dim3(64 * kSsdWaves), 0, st, x, dt, dA, Bm, prevT, H, G, nc, Q, P, N, nb);
+void launch_state(const SsdStateParams& p, int grid_x, int grid_y, hipStream_t st) {
+  const int ptiles = p.P / 16;
+  if (kSsdWaves % ptiles == 0)
+    hipLaunchKernelGGL((ssd_state_kernel<TPW, true>), dim3((unsigned)grid_x, (unsigned)grid_y),
+                       dim3(64 * kSsdWaves), 0, st, p);
+  else
+    hipLaunchKernelGGL((ssd_state_kernel<TPW, false>), dim3((unsigned)grid_x, (unsigned)grid_y),
+                       dim3(64 * kSsdWaves), 0, st, p);
 }
 
 int check_ssd(const char* fn, int64_t batch, int64_t nchunks, int64_t nheads, int64_t ngroups,
@@ -281,9 +364,6 @@ int check_ssd(const char* fn, int64_t batch, int64_t nchunks, int64_t nheads, in
                      "%s: built for chunk_size <= %d, headdim <= %d, dstate <= 128 "
                      "(a multiple of 32 above 32)",
                      fn, kSsdQmax, kSsdPmax);
-  if (((chunk_size + 31) & ~31) * headdim * 2 > kSsdXBytes)
-    return loom_fail(err, errlen, LOOM_EUNSUP,
-                     "%s: chunk_size x headdim above the %d-byte LDS chunk buffer", fn, kSsdXBytes);
   if (batch * nheads * nchunks * chunk_size * headdim >= (int64_t)1 << 40)
     return loom_fail(err, errlen, LOOM_EINVAL, "%s: problem too large", fn);
   return LOOM_OK;
@@ -349,17 +429,46 @@ int loom_hip_ssd_chunk_state_passing(const void* x, const void* dt, const void* 
     return loom_fail(err, errlen, LOOM_EUNSUP,
                      "ssd_chunk_state_passing: dstate %lld with headdim %lld not built",
                      (long long)dstate, (long long)headdim);
+  SsdStateParams p{};
+  p.x = static_cast<const uint16_t*>(x);
+  p.dt = static_cast<const float*>(dt);
+  p.dA = static_cast<const float*>(dA_cumsum);
+  p.B = static_cast<const uint16_t*>(B);
+  p.prevT = static_cast<float*>(prev_states_T);
+  p.H = (int)nheads; p.G = (int)ngroups; p.nc = (int)nchunks; p.Q = (int)chunk_size;
+  p.P = (int)headdim; p.N = (int)dstate; p.nb = nb;
+  // unit: the largest of 128, 64, 32 keys dividing Q whose stage fits; a Q
+  // that is not a multiple of 32 is one unit padded to the next 32
+  p.QS = 0;
+  for (int qs : {128, 64, 32})
+    if (p.Q % qs == 0 && qs * (p.P + nb) * 2 + 2048 <= kSsdStageMax) { p.QS = qs; break; }
+  if (p.QS == 0 && p.Q % 32 != 0 && p.Q < 128) p.QS = p.Q;
+  p.QSP = (p.QS + 31) & ~31;
+  if (p.QS == 0 || p.QSP * (p.P + nb) * 2 + 2048 > kSsdStageMax)
+    return loom_fail(err, errlen, LOOM_EUNSUP,
+                     "ssd_chunk_state_passing: chunk_size %lld with headdim %lld does not fit "
+                     "an LDS stage",
+                     (long long)chunk_size, (long long)headdim);
+  p.upc = p.Q / p.QS;
+  p.xbytes = p.QSP * p.P * 2;
+  p.bbytes = p.QSP * nb * 2;
+  if (p.xbytes % 1024 || p.bbytes % 1024) {
+    // rows of fewer than 1 KB per 32 keys: pad the unit to whole DMA copies
+    p.xbytes = (p.xbytes + 1023) & ~1023;
+    p.bbytes = (p.bbytes + 1023) & ~1023;
+  }
+  p.ninstr = p.xbytes / 1024 + p.bbytes / 1024 + 2;
+  p.lpw = (p.ninstr + kSsdWaves - 1) / kSsdWaves;
+  // as many stages as fit, while the wait count stays encodable
+  p.ns = std::min(kSsdNSMax, kSsdRing / (p.xbytes + p.bbytes + 2048));
+  while (p.ns > 3 && p.lpw * (p.ns - 2) + tpw > 24) --p.ns;
+  if (p.ns < 3 || p.lpw * (p.ns - 2) + tpw > 24)
+    return loom_fail(err, errlen, LOOM_EUNSUP, "ssd_chunk_state_passing: stage too large");
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const auto* xp = static_cast<const uint16_t*>(x);
-  const auto* dtp = static_cast<const float*>(dt);
-  const auto* dAp = static_cast<const float*>(dA_cumsum);
-  const auto* bp = static_cast<const uint16_t*>(B);
-  auto* pp = static_cast<float*>(prev_states_T);
-  const int Bb = (int)batch, H = (int)nheads, G = (int)ngroups, nc = (int)nchunks,
-            Q = (int)chunk_size, P = (int)headdim, N = (int)dstate;
-  if (tpw <= 1) launch_state<1>(xp, dtp, dAp, bp, pp, Bb, H, G, nc, Q, P, N, nb, st);
-  else if (tpw <= 2) launch_state<2>(xp, dtp, dAp, bp, pp, Bb, H, G, nc, Q, P, N, nb, st);
-  else launch_state<4>(xp, dtp, dAp, bp, pp, Bb, H, G, nc, Q, P, N, nb, st);
+  const int gx = (int)(batch * nheads), gy = (int)(dstate / nb);
+  if (tpw <= 1) launch_state<1>(p, gx, gy, st);
+  else if (tpw <= 2) launch_state<2>(p, gx, gy, st);
+  else launch_state<4>(p, gx, gy, st);
   return loom_check_launch(err, errlen, "ssd_chunk_state_passing");
 }
 

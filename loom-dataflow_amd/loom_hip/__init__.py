@@ -176,7 +176,7 @@ def split_k_matmul_gather(a, b, out=None, partials=None, *, tile_m=64, tile_n=64
     return out, partials
 
 
-def attention(k, v, q, out=None, *, scale=None, causal=False, tile_b=1, tile_m=192,
+def attention(k, v, q, out=None, *, scale=None, causal=False, tile_b=1, tile_m=256,
               tile_n=64):
     """@attention (examples/flashattn/IR/00_from_helion_frontend.mlir:4).
 

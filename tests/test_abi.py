@@ -126,8 +126,8 @@ def test_ssd_rejections(lh):
     assert rc == 2 and "multiples of 16" in msg
     rc, msg = _call(lh, "loom_hip_ssd_prologue", *([FAKE] * 8), 1, 2, 4, 1, 512, 64, 128, None)
     assert rc == 2 and "chunk_size <= 256" in msg
-    rc, msg = _call(lh, "loom_hip_ssd_prologue", *([FAKE] * 8), 1, 2, 4, 1, 256, 160, 128, None)
-    assert rc == 2 and "LDS" in msg
+    rc, msg = _call(lh, "loom_hip_ssd_prologue", *([FAKE] * 8), 1, 2, 4, 1, 256, 64, 48, None)
+    assert rc == 2 and "multiple of 32" in msg
     rc, msg = _call(lh, "loom_hip_ssd_chunk_state_passing", None, *([FAKE] * 4),
                     1, 2, 4, 1, 64, 64, 128, None)
     assert rc == 1 and "null" in msg

@@ -204,14 +204,15 @@ def test_attention_vs_oracle_mid(lh):
             assert_close(got, ref, **ATTN_TOL, what=f"attention S=1000 causal={causal} tile_m={tm}")
 
 
-def test_attention_baseline_heads(lh):
+@pytest.mark.parametrize("tile_m", [192, 256])
+def test_attention_baseline_heads(lh, tile_m):
     """B4 x H32, S 4096, D 128, causal (the bench config): 3 heads vs the oracle."""
     torch.manual_seed(1)
     BH, S, D = 128, 4096, 128
     k = torch.randn(BH, D, S, device="cuda").to(torch.bfloat16)
     v = torch.randn(BH, S, D, device="cuda").to(torch.bfloat16)
     q = torch.randn(BH, S, D, device="cuda").to(torch.bfloat16)
-    out = host(lh.attention(k, v, q, causal=True, tile_m=192, tile_n=64))
+    out = host(lh.attention(k, v, q, causal=True, tile_m=tile_m, tile_n=64))
     assert np.isfinite(from_bf16(out)).all()
     for h in (0, 77, 127):
         ref = oracle.attention(host(k[h:h + 1]), host(v[h:h + 1]), host(q[h:h + 1]),
