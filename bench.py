@@ -44,6 +44,9 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--kernels", default="all", help="per-kernel table: all, none or a list")
     ap.add_argument("--iters", type=int, default=20, help="timed calls per kernel in the table")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="only run the workload profiled for roofline.traffic: a 256 MiB "
+                         "device copy (the calibration kernel) and three headline bmm launches")
     return ap.parse_args()
 
 
@@ -263,6 +266,23 @@ def main():
     torch.cuda.set_device(0)
     print(f"# device: {torch.cuda.get_device_name(0)}; {lh.__version__}", file=sys.stderr,
           flush=True)
+
+    if args.traffic_probe:
+        # profiled under rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE: the copy
+        # reads and writes exactly 256 MiB, which calibrates both counters
+        src = torch.ones(64 << 20, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+        a0 = (torch.randn(16, 2048, 2048, device="cuda") * 0.02).to(torch.bfloat16)
+        a1 = (torch.randn(16, 2048, 2048, device="cuda") * 0.02).to(torch.bfloat16)
+        out = torch.empty(16, 2048, 2048, dtype=torch.bfloat16, device="cuda")
+        for _ in range(3):
+            lh.batch_matmul(a0, a1, out, tile_m=256, tile_n=256)
+        torch.cuda.synchronize()
+        print("traffic probe done", file=sys.stderr, flush=True)
+        return
 
     cases = make_cases(torch, lh)
     head = cases["bmm"]()

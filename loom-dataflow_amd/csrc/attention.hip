@@ -10,21 +10,12 @@
 //   `causal` (absent from the reference) makes key j visible to query i
 //   only when j <= i; fully hidden KV blocks are skipped.
 //
-// gfx950 mapping.  A workgroup owns tile_m query rows of one (b, h) and
-// loops over 64-key blocks.  Each block of K and V is copied to LDS by
-// register-transposed 8x8 blocks so both products read 16-byte operands:
-//   Ks [key][d]  (K^T)  -- S^T[key, query] = K . Q^T, A operand from Ks,
-//                          B operand Q^T kept in registers;
-//   Vt [d][key]  (V^T)  -- O^T[d, query] += V^T . P^T, A operand from Vt,
-//                          B operand P^T taken directly from the S^T
-//                          accumulators (no shuffle, no LDS round trip).
-// Inside a 32-key pair of S^T tiles the MFMA row -> key assignment is
-// permuted (row rr of tile 2p+h holds key 32p + 8*(rr/4) + 4h + rr%4) so
-// that every lane's eight P^T values are eight consecutive keys, matching
-// one 16-byte read of Vt.  Softmax runs in fp32 in the log2 domain; rows'
-// sums stay per lane until the end.  LDS rows are XOR-swizzled in 16-byte
-// chunks so operand reads and transposed stores avoid bank conflicts.
-// Causal tiles are launched heaviest first.
+// gfx950 mapping (attention_dma_kernel below): a workgroup of W waves owns
+// 16 QT W query rows of one (b, h) and streams K and V through LDS in
+// 64-key blocks copied by LDS DMA; the MFMAs compute S^T = K^T Q^T and
+// O^T += V^T P^T so P^T is built straight from the S^T accumulators.
+// Softmax runs in fp32 in the log2 domain with a lazily moved base.  Causal
+// tiles are launched heaviest first.
 #include "common.h"
 
 namespace {

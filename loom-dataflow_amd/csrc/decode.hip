@@ -11,18 +11,17 @@
 //
 // gfx950 mapping.  Decode is bound by streaming K and V from HBM (the 32
 // heads give 32 FLOP per KV byte), so nothing goes through LDS on the way
-// in: each wave pulls a 128-key block of K and V straight into registers
-// with 16-byte loads (16 lanes cover one 256-byte row, fully coalesced) and
-// turns 8x8 blocks into MFMA operands with a register transpose:
-//   S^T[key, head] = K^T . Q^T  -- A operand: lane (r, g) holds keys
-//                                 base + 8r + j, d-group g (j = tile index)
+// in: each wave walks 64-key blocks, pulling K and V straight into
+// registers with raw buffer loads, and builds the MFMA operands with
+// register transposes (v_perm_b32):
+//   S^T[key, head] = K^T . Q^T  -- A operand from 8-byte K loads (four keys
+//                                 of eight d rows) transposed 8x4
 //   O^T[d, head]  += V^T . P^T  -- B operand P^T comes straight from the
-//                                 S^T accumulators of two key tiles, A
-//                                 operand V^T from eight V rows transposed.
-// Keys and d are permuted inside a block (key = base + 8r + j,
-// d = VEC*r + u) and the permutation is undone only where results are
-// addressed, which is sound because softmax and P.V do not depend on the
-// order of the keys.  Softmax runs in the log2 domain in fp32.
+//                                 S^T accumulators, A operand V^T from
+//                                 16-byte V row loads transposed.
+// Keys are permuted inside a block and the permutation is undone only where
+// results are addressed, which is sound because softmax and P.V do not
+// depend on the order of the keys.  Softmax runs in the log2 domain in fp32.
 // One workgroup (4 waves) per (batch, split); the waves' partial states
 // are merged through LDS into (lse_s, o_s), exactly the reference's
 // gathered tensors; a second kernel performs the split-0 combine.

@@ -225,8 +225,9 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_bf16_kernel(GemmParams p) {
 // ---------------------------------------------------------------------------
 // 256x256 tile, LDS-DMA pipeline.  Four waves, each owning a 128x128 block of
 // C.  Per stage, A [256][BK] and B [BK][256] are copied global -> LDS by
-// buffer_load ... lds (no staging registers, range-checked against each
-// operand's extent), NS stages deep.  B stays in its [k][n] layout: the MFMA
+// global_load_lds_dwordx4 (no staging registers; addresses clamped inside
+// each operand, the rows and columns past its extent are never stored),
+// NS stages deep.  B stays in its [k][n] layout: the MFMA
 // operand with eight consecutive k per lane comes from two ds_read_b64_tr_b16.
 // The MFMA computes C^T tiles (B^T as the row operand, A^T as the column
 // operand), so each lane ends with four consecutive columns of one row of C:
@@ -235,8 +236,9 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_bf16_kernel(GemmParams p) {
 // keep the operand reads free of bank conflicts; the DMA writes are linear
 // 1 KB blocks per instruction.
 // Each stage buffer is its own __shared__ array and the main loop is unrolled
-// by NS, so the compiler can tell a stage being read from the stages whose DMA
-// is still in flight and only waits for the one it needs.
+// by NS, so every LDS address is a constant offset; the DMAs are issued from
+// inline assembly and waited for by hand (s_waitcnt vmcnt(n) for the stage
+// needed next), with barriers that do not drain the DMAs still in flight.
 // ---------------------------------------------------------------------------
 // A rows hold BK/8 16-byte chunks.  BK 32: the 16 lanes that read one chunk
 // column from 16 consecutive rows must land in distinct 16-byte bank slots
