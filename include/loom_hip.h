@@ -225,6 +225,35 @@ int loom_hip_dispatch(const char* variant, void* const* tensors, int ntensors,
                       const int64_t* dims, int ndims, float scale, int causal, void* workspace,
                       size_t workspace_bytes, void* stream, char* err, size_t errlen);
 
+/* Validates a materialized variant against its extents exactly as
+ * loom_hip_dispatch would -- same checks, same codes and messages -- and
+ * launches nothing (no device is needed).  `dims` as for loom_hip_dispatch. */
+int loom_hip_check_variant(const char* variant, const int64_t* dims, int ndims, char* err,
+                           size_t errlen);
+
+/* ---- gfx950 block-size constraints for the external solver ---------------
+ * The reference hands its solver one constraint scope per variant
+ * (examples/mm/constraint_space/staged_etg_dump.json; built in
+ * lib/passes/lcs/src/staged_etg_builder.cpp:1465-1478 and
+ * hard_constraint_pipeline.cpp:162-213) with Tenstorrent rules: inner tile
+ * dims aligned to 32 (hw_alignment.cpp:16) and an L1 budget of 1499136 bytes.
+ * loom_hip_constraint_scope writes the same JSON object for gfx950 --
+ * {"variant_name", "constraint_scope": {"metadata": {"datatype", "booleans",
+ * "iter_num", "L1_footprint" (LDS bytes here), "symbols": {sym: {"type",
+ * "natural_ub", "alignment"}}}, "hard_constraints": [...]}} in the grammar of
+ * lib/passes/lcs/inc/expr.h and constraint_expr.h -- whose hard constraints
+ * accept exactly the bindings this library builds for those extents (the
+ * workgroup tiles of each kernel, LDS <= 160 KiB).  `dims` as for
+ * loom_hip_dispatch; a shape no kernel supports returns LOOM_HIP_EUNSUP. */
+int loom_hip_constraint_scope(const char* func, const int64_t* dims, int ndims, char* out,
+                              size_t outlen, char* err, size_t errlen);
+
+/* The binding this library runs fastest for those extents on MI355X (one
+ * JSON object {"tile_m": 256, ...} over the function's symbols; a legal
+ * point of loom_hip_constraint_scope), usable as a block_sizes_json entry. */
+int loom_hip_preferred_block_sizes(const char* func, const int64_t* dims, int ndims, char* out,
+                                   size_t outlen, char* err, size_t errlen);
+
 #ifdef __cplusplus
 }
 #endif

@@ -469,11 +469,282 @@ int need_tiles(const std::string& func, const int64_t* tiles, std::initializer_l
   return LOOM_HIP_OK;
 }
 
+// ---------------------------------------------------------------------------
+// gfx950 block-size constraint scopes, in the reference's constraint JSON
+// grammar (lib/passes/lcs/inc/expr.h:17-25, constraint_expr.h:13-22):
+//   Expr        {"Const": v} {"Sym": s} {"Add"|"Sub"|"Mul"|"Div"|"Min"|"Max": [a, b]}
+//   Constraint  {"And"|"Or": [...]} {"Not": c} {"Eq"|"Le"|"Lt"|"Ge"|"Gt": [a, b]}
+//               {"InRange": {"x", "lo", "hi"}} {"Divisible": {"x", "by"}}
+// ---------------------------------------------------------------------------
+std::string jc(long long v) { return "{\"Const\":" + std::to_string(v) + "}"; }
+std::string js(const char* s) { return std::string("{\"Sym\":\"") + s + "\"}"; }
+std::string jop(const char* op, const std::string& a, const std::string& b) {
+  return std::string("{\"") + op + "\":[" + a + "," + b + "]}";
+}
+std::string jlist(const char* op, const std::vector<std::string>& xs) {
+  std::string o = std::string("{\"") + op + "\":[";
+  for (size_t i = 0; i < xs.size(); ++i) o += (i ? "," : "") + xs[i];
+  return o + "]}";
+}
+std::string jrange(const char* sym, long long lo, long long hi) {
+  return std::string("{\"InRange\":{\"x\":") + js(sym) + ",\"lo\":" + jc(lo) + ",\"hi\":" + jc(hi) + "}}";
+}
+std::string jin(const char* sym, std::initializer_list<long long> vals) {
+  std::vector<std::string> alts;
+  for (long long v : vals) alts.push_back(jop("Eq", js(sym), jc(v)));
+  return jlist("Or", alts);
+}
+std::string jsym(const char* name, long long ub, long long align) {
+  return std::string("\"") + name + "\":{\"type\":\"int\",\"natural_ub\":" + std::to_string(ub) +
+         ",\"alignment\":" + std::to_string(align) + "}";
+}
+
+constexpr long long kLdsBytes = 160 * 1024;   // LDS per workgroup on gfx950
+
+struct Scope {
+  std::vector<std::string> symbols, footprint, hard, temp_iter;
+  std::string seq_iter;
+};
+
+int build_scope(const std::string& f, const int64_t* d, int nd, Scope& sc, std::string& err) {
+  auto need = [&](int n) {
+    if (nd != n) {
+      err = "constraint_scope: " + f + " takes " + std::to_string(n) + " extents";
+      return false;
+    }
+    for (int i = 0; i < n; ++i)
+      if (d[i] <= 0) {
+        err = "constraint_scope: extents must be positive";
+        return false;
+      }
+    return true;
+  };
+  // the GEMM tile pairs; both LDS-staged kernels hold 256 (tile_m + tile_n) bytes
+  auto gemm_tiles = [&](long long M, long long N) {
+    sc.symbols.push_back(jsym("tile_m", M, 64));
+    sc.symbols.push_back(jsym("tile_n", N, 64));
+    sc.hard.push_back(jlist("Or", {jlist("And", {jop("Eq", js("tile_m"), jc(64)), jop("Eq", js("tile_n"), jc(64))}),
+                                   jlist("And", {jop("Eq", js("tile_m"), jc(128)), jop("Eq", js("tile_n"), jc(128))}),
+                                   jlist("And", {jop("Eq", js("tile_m"), jc(256)), jop("Eq", js("tile_n"), jc(256))})}));
+    sc.footprint.push_back(jop("Mul", jc(256), js("tile_m")));
+    sc.footprint.push_back(jop("Mul", jc(256), js("tile_n")));
+    sc.hard.push_back(jop("Le", jop("Add", sc.footprint[0], sc.footprint[1]), jc(kLdsBytes)));
+    sc.temp_iter.push_back(jop("Div", jc(M), js("tile_m")));
+    sc.temp_iter.push_back(jop("Div", jc(N), js("tile_n")));
+  };
+  if (f == "matmul") {
+    if (!need(3)) return LOOM_HIP_EINVAL;
+    gemm_tiles(d[0], d[1]);
+    sc.symbols.push_back(jsym("tile_k", d[2], 1));
+    sc.hard.push_back(jop("Ge", js("tile_k"), jc(1)));
+    sc.seq_iter = jop("Div", jc(d[2]), js("tile_k"));
+  } else if (f == "batch_matmul") {
+    if (!need(4)) return LOOM_HIP_EINVAL;
+    sc.symbols.push_back(jsym("tile_b", d[0], 1));
+    sc.hard.push_back(jop("Ge", js("tile_b"), jc(1)));
+    gemm_tiles(d[1], d[2]);
+    sc.symbols.push_back(jsym("tile_k", d[3], 1));
+    sc.hard.push_back(jop("Ge", js("tile_k"), jc(1)));
+    sc.temp_iter.insert(sc.temp_iter.begin(), jop("Div", jc(d[0]), js("tile_b")));
+    sc.seq_iter = jop("Div", jc(d[3]), js("tile_k"));
+  } else if (f == "split_k_matmul_gather") {
+    if (!need(3)) return LOOM_HIP_EINVAL;
+    gemm_tiles(d[0], d[1]);
+    sc.symbols.push_back(jsym("tile_k", d[2], 1));
+    sc.hard.push_back(jrange("tile_k", 1, d[2]));
+    sc.temp_iter.push_back(jop("Div", jc(d[2]), js("tile_k")));
+  } else if (f == "attention") {
+    if (!need(4)) return LOOM_HIP_EINVAL;
+    if (!(d[3] == 64 || d[3] == 128) || d[2] % 8) {
+      err = "constraint_scope: attention is built for head_dim 64 or 128 and Skv a multiple of 8";
+      return LOOM_HIP_EUNSUP;
+    }
+    sc.symbols.push_back(jsym("tile_b", d[0], 1));
+    sc.symbols.push_back(jsym("tile_m", d[1], 64));
+    sc.symbols.push_back(jsym("tile_n", d[2], 1));
+    sc.hard.push_back(jrange("tile_b", 1, d[0]));
+    sc.hard.push_back(jin("tile_m", {64, 128, 192, 256}));
+    sc.hard.push_back(jrange("tile_n", 1, d[2]));
+    // four stages of 64-key K and V blocks
+    sc.footprint.push_back(jc(4 * 64 * d[3] * 2));
+    sc.footprint.push_back(jc(4 * 64 * d[3] * 2));
+    sc.hard.push_back(jop("Le", jop("Add", sc.footprint[0], sc.footprint[1]), jc(kLdsBytes)));
+    sc.temp_iter.push_back(jop("Div", jc(d[0]), js("tile_b")));
+    sc.temp_iter.push_back(jop("Div", jc(d[1]), js("tile_m")));
+    sc.seq_iter = jop("Div", jc(d[2]), js("tile_n"));
+  } else if (f == "flash_decode") {
+    if (!need(4)) return LOOM_HIP_EINVAL;
+    if (!(d[2] == 64 || d[2] == 128) || d[1] > 32) {
+      err = "constraint_scope: flash_decode is built for head_dim 64 or 128 and H <= 32";
+      return LOOM_HIP_EUNSUP;
+    }
+    sc.symbols.push_back(jsym("tile_b", d[0], 1));
+    sc.symbols.push_back(jsym("tile_s", d[3], 1));
+    sc.symbols.push_back(jsym("tile_n", d[3], 1));
+    sc.hard.push_back(jrange("tile_b", 1, d[0]));
+    sc.hard.push_back(jrange("tile_s", 1, d[3]));
+    sc.hard.push_back(jrange("tile_n", 1, d[3]));
+    sc.temp_iter.push_back(jop("Div", jc(d[0]), js("tile_b")));
+    sc.temp_iter.push_back(jop("Div", jc(d[3]), js("tile_s")));
+    sc.seq_iter = jop("Div", js("tile_s"), js("tile_n"));
+  } else if (f == "helion_mamba2_chunk_scan_kernel") {
+    if (!need(7)) return LOOM_HIP_EINVAL;
+    if (d[4] > 256 || d[6] > 128 || d[4] % 8 || d[5] % 8 || d[6] % 8 || d[2] % d[3]) {
+      err = "constraint_scope: chunk scan is built for chunk_size <= 256, dstate <= 128, "
+            "multiples of 8, and nheads a multiple of ngroups";
+      return LOOM_HIP_EUNSUP;
+    }
+    sc.symbols.push_back(jsym("tile_m", d[4], 64));
+    sc.symbols.push_back(jsym("tile_n", d[5], 16));
+    sc.symbols.push_back(jsym("tile_k", d[4], 1));
+    sc.symbols.push_back(jsym("tile_c", d[1], 1));
+    sc.symbols.push_back(jsym("tile_b", d[0], 1));
+    sc.symbols.push_back(jsym("tile_h", d[2], 1));
+    sc.hard.push_back(jop("Eq", js("tile_b"), jc(1)));
+    sc.hard.push_back(jop("Eq", js("tile_h"), jc(1)));
+    sc.hard.push_back(jop("Eq", js("tile_c"), jc(1)));
+    sc.hard.push_back(jin("tile_m", {64, 128, 192, 256}));
+    sc.hard.push_back(jin("tile_n", {16, 32, 64}));
+    sc.hard.push_back(jop("Ge", js("tile_k"), jc(1)));
+    sc.temp_iter.push_back(jop("Div", jc(d[4]), js("tile_m")));
+    sc.temp_iter.push_back(jop("Div", jc(d[5]), js("tile_n")));
+    sc.seq_iter = jop("Div", jc(d[4]), js("tile_k"));
+  } else {
+    err = "constraint_scope: no gfx950 kernel for function '" + f + "'";
+    return LOOM_HIP_EUNSUP;
+  }
+  return LOOM_HIP_OK;
+}
+
+int tensors_of(const std::string& f) {
+  if (f == "attention" || f == "flash_decode") return 4;
+  if (f == "helion_mamba2_chunk_scan_kernel") return 8;
+  return 3;
+}
+
+long long ceil_div(long long a, long long b) { return (a + b - 1) / b; }
+
+int copy_out(const std::string& js_, char* out, size_t outlen, char* err, size_t errlen,
+             const char* fn) {
+  if (!out || outlen <= js_.size())
+    return fail(err, errlen, LOOM_HIP_EINVAL, "%s: output buffer needs %zu bytes", fn,
+                js_.size() + 1);
+  memcpy(out, js_.c_str(), js_.size() + 1);
+  if (err && errlen) err[0] = '\0';
+  return LOOM_HIP_OK;
+}
+
+thread_local bool g_validate_only = false;
+
 }  // namespace
+
+// entry points check this before launching (declared in csrc/common.h)
+bool& loom_validate_only_flag() { return g_validate_only; }
 
 extern "C" {
 
 const char* loom_hip_version(void) { return LOOM_HIP_VERSION_STRING; }
+
+int loom_hip_check_variant(const char* variant, const int64_t* dims, int ndims, char* err,
+                           size_t errlen) {
+  if (!variant) return fail(err, errlen, LOOM_HIP_EINVAL, "check_variant: null variant");
+  std::string f, perr;
+  int64_t t[LOOM_HIP_NTILES];
+  int rc = parse_variant(variant, f, t, perr);
+  if (rc) return fail(err, errlen, rc, "check_variant: %s", perr.c_str());
+  // stand-in pointers: aligned, never dereferenced (nothing launches)
+  void* fake[8];
+  for (auto& x : fake) x = reinterpret_cast<void*>(uintptr_t(1) << 20);
+  struct Guard {
+    Guard() { g_validate_only = true; }
+    ~Guard() { g_validate_only = false; }
+  } guard;
+  return loom_hip_dispatch(variant, fake, tensors_of(f), dims, ndims, 1.0f, 0, fake[0],
+                           ~(size_t)0, nullptr, err, errlen);
+}
+
+int loom_hip_constraint_scope(const char* func, const int64_t* dims, int ndims, char* out,
+                              size_t outlen, char* err, size_t errlen) {
+  if (!func || (ndims > 0 && !dims))
+    return fail(err, errlen, LOOM_HIP_EINVAL, "constraint_scope: null argument");
+  const std::string f = std::string(func).substr(0, std::string(func).find("__"));
+  Scope sc;
+  std::string perr;
+  const int rc = build_scope(f, dims, ndims, sc, perr);
+  if (rc) return fail(err, errlen, rc, "%s", perr.c_str());
+  std::string j = std::string("{\"variant_name\":\"") + func + "\",\"constraint_scope\":{" +
+                  "\"metadata\":{\"datatype\":\"bf16\",\"target\":\"gfx950\",\"memory\":\"LDS\"," +
+                  "\"capacity_bytes\":" + std::to_string(kLdsBytes) + ",\"booleans\":[]," +
+                  "\"iter_num\":{\"temp_iter\":[";
+  for (size_t i = 0; i < sc.temp_iter.size(); ++i) j += (i ? "," : "") + sc.temp_iter[i];
+  j += "]";
+  if (!sc.seq_iter.empty()) j += ",\"seq_iter\":" + sc.seq_iter;
+  j += "},\"L1_footprint\":[";
+  for (size_t i = 0; i < sc.footprint.size(); ++i) j += (i ? "," : "") + sc.footprint[i];
+  j += "],\"symbols\":{";
+  for (size_t i = 0; i < sc.symbols.size(); ++i) j += (i ? "," : "") + sc.symbols[i];
+  j += "}},\"hard_constraints\":[";
+  for (size_t i = 0; i < sc.hard.size(); ++i) j += (i ? "," : "") + sc.hard[i];
+  j += "]}}";
+  return copy_out(j, out, outlen, err, errlen, "constraint_scope");
+}
+
+int loom_hip_preferred_block_sizes(const char* func, const int64_t* dims, int ndims, char* out,
+                                   size_t outlen, char* err, size_t errlen) {
+  if (!func || (ndims > 0 && !dims))
+    return fail(err, errlen, LOOM_HIP_EINVAL, "preferred_block_sizes: null argument");
+  const std::string f = std::string(func).substr(0, std::string(func).find("__"));
+  Scope sc;
+  std::string perr;
+  int rc = build_scope(f, dims, ndims, sc, perr);   // validates f and the extents
+  if (rc) return fail(err, errlen, rc, "%s", perr.c_str());
+  const int64_t* d = dims;
+  constexpr long long kCUs = 256;
+  std::map<std::string, long long> b;
+  // largest GEMM tile that still gives every CU a workgroup
+  auto gemm_tile = [&](long long M, long long N, long long z) {
+    for (long long t : {256LL, 128LL})
+      if (ceil_div(M, t) * ceil_div(N, t) * z >= kCUs) return t;
+    return 64LL;
+  };
+  if (f == "matmul") {
+    b["tile_m"] = b["tile_n"] = gemm_tile(d[0], d[1], 1);
+    b["tile_k"] = 64;
+  } else if (f == "batch_matmul") {
+    b["tile_b"] = 1;
+    b["tile_m"] = b["tile_n"] = gemm_tile(d[1], d[2], d[0]);
+    b["tile_k"] = 64;
+  } else if (f == "split_k_matmul_gather") {
+    b["tile_m"] = b["tile_n"] = 64;
+    // enough K slabs to cover the CUs, slabs a multiple of 64 deep
+    const long long tiles = ceil_div(d[0], 64) * ceil_div(d[1], 64);
+    const long long S = std::max(1LL, std::min(ceil_div(kCUs, tiles), ceil_div(d[2], 64)));
+    b["tile_k"] = std::min<long long>(d[2], ceil_div(ceil_div(d[2], S), 64) * 64);
+  } else if (f == "attention") {
+    b["tile_b"] = 1;
+    b["tile_m"] = 256;
+    b["tile_n"] = std::min<long long>(64, d[2]);
+  } else if (f == "flash_decode") {
+    b["tile_b"] = 1;
+    // one workgroup per (batch, split): about one per CU
+    const long long ns = std::max(1LL, ceil_div(kCUs, d[0]));
+    b["tile_s"] = std::min<long long>(d[3], ceil_div(ceil_div(d[3], ns), 64) * 64);
+    b["tile_n"] = std::min<long long>(128, b["tile_s"]);
+  } else {  // helion_mamba2_chunk_scan_kernel
+    b["tile_b"] = b["tile_h"] = b["tile_c"] = 1;
+    b["tile_m"] = std::min<long long>(256, ceil_div(d[4], 64) * 64);
+    b["tile_n"] = d[5] >= 64 ? 64 : d[5] >= 32 ? 32 : 16;
+    b["tile_k"] = 64;
+  }
+  std::string j = "{";
+  bool first = true;
+  for (const auto& kv : b) {
+    j += (first ? "\"" : ",\"") + kv.first + "\":" + std::to_string(kv.second);
+    first = false;
+  }
+  j += "}";
+  return copy_out(j, out, outlen, err, errlen, "preferred_block_sizes");
+}
 
 int loom_hip_materialize_variants(const char* block_sizes_json, const char* const* funcs,
                                   int nfuncs, char* out, size_t outlen, char* err,

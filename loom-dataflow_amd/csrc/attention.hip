@@ -339,6 +339,7 @@ int loom_hip_attention(const void* k, const void* v, const void* q, void* out, i
   p.causal = causal ? 1 : 0;
   p.nqt = (int)cdiv64(Sq, tile_m);
   p.c2 = scale * 1.4426950408889634f;
+  if (loom_validate_only()) return loom_ok(err, errlen);
   hipStream_t st = static_cast<hipStream_t>(stream);
   {
     const dim3 grid((unsigned)(p.BH * p.nqt)), b4(256), b8(512);

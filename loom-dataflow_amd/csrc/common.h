@@ -105,6 +105,11 @@ static inline int loom_fail(char* err, size_t errlen, int code, const char* fmt,
   return code;
 }
 
+// Set (per thread) by loom_hip_check_variant: entry points validate their
+// arguments and return before launching anything.
+bool& loom_validate_only_flag();
+static inline bool loom_validate_only() { return loom_validate_only_flag(); }
+
 static inline int loom_ok(char* err, size_t errlen) {
   if (err && errlen) err[0] = '\0';
   return LOOM_OK;

@@ -399,6 +399,7 @@ int loom_hip_flash_decode(const void* k, const void* v, const void* q, void* out
   p.ns = (int)ns;
   p.c2 = scale * 1.4426950408889634f;
   const bool al = S % 4 == 0;
+  if (loom_validate_only()) return loom_ok(err, errlen);
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (D == 128) {
     if (H > 16) launch_split<128, 2>(p, al, st); else launch_split<128, 1>(p, al, st);

@@ -550,6 +550,7 @@ int loom_hip_matmul(const void* x, const void* y, void* out, int64_t M, int64_t 
   p.split = 0;
   p.nz = 1;
   const bool al = K % 8 == 0 && N % 8 == 0 && aligned16(x) && aligned16(y);
+  if (loom_validate_only()) return loom_ok(err, errlen);
   (void)launch_gemm(p, tile_m, tile_n, al, false, static_cast<hipStream_t>(stream));
   return loom_check_launch(err, errlen, "matmul");
 }
@@ -582,6 +583,7 @@ int loom_hip_batch_matmul(const void* arg0, const void* arg1, void* arg2, int64_
   p.split = 0;
   p.nz = (int)Bt;
   const bool al = K % 8 == 0 && N % 8 == 0 && aligned16(arg0) && aligned16(arg1);
+  if (loom_validate_only()) return loom_ok(err, errlen);
   (void)launch_gemm(p, tile_m, tile_n, al, false, static_cast<hipStream_t>(stream));
   return loom_check_launch(err, errlen, "batch_matmul");
 }
@@ -626,6 +628,7 @@ int loom_hip_split_k_matmul_gather(const void* a, const void* b, void* out, void
   p.split = 1;
   p.nz = (int)S;
   const bool al = K % 8 == 0 && N % 8 == 0 && tile_k % 8 == 0 && aligned16(a) && aligned16(b);
+  if (loom_validate_only()) return loom_ok(err, errlen);
   (void)launch_gemm(p, tile_m, tile_n, al, true, st);
   rc = loom_check_launch(err, errlen, "split_k_matmul_gather (slab GEMM)");
   if (rc) return rc;

@@ -373,6 +373,7 @@ int loom_hip_helion_mamba2_chunk_scan_kernel(
   p.tile_n = (int)tile_n;
   p.nmt = (int)nmt;
   p.npt = (int)npt;
+  if (loom_validate_only()) return loom_ok(err, errlen);
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (tile_n == 64) launch_mamba<4>(p, st);
   else if (tile_n == 32) launch_mamba<2>(p, st);

@@ -385,6 +385,7 @@ int loom_hip_ssd_chunk_cumsum(const void* dt, const void* A, void* dA_cumsum, in
   if (batch * nheads * nchunks > 0x7fffffff / 64)
     return loom_fail(err, errlen, LOOM_EINVAL, "ssd_chunk_cumsum: problem too large");
   const int per_lane = (int)((chunk_size + 63) / 64);
+  if (loom_validate_only()) return loom_ok(err, errlen);
   hipLaunchKernelGGL(ssd_cumsum_kernel, dim3((unsigned)(batch * nheads * nchunks)), dim3(64), 0,
                      static_cast<hipStream_t>(stream), static_cast<const float*>(dt),
                      static_cast<const float*>(A), static_cast<float*>(dA_cumsum), (int)nheads,
@@ -401,6 +402,7 @@ int loom_hip_ssd_bmm_chunk(const void* B, const void* C, void* cb, int64_t batch
   if (rc) return rc;
   if (!aligned16(B) || !aligned16(C) || (reinterpret_cast<uintptr_t>(cb) & 7u))
     return loom_fail(err, errlen, LOOM_EINVAL, "ssd_bmm_chunk: B, C 16-byte and cb 8-byte aligned");
+  if (loom_validate_only()) return loom_ok(err, errlen);
   hipLaunchKernelGGL(ssd_cb_kernel, dim3((unsigned)(batch * nchunks * ngroups), (unsigned)(chunk_size / 16)),
                      dim3(64), 0, static_cast<hipStream_t>(stream),
                      static_cast<const uint16_t*>(B), static_cast<const uint16_t*>(C),
@@ -466,6 +468,7 @@ int loom_hip_ssd_chunk_state_passing(const void* x, const void* dt, const void* 
     return loom_fail(err, errlen, LOOM_EUNSUP, "ssd_chunk_state_passing: stage too large");
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int gx = (int)(batch * nheads), gy = (int)(dstate / nb);
+  if (loom_validate_only()) return loom_ok(err, errlen);
   if (tpw <= 1) launch_state<1>(p, gx, gy, st);
   else if (tpw <= 2) launch_state<2>(p, gx, gy, st);
   else launch_state<4>(p, gx, gy, st);

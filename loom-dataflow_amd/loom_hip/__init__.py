@@ -68,11 +68,18 @@ _lib.loom_hip_dispatch.argtypes = [ctypes.c_char_p, ctypes.POINTER(_vp), ctypes.
                                    ctypes.POINTER(_i64), ctypes.c_int, _f32, ctypes.c_int,
                                    _vp, _sz, _vp, *_ERR]
 _lib.loom_hip_dispatch.restype = ctypes.c_int
+_lib.loom_hip_check_variant.argtypes = [ctypes.c_char_p, ctypes.POINTER(_i64), ctypes.c_int, *_ERR]
+_lib.loom_hip_check_variant.restype = ctypes.c_int
+for _fn in ("loom_hip_constraint_scope", "loom_hip_preferred_block_sizes"):
+    getattr(_lib, _fn).argtypes = [ctypes.c_char_p, ctypes.POINTER(_i64), ctypes.c_int,
+                                   ctypes.c_char_p, _sz, *_ERR]
+    getattr(_lib, _fn).restype = ctypes.c_int
 
 EXPORTED = tuple(_SIGS) + ("loom_hip_split_k_workspace_bytes",
                            "loom_hip_flash_decode_workspace_bytes", "loom_hip_version",
                            "loom_hip_materialize_variants", "loom_hip_parse_variant",
-                           "loom_hip_dispatch")
+                           "loom_hip_dispatch", "loom_hip_check_variant",
+                           "loom_hip_constraint_scope", "loom_hip_preferred_block_sizes")
 
 #: block-size symbols in the slot order of loom_hip_parse_variant's tiles[]
 TILE_SYMBOLS = ("tile_b", "tile_m", "tile_n", "tile_k", "tile_s", "tile_h", "tile_c")
@@ -388,3 +395,39 @@ def dispatch(variant: str, *tensors, workspace=None, scale=None, causal=False):
     if rc != 0:
         raise LoomHipError("loom_hip_dispatch", rc, err.value.decode(errors="replace"))
     return tensors[-1], workspace
+
+
+# ---------------------------------------------------------------------------
+# gfx950 block-size constraints (the solver's input) and validation
+# ---------------------------------------------------------------------------
+
+def check_variant(variant: str, dims) -> None:
+    """Raises ``LoomHipError`` if ``loom_hip_dispatch`` would reject the
+    variant for these extents; launches nothing."""
+    darr = (_i64 * max(len(dims), 1))(*dims)
+    err = ctypes.create_string_buffer(512)
+    rc = _lib.loom_hip_check_variant(variant.encode(), darr, len(dims), err, len(err))
+    if rc != 0:
+        raise LoomHipError("loom_hip_check_variant", rc, err.value.decode(errors="replace"))
+
+
+def _json_call(name, func, dims):
+    import json
+    darr = (_i64 * max(len(dims), 1))(*dims)
+    out = ctypes.create_string_buffer(1 << 16)
+    err = ctypes.create_string_buffer(512)
+    rc = getattr(_lib, name)(func.encode(), darr, len(dims), out, len(out), err, len(err))
+    if rc != 0:
+        raise LoomHipError(name, rc, err.value.decode(errors="replace"))
+    return json.loads(out.value.decode())
+
+
+def constraint_scope(func: str, dims) -> dict:
+    """The gfx950 constraint scope of ``func`` for these extents, in the
+    reference's staged-ETG JSON shape (see include/loom_hip.h)."""
+    return _json_call("loom_hip_constraint_scope", func, dims)
+
+
+def preferred_block_sizes(func: str, dims) -> dict:
+    """The binding this library runs fastest for these extents."""
+    return _json_call("loom_hip_preferred_block_sizes", func, dims)

@@ -1,0 +1,149 @@
+"""gfx950 block-size constraint scopes (CPU only: nothing launches).
+
+The scopes are written in the reference's constraint grammar
+(lib/passes/lcs/inc/expr.h, constraint_expr.h).  `evaluate` below is an
+interpreter of that published grammar; the tests check, over a grid of
+candidate bindings per function and shape, that the scope's hard constraints
+accept exactly the bindings the library itself accepts
+(loom_hip_check_variant runs the entry point's own validation and launches
+nothing), that the symbol set is the function's loom.sym set, and that the
+preferred binding is legal.
+"""
+import itertools
+import json
+
+import pytest
+
+import loom_hip
+
+
+def evaluate(node, env):
+    """Interpreter of the reference's Expr / ConstraintExpr JSON."""
+    if node == "True":
+        return True
+    if node == "False":
+        return False
+    (op, arg), = node.items()
+    if op == "Const":
+        return arg
+    if op == "Sym":
+        return env[arg]
+    if op in ("Add", "Sub", "Mul", "Div", "Min", "Max"):
+        a, b = (evaluate(x, env) for x in arg)
+        return {"Add": a + b, "Sub": a - b, "Mul": a * b, "Div": a // b,
+                "Min": min(a, b), "Max": max(a, b)}[op]
+    if op == "IfElse":
+        return evaluate(arg["then_expr"] if evaluate(arg["cond"], env) else arg["else_expr"], env)
+    if op == "And":
+        return all(evaluate(x, env) for x in arg)
+    if op == "Or":
+        return any(evaluate(x, env) for x in arg)
+    if op == "Not":
+        return not evaluate(arg, env)
+    if op in ("Eq", "Le", "Lt", "Ge", "Gt"):
+        a, b = (evaluate(x, env) for x in arg)
+        return {"Eq": a == b, "Le": a <= b, "Lt": a < b, "Ge": a >= b, "Gt": a > b}[op]
+    if op == "InRange":
+        x = evaluate(arg["x"], env)
+        return evaluate(arg["lo"], env) <= x <= evaluate(arg["hi"], env)
+    if op == "Divisible":
+        return evaluate(arg["x"], env) % evaluate(arg["by"], env) == 0
+    raise AssertionError(f"unknown node {op}")
+
+
+# function -> (loom.sym symbols in the example IR, extents cases)
+CASES = {
+    "matmul": (["tile_m", "tile_n", "tile_k"], [(1024, 1024, 1024), (2048, 256, 256), (48, 40, 24)]),
+    "batch_matmul": (["tile_b", "tile_m", "tile_n", "tile_k"], [(16, 2048, 2048, 2048), (2, 96, 80, 64)]),
+    "split_k_matmul_gather": (["tile_m", "tile_n", "tile_k"], [(512, 512, 16384), (48, 96, 1000)]),
+    "attention": (["tile_b", "tile_m", "tile_n"], [(128, 4096, 4096, 128), (3, 1000, 1000, 64)]),
+    "flash_decode": (["tile_b", "tile_s", "tile_n"], [(32, 32, 128, 8192), (3, 5, 64, 1000)]),
+    "helion_mamba2_chunk_scan_kernel": (["tile_m", "tile_n", "tile_k", "tile_c", "tile_b", "tile_h"],
+                                        [(4, 16, 32, 1, 256, 64, 128), (2, 8, 32, 4, 192, 160, 128)]),
+}
+GRID = [1, 16, 48, 64, 96, 128, 192, 256, 1024]
+SMALL = [1, 2]
+
+
+def _variant(func, binding):
+    return func + "".join(f"__{k}{v}" for k, v in sorted(binding.items()))
+
+
+@pytest.mark.parametrize("func", sorted(CASES))
+def test_scope_accepts_exactly_what_the_kernels_build(func):
+    syms, shapes = CASES[func]
+    for dims in shapes:
+        scope = loom_hip.constraint_scope(func, dims)
+        assert scope["variant_name"] == func
+        meta = scope["constraint_scope"]["metadata"]
+        assert sorted(meta["symbols"]) == sorted(syms)
+        hard = scope["constraint_scope"]["hard_constraints"]
+        # every symbol takes grid values plus its natural upper bound (+1)
+        values = {s: sorted(set((SMALL if s in ("tile_b", "tile_h", "tile_c") else GRID) +
+                                [meta["symbols"][s]["natural_ub"],
+                                 meta["symbols"][s]["natural_ub"] + 1]))
+                  for s in syms}
+        accepted = 0
+        for combo in itertools.product(*(values[s] for s in syms)):
+            env = dict(zip(syms, combo))
+            legal = all(evaluate(c, env) for c in hard)
+            try:
+                loom_hip.check_variant(_variant(func, env), dims)
+                built = True
+            except RuntimeError as e:
+                assert e.code in (1, 2), str(e)
+                built = False
+            assert legal == built, (func, dims, env, legal, built)
+            accepted += legal
+        assert accepted > 0, (func, dims)
+
+
+@pytest.mark.parametrize("func", sorted(CASES))
+def test_preferred_binding_is_legal(func):
+    syms, shapes = CASES[func]
+    for dims in shapes:
+        pref = loom_hip.preferred_block_sizes(func, dims)
+        assert sorted(pref) == sorted(syms)
+        hard = loom_hip.constraint_scope(func, dims)["constraint_scope"]["hard_constraints"]
+        assert all(evaluate(c, pref) for c in hard), (func, dims, pref)
+        loom_hip.check_variant(_variant(func, pref), dims)
+
+
+def test_preferred_bindings_at_baseline_shapes():
+    """The tunings the bench runs."""
+    assert loom_hip.preferred_block_sizes("batch_matmul", (16, 2048, 2048, 2048)) == {
+        "tile_b": 1, "tile_k": 64, "tile_m": 256, "tile_n": 256}
+    assert loom_hip.preferred_block_sizes("attention", (128, 4096, 4096, 128))["tile_m"] == 256
+    assert loom_hip.preferred_block_sizes("flash_decode", (32, 32, 128, 8192))["tile_s"] == 1024
+    # split-K: enough K slabs for a workgroup per CU (BASELINE itself fixes 16 slabs)
+    tk = loom_hip.preferred_block_sizes("split_k_matmul_gather", (512, 512, 16384))["tile_k"]
+    assert 16384 // tk * (512 // 64) ** 2 >= 256
+    m = loom_hip.preferred_block_sizes("helion_mamba2_chunk_scan_kernel", (4, 16, 32, 1, 256, 64, 128))
+    assert (m["tile_m"], m["tile_n"]) == (256, 64)
+
+
+def test_scope_json_round_trips_into_block_sizes_json():
+    """A preferred binding is a valid block_sizes_json entry for the
+    materialization contract, and its variant name parses back."""
+    dims = (16, 2048, 2048, 2048)
+    pref = loom_hip.preferred_block_sizes("batch_matmul", dims)
+    names = loom_hip.materialize_variants(json.dumps({"batch_matmul": pref}), ["batch_matmul"])
+    assert names == ["batch_matmul__tile_b1__tile_k64__tile_m256__tile_n256"]
+    assert loom_hip.parse_variant(names[0]) == ("batch_matmul", pref)
+    loom_hip.check_variant(names[0], dims)
+
+
+def test_unsupported_shapes_and_functions():
+    with pytest.raises(RuntimeError) as ei:
+        loom_hip.constraint_scope("attention", (4, 128, 128, 80))
+    assert ei.value.code == 2
+    with pytest.raises(RuntimeError) as ei:
+        loom_hip.constraint_scope("conv2d", (1, 2, 3))
+    assert ei.value.code == 2
+    with pytest.raises(RuntimeError) as ei:
+        loom_hip.constraint_scope("matmul", (1, 2))
+    assert ei.value.code == 1
+    # TT-style alignment is gone: tile 64 is legal for a 48x40 GEMM, 32 is not
+    hard = loom_hip.constraint_scope("matmul", (48, 40, 24))["constraint_scope"]["hard_constraints"]
+    assert all(evaluate(c, {"tile_m": 64, "tile_n": 64, "tile_k": 24}) for c in hard)
+    assert not all(evaluate(c, {"tile_m": 32, "tile_n": 32, "tile_k": 24}) for c in hard)
