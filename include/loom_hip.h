@@ -141,6 +141,40 @@ int loom_hip_helion_mamba2_chunk_scan_kernel(
     int64_t tile_b, int64_t tile_h, int64_t tile_c, int64_t tile_m, int64_t tile_n,
     int64_t tile_k, void* stream, char* err, size_t errlen);
 
+/* ---- f16 variants ----------------------------------------------------------
+ * The reference's example IR is f16 throughout (EX(*,00) signatures: f16
+ * memrefs).  Each entry point below is its bf16 namesake above with every
+ * 16-bit tensor (inputs and outputs alike) in IEEE binary16 instead: same
+ * arguments, tiles, workspaces, validation and return codes; MFMAs run on
+ * f16 operands (v_mfma_f32_16x16x32_f16) with fp32 accumulation, and every
+ * rounding to f16 is to nearest even.  fp32 tensors (dt, dA_cumsum, D,
+ * prev_states_T, partials) stay fp32. */
+int loom_hip_matmul_f16(const void* x, const void* y, void* out, int64_t M, int64_t N, int64_t K,
+                        int64_t tile_m, int64_t tile_n, int64_t tile_k, void* stream, char* err,
+                        size_t errlen);
+int loom_hip_batch_matmul_f16(const void* arg0, const void* arg1, void* arg2, int64_t B,
+                              int64_t M, int64_t N, int64_t K, int64_t tile_b, int64_t tile_m,
+                              int64_t tile_n, int64_t tile_k, void* stream, char* err,
+                              size_t errlen);
+int loom_hip_split_k_matmul_gather_f16(const void* a, const void* b, void* out, void* partials,
+                                       size_t partials_bytes, int64_t M, int64_t N, int64_t K,
+                                       int64_t tile_m, int64_t tile_n, int64_t tile_k,
+                                       void* stream, char* err, size_t errlen);
+int loom_hip_attention_f16(const void* k, const void* v, const void* q, void* out, int64_t BH,
+                           int64_t Sq, int64_t Skv, int64_t D, float scale, int causal,
+                           int64_t tile_b, int64_t tile_m, int64_t tile_n, void* stream,
+                           char* err, size_t errlen);
+int loom_hip_flash_decode_f16(const void* k, const void* v, const void* q, void* out,
+                              void* workspace, size_t workspace_bytes, int64_t B, int64_t H,
+                              int64_t D, int64_t S, float scale, int64_t tile_b, int64_t tile_s,
+                              int64_t tile_n, void* stream, char* err, size_t errlen);
+int loom_hip_helion_mamba2_chunk_scan_kernel_f16(
+    const void* cb, const void* x, const void* dt, const void* dA_cumsum, const void* C,
+    const void* D, const void* prev_states_T, void* out, int64_t batch, int64_t nchunks,
+    int64_t nheads, int64_t ngroups, int64_t chunk_size, int64_t headdim, int64_t dstate,
+    int64_t tile_b, int64_t tile_h, int64_t tile_c, int64_t tile_m, int64_t tile_n,
+    int64_t tile_k, void* stream, char* err, size_t errlen);
+
 /* ---- Mamba-2 SSD prologue --------------------------------------------------
  * The chunk-scan example takes cb, dA_cumsum and prev_states_T ready-made
  * (examples/mamba_chunk_scan/IR/00_from_helion_frontend.mlir:4); the
@@ -180,6 +214,21 @@ int loom_hip_ssd_prologue(const void* x, const void* dt, const void* A, const vo
                           int64_t batch, int64_t nchunks, int64_t nheads, int64_t ngroups,
                           int64_t chunk_size, int64_t headdim, int64_t dstate, void* stream,
                           char* err, size_t errlen);
+
+/* f16 forms of the SSD stages whose tensors are 16-bit (x, B, C, cb). */
+int loom_hip_ssd_bmm_chunk_f16(const void* B, const void* C, void* cb, int64_t batch,
+                               int64_t nchunks, int64_t ngroups, int64_t chunk_size,
+                               int64_t dstate, void* stream, char* err, size_t errlen);
+int loom_hip_ssd_chunk_state_passing_f16(const void* x, const void* dt, const void* dA_cumsum,
+                                         const void* B, void* prev_states_T, int64_t batch,
+                                         int64_t nchunks, int64_t nheads, int64_t ngroups,
+                                         int64_t chunk_size, int64_t headdim, int64_t dstate,
+                                         void* stream, char* err, size_t errlen);
+int loom_hip_ssd_prologue_f16(const void* x, const void* dt, const void* A, const void* B,
+                              const void* C, void* dA_cumsum, void* cb, void* prev_states_T,
+                              int64_t batch, int64_t nchunks, int64_t nheads, int64_t ngroups,
+                              int64_t chunk_size, int64_t headdim, int64_t dstate, void* stream,
+                              char* err, size_t errlen);
 
 /* ---- materialization contract and by-name dispatch ---------------------- */
 
@@ -224,6 +273,13 @@ int loom_hip_parse_variant(const char* variant, char* func, size_t funclen, int6
 int loom_hip_dispatch(const char* variant, void* const* tensors, int ntensors,
                       const int64_t* dims, int ndims, float scale, int causal, void* workspace,
                       size_t workspace_bytes, void* stream, char* err, size_t errlen);
+
+/* loom_hip_dispatch for variants whose 16-bit tensors are f16 (the
+ * reference's own element type): launches the *_f16 entry points. */
+int loom_hip_dispatch_f16(const char* variant, void* const* tensors, int ntensors,
+                          const int64_t* dims, int ndims, float scale, int causal,
+                          void* workspace, size_t workspace_bytes, void* stream, char* err,
+                          size_t errlen);
 
 /* Validates a materialized variant against its extents exactly as
  * loom_hip_dispatch would -- same checks, same codes and messages -- and

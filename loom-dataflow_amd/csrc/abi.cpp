@@ -636,6 +636,72 @@ int copy_out(const std::string& js_, char* out, size_t outlen, char* err, size_t
 
 thread_local bool g_validate_only = false;
 
+template <bool F16>
+int dispatch_impl(const char* variant, void* const* tensors, int ntensors,
+                      const int64_t* dims, int ndims, float scale, int causal,
+                      void* workspace, size_t workspace_bytes, void* stream, char* err,
+                      size_t errlen) {
+  if (!variant || (ntensors > 0 && !tensors) || (ndims > 0 && !dims))
+    return fail(err, errlen, LOOM_HIP_EINVAL, "dispatch: null argument");
+  std::string f, perr;
+  int64_t t[LOOM_HIP_NTILES];
+  int rc = parse_variant(variant, f, t, perr);
+  if (rc) return fail(err, errlen, rc, "dispatch: %s", perr.c_str());
+  if (!known_function(f))
+    return fail(err, errlen, LOOM_HIP_EUNSUP, "dispatch: no gfx950 kernel for function '%s'",
+                f.c_str());
+  auto shape = [&](int nt, int nd) {
+    if (ntensors != nt || ndims != nd)
+      return fail(err, errlen, LOOM_HIP_EINVAL,
+                  "dispatch: %s takes %d tensors and %d extents (got %d and %d)", f.c_str(), nt,
+                  nd, ntensors, ndims);
+    return (int)LOOM_HIP_OK;
+  };
+  if (f == "matmul") {
+    if ((rc = shape(3, 3)) || (rc = need_tiles(f, t, {1, 2, 3}, err, errlen))) return rc;
+    const auto fn = F16 ? loom_hip_matmul_f16 : loom_hip_matmul;
+    return fn(tensors[0], tensors[1], tensors[2], dims[0], dims[1], dims[2], t[LOOM_HIP_TILE_M],
+              t[LOOM_HIP_TILE_N], t[LOOM_HIP_TILE_K], stream, err, errlen);
+  }
+  if (f == "batch_matmul") {
+    if ((rc = shape(3, 4)) || (rc = need_tiles(f, t, {0, 1, 2, 3}, err, errlen))) return rc;
+    const auto fn = F16 ? loom_hip_batch_matmul_f16 : loom_hip_batch_matmul;
+    return fn(tensors[0], tensors[1], tensors[2], dims[0], dims[1], dims[2], dims[3],
+              t[LOOM_HIP_TILE_B], t[LOOM_HIP_TILE_M], t[LOOM_HIP_TILE_N], t[LOOM_HIP_TILE_K],
+              stream, err, errlen);
+  }
+  if (f == "split_k_matmul_gather") {
+    if ((rc = shape(3, 3)) || (rc = need_tiles(f, t, {1, 2, 3}, err, errlen))) return rc;
+    const auto fn = F16 ? loom_hip_split_k_matmul_gather_f16 : loom_hip_split_k_matmul_gather;
+    return fn(tensors[0], tensors[1], tensors[2], workspace, workspace_bytes, dims[0], dims[1],
+              dims[2], t[LOOM_HIP_TILE_M], t[LOOM_HIP_TILE_N], t[LOOM_HIP_TILE_K], stream, err,
+              errlen);
+  }
+  if (f == "attention") {
+    if ((rc = shape(4, 4)) || (rc = need_tiles(f, t, {0, 1, 2}, err, errlen))) return rc;
+    const auto fn = F16 ? loom_hip_attention_f16 : loom_hip_attention;
+    return fn(tensors[0], tensors[1], tensors[2], tensors[3], dims[0], dims[1], dims[2], dims[3],
+              scale, causal, t[LOOM_HIP_TILE_B], t[LOOM_HIP_TILE_M], t[LOOM_HIP_TILE_N], stream,
+              err, errlen);
+  }
+  if (f == "flash_decode") {
+    if ((rc = shape(4, 4)) || (rc = need_tiles(f, t, {0, 2, 4}, err, errlen))) return rc;
+    const auto fn = F16 ? loom_hip_flash_decode_f16 : loom_hip_flash_decode;
+    return fn(tensors[0], tensors[1], tensors[2], tensors[3], workspace, workspace_bytes, dims[0],
+              dims[1], dims[2], dims[3], scale, t[LOOM_HIP_TILE_B], t[LOOM_HIP_TILE_S],
+              t[LOOM_HIP_TILE_N], stream, err, errlen);
+  }
+  // helion_mamba2_chunk_scan_kernel
+  if ((rc = shape(8, 7)) || (rc = need_tiles(f, t, {0, 1, 2, 3, 5, 6}, err, errlen))) return rc;
+  const auto fn =
+      F16 ? loom_hip_helion_mamba2_chunk_scan_kernel_f16 : loom_hip_helion_mamba2_chunk_scan_kernel;
+  return fn(tensors[0], tensors[1], tensors[2], tensors[3], tensors[4], tensors[5], tensors[6],
+            tensors[7], dims[0], dims[1], dims[2], dims[3], dims[4], dims[5], dims[6],
+            t[LOOM_HIP_TILE_B], t[LOOM_HIP_TILE_H], t[LOOM_HIP_TILE_C], t[LOOM_HIP_TILE_M],
+            t[LOOM_HIP_TILE_N], t[LOOM_HIP_TILE_K], stream, err, errlen);
+}
+
+
 }  // namespace
 
 // entry points check this before launching (declared in csrc/common.h)
@@ -842,61 +908,16 @@ int loom_hip_dispatch(const char* variant, void* const* tensors, int ntensors,
                       const int64_t* dims, int ndims, float scale, int causal,
                       void* workspace, size_t workspace_bytes, void* stream, char* err,
                       size_t errlen) {
-  if (!variant || (ntensors > 0 && !tensors) || (ndims > 0 && !dims))
-    return fail(err, errlen, LOOM_HIP_EINVAL, "dispatch: null argument");
-  std::string f, perr;
-  int64_t t[LOOM_HIP_NTILES];
-  int rc = parse_variant(variant, f, t, perr);
-  if (rc) return fail(err, errlen, rc, "dispatch: %s", perr.c_str());
-  if (!known_function(f))
-    return fail(err, errlen, LOOM_HIP_EUNSUP, "dispatch: no gfx950 kernel for function '%s'",
-                f.c_str());
-  auto shape = [&](int nt, int nd) {
-    if (ntensors != nt || ndims != nd)
-      return fail(err, errlen, LOOM_HIP_EINVAL,
-                  "dispatch: %s takes %d tensors and %d extents (got %d and %d)", f.c_str(), nt,
-                  nd, ntensors, ndims);
-    return (int)LOOM_HIP_OK;
-  };
-  if (f == "matmul") {
-    if ((rc = shape(3, 3)) || (rc = need_tiles(f, t, {1, 2, 3}, err, errlen))) return rc;
-    return loom_hip_matmul(tensors[0], tensors[1], tensors[2], dims[0], dims[1], dims[2],
-                           t[LOOM_HIP_TILE_M], t[LOOM_HIP_TILE_N], t[LOOM_HIP_TILE_K], stream,
-                           err, errlen);
-  }
-  if (f == "batch_matmul") {
-    if ((rc = shape(3, 4)) || (rc = need_tiles(f, t, {0, 1, 2, 3}, err, errlen))) return rc;
-    return loom_hip_batch_matmul(tensors[0], tensors[1], tensors[2], dims[0], dims[1], dims[2],
-                                 dims[3], t[LOOM_HIP_TILE_B], t[LOOM_HIP_TILE_M],
-                                 t[LOOM_HIP_TILE_N], t[LOOM_HIP_TILE_K], stream, err, errlen);
-  }
-  if (f == "split_k_matmul_gather") {
-    if ((rc = shape(3, 3)) || (rc = need_tiles(f, t, {1, 2, 3}, err, errlen))) return rc;
-    return loom_hip_split_k_matmul_gather(tensors[0], tensors[1], tensors[2], workspace,
-                                          workspace_bytes, dims[0], dims[1], dims[2],
-                                          t[LOOM_HIP_TILE_M], t[LOOM_HIP_TILE_N],
-                                          t[LOOM_HIP_TILE_K], stream, err, errlen);
-  }
-  if (f == "attention") {
-    if ((rc = shape(4, 4)) || (rc = need_tiles(f, t, {0, 1, 2}, err, errlen))) return rc;
-    return loom_hip_attention(tensors[0], tensors[1], tensors[2], tensors[3], dims[0], dims[1],
-                              dims[2], dims[3], scale, causal, t[LOOM_HIP_TILE_B],
-                              t[LOOM_HIP_TILE_M], t[LOOM_HIP_TILE_N], stream, err, errlen);
-  }
-  if (f == "flash_decode") {
-    if ((rc = shape(4, 4)) || (rc = need_tiles(f, t, {0, 2, 4}, err, errlen))) return rc;
-    return loom_hip_flash_decode(tensors[0], tensors[1], tensors[2], tensors[3], workspace,
-                                 workspace_bytes, dims[0], dims[1], dims[2], dims[3], scale,
-                                 t[LOOM_HIP_TILE_B], t[LOOM_HIP_TILE_S], t[LOOM_HIP_TILE_N],
-                                 stream, err, errlen);
-  }
-  // helion_mamba2_chunk_scan_kernel
-  if ((rc = shape(8, 7)) || (rc = need_tiles(f, t, {0, 1, 2, 3, 5, 6}, err, errlen))) return rc;
-  return loom_hip_helion_mamba2_chunk_scan_kernel(
-      tensors[0], tensors[1], tensors[2], tensors[3], tensors[4], tensors[5], tensors[6],
-      tensors[7], dims[0], dims[1], dims[2], dims[3], dims[4], dims[5], dims[6],
-      t[LOOM_HIP_TILE_B], t[LOOM_HIP_TILE_H], t[LOOM_HIP_TILE_C], t[LOOM_HIP_TILE_M],
-      t[LOOM_HIP_TILE_N], t[LOOM_HIP_TILE_K], stream, err, errlen);
+  return dispatch_impl<false>(variant, tensors, ntensors, dims, ndims, scale, causal, workspace,
+                              workspace_bytes, stream, err, errlen);
+}
+
+int loom_hip_dispatch_f16(const char* variant, void* const* tensors, int ntensors,
+                          const int64_t* dims, int ndims, float scale, int causal,
+                          void* workspace, size_t workspace_bytes, void* stream, char* err,
+                          size_t errlen) {
+  return dispatch_impl<true>(variant, tensors, ntensors, dims, ndims, scale, causal, workspace,
+                             workspace_bytes, stream, err, errlen);
 }
 
 }  // extern "C"

@@ -46,7 +46,7 @@ struct AttnParams {
 // Ks rows (128 B) and Vs rows (2 D bytes) XOR their 16-byte chunk index with
 // 2 (row & 3), so a transposed read's four rows hit distinct banks.
 // ---------------------------------------------------------------------------
-template <int D, int QT, int W>
+template <int D, int QT, int W, bool H>
 __global__ void __launch_bounds__(64 * W) attention_dma_kernel(AttnParams p) {
   constexpr int KB = 64;                        // keys per stage
   constexpr int NS = 4;                         // stages
@@ -127,8 +127,7 @@ __global__ void __launch_bounds__(64 * W) attention_dma_kernel(AttnParams p) {
           *reinterpret_cast<const u32x4_t*>(qg + (int64_t)qrow * D + ds * 32 + g * 8);
 #pragma unroll
       for (int e = 0; e < 4; ++e)
-        qf[ds][qt][e] = pack_bf16x2(__uint_as_float(raw[e] << 16) * p.c2,
-                                    __uint_as_float(raw[e] & 0xffff0000u) * p.c2);
+        qf[ds][qt][e] = pack2<H>(lo16<H>(raw[e]) * p.c2, hi16<H>(raw[e]) * p.c2);
     }
   }
 
@@ -136,7 +135,7 @@ __global__ void __launch_bounds__(64 * W) attention_dma_kernel(AttnParams p) {
   // MFMA of P^T against ones: every row of that tile holds l) share it
   float m_run[QT];
   f32x4_t ot[DT][QT], lacc[QT];
-  const u32x4_t ones = u32x4_t{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
+  const u32x4_t ones = u32x4_t{kOnePair<H>, kOnePair<H>, kOnePair<H>, kOnePair<H>};
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
     m_run[qt] = 0.f;
@@ -177,7 +176,7 @@ __global__ void __launch_bounds__(64 * W) attention_dma_kernel(AttnParams p) {
           const u32x2_t hi = lds_read_tr16(q + 4 * (KB * 2));
           const u32x4_t kf = u32x4_t{lo[0], lo[1], hi[0], hi[1]};
 #pragma unroll
-          for (int qt = 0; qt < QT; ++qt) st[j][qt] = mfma16(kf, qf[ds][qt], st[j][qt]);
+          for (int qt = 0; qt < QT; ++qt) st[j][qt] = mfma16t<H>(kf, qf[ds][qt], st[j][qt]);
         }
       }
       // ---- masking (only blocks that reach past Skv or the diagonal)
@@ -240,9 +239,9 @@ __global__ void __launch_bounds__(64 * W) attention_dma_kernel(AttnParams p) {
           e0[i] = fast_exp2(st[0][qt][i]);
           e1[i] = fast_exp2(st[1][qt][i]);
         }
-        pf[qt] = u32x4_t{pack_bf16x2(e0[0], e0[1]), pack_bf16x2(e0[2], e0[3]),
-                         pack_bf16x2(e1[0], e1[1]), pack_bf16x2(e1[2], e1[3])};
-        lacc[qt] = mfma16(ones, pf[qt], lacc[qt]);
+        pf[qt] = u32x4_t{pack2<H>(e0[0], e0[1]), pack2<H>(e0[2], e0[3]),
+                         pack2<H>(e1[0], e1[1]), pack2<H>(e1[2], e1[3])};
+        lacc[qt] = mfma16t<H>(ones, pf[qt], lacc[qt]);
       }
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
@@ -253,7 +252,7 @@ __global__ void __launch_bounds__(64 * W) attention_dma_kernel(AttnParams p) {
         const u32x2_t hi = lds_read_tr16(q + 16 * VROW);    // keys 32h + 16 + 4g + 0..3
         const u32x4_t vf = u32x4_t{lo[0], lo[1], hi[0], hi[1]};
 #pragma unroll
-        for (int qt = 0; qt < QT; ++qt) ot[dt][qt] = mfma16(vf, pf[qt], ot[dt][qt]);
+        for (int qt = 0; qt < QT; ++qt) ot[dt][qt] = mfma16t<H>(vf, pf[qt], ot[dt][qt]);
       }
     }
   };
@@ -290,17 +289,14 @@ __global__ void __launch_bounds__(64 * W) attention_dma_kernel(AttnParams p) {
       for (int dt = 0; dt < DT; ++dt) {
         const f32x4_t o = ot[dt][qt];
         *reinterpret_cast<u32x2_t*>(orow + dt * 16 + 4 * g) =
-            u32x2_t{pack_bf16x2(o[0] * inv, o[1] * inv), pack_bf16x2(o[2] * inv, o[3] * inv)};
+            u32x2_t{pack2<H>(o[0] * inv, o[1] * inv), pack2<H>(o[2] * inv, o[3] * inv)};
       }
     }
   }
 }
 
-}  // namespace
-
-extern "C" {
-
-int loom_hip_attention(const void* k, const void* v, const void* q, void* out, int64_t BH,
+template <bool H>
+int attention_impl(const void* k, const void* v, const void* q, void* out, int64_t BH,
                        int64_t Sq, int64_t Skv, int64_t D, float scale, int causal,
                        int64_t tile_b, int64_t tile_m, int64_t tile_n, void* stream, char* err,
                        size_t errlen) {
@@ -344,17 +340,36 @@ int loom_hip_attention(const void* k, const void* v, const void* q, void* out, i
   {
     const dim3 grid((unsigned)(p.BH * p.nqt)), b4(256), b8(512);
     switch ((D == 128 ? 10 : 0) + (int)(tile_m / 64)) {
-      case 11: hipLaunchKernelGGL((attention_dma_kernel<128, 1, 4>), grid, b4, 0, st, p); break;
-      case 12: hipLaunchKernelGGL((attention_dma_kernel<128, 1, 8>), grid, b8, 0, st, p); break;
-      case 13: hipLaunchKernelGGL((attention_dma_kernel<128, 3, 4>), grid, b4, 0, st, p); break;
-      case 14: hipLaunchKernelGGL((attention_dma_kernel<128, 2, 8>), grid, b8, 0, st, p); break;
-      case 1: hipLaunchKernelGGL((attention_dma_kernel<64, 1, 4>), grid, b4, 0, st, p); break;
-      case 2: hipLaunchKernelGGL((attention_dma_kernel<64, 1, 8>), grid, b8, 0, st, p); break;
-      case 3: hipLaunchKernelGGL((attention_dma_kernel<64, 3, 4>), grid, b4, 0, st, p); break;
-      default: hipLaunchKernelGGL((attention_dma_kernel<64, 2, 8>), grid, b8, 0, st, p); break;
+      case 11: hipLaunchKernelGGL((attention_dma_kernel<128, 1, 4, H>), grid, b4, 0, st, p); break;
+      case 12: hipLaunchKernelGGL((attention_dma_kernel<128, 1, 8, H>), grid, b8, 0, st, p); break;
+      case 13: hipLaunchKernelGGL((attention_dma_kernel<128, 3, 4, H>), grid, b4, 0, st, p); break;
+      case 14: hipLaunchKernelGGL((attention_dma_kernel<128, 2, 8, H>), grid, b8, 0, st, p); break;
+      case 1: hipLaunchKernelGGL((attention_dma_kernel<64, 1, 4, H>), grid, b4, 0, st, p); break;
+      case 2: hipLaunchKernelGGL((attention_dma_kernel<64, 1, 8, H>), grid, b8, 0, st, p); break;
+      case 3: hipLaunchKernelGGL((attention_dma_kernel<64, 3, 4, H>), grid, b4, 0, st, p); break;
+      default: hipLaunchKernelGGL((attention_dma_kernel<64, 2, 8, H>), grid, b8, 0, st, p); break;
     }
   }
   return loom_check_launch(err, errlen, "attention");
+}
+
+}  // namespace
+
+extern "C" {
+
+int loom_hip_attention(const void* k, const void* v, const void* q, void* out, int64_t BH,
+                       int64_t Sq, int64_t Skv, int64_t D, float scale, int causal,
+                       int64_t tile_b, int64_t tile_m, int64_t tile_n, void* stream, char* err,
+                       size_t errlen) {
+  return attention_impl<false>(k, v, q, out, BH, Sq, Skv, D, scale, causal, tile_b, tile_m,
+                               tile_n, stream, err, errlen);
+}
+int loom_hip_attention_f16(const void* k, const void* v, const void* q, void* out, int64_t BH,
+                           int64_t Sq, int64_t Skv, int64_t D, float scale, int causal,
+                           int64_t tile_b, int64_t tile_m, int64_t tile_n, void* stream,
+                           char* err, size_t errlen) {
+  return attention_impl<true>(k, v, q, out, BH, Sq, Skv, D, scale, causal, tile_b, tile_m,
+                              tile_n, stream, err, errlen);
 }
 
 }  // extern "C"

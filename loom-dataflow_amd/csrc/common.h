@@ -15,6 +15,8 @@
 
 #include <algorithm>
 
+#include "../../include/loom_hip.h"   // every entry point matches its declaration
+
 // ---------------------------------------------------------------------------
 // vector types for the gfx950 bf16 MFMA builtins
 // ---------------------------------------------------------------------------
@@ -54,6 +56,58 @@ LOOM_DEV f32x4_t mfma16(const u32x4_t& a, const u32x4_t& b, const f32x4_t& c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
                                                  __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
 }
+
+// ---------------------------------------------------------------------------
+// 16-bit element type: kernels are templated on H (false = bf16, true =
+// IEEE f16, the reference's own element type).  Both travel as raw 16-bit
+// patterns; only the MFMA, the fp32 -> 16-bit rounding (round to nearest
+// even in both cases) and the 16-bit -> fp32 widening differ.
+// ---------------------------------------------------------------------------
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+
+template <bool H>
+LOOM_DEV f32x4_t mfma16t(const u32x4_t& a, const u32x4_t& b, const f32x4_t& c) {
+  if constexpr (H)
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+  else
+    return mfma16(a, b, c);
+}
+// two fp32 -> one dword (lo = a, hi = b) in the element type
+template <bool H>
+LOOM_DEV uint32_t pack2(float a, float b) {
+  if constexpr (H)
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, f16x2_t));
+  else
+    return pack_bf16x2(a, b);
+}
+// one fp32 -> element bits
+template <bool H>
+LOOM_DEV uint32_t cvt16(float a) {
+  if constexpr (H)
+    return __builtin_bit_cast(uint16_t, (_Float16)a);
+  else
+    return f2bf(a);
+}
+// low / high element of a dword -> fp32 (exact)
+template <bool H>
+LOOM_DEV float lo16(uint32_t w) {
+  if constexpr (H)
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(w & 0xffffu));
+  else
+    return bf2f_lo(w);
+}
+template <bool H>
+LOOM_DEV float hi16(uint32_t w) {
+  if constexpr (H)
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
+  else
+    return bf2f_hi(w);
+}
+// a dword holding two 1.0s
+template <bool H>
+constexpr uint32_t kOnePair = H ? 0x3C003C00u : 0x3F803F80u;
 
 // Pack the low (pack_lo) or high (pack_hi) 16-bit halves of two dwords:
 // result low half from x, high half from y.  One v_perm_b32 each: the

@@ -49,7 +49,7 @@ struct DecodeParams {
 // (w_s = exp(lse_s - M) / den, ascending s) for its D/64 values of d with
 // eight splits' loads in flight at a time.  Splits beyond 64 are taken in
 // chunks of 64.
-template <int D>
+template <int D, bool F16>
 __global__ void __launch_bounds__(256) decode_combine_kernel(DecodeParams p) {
   constexpr int DPL = D / 64;  // d values per lane
   const int lane = threadIdx.x & 63;
@@ -89,9 +89,9 @@ __global__ void __launch_bounds__(256) decode_combine_kernel(DecodeParams p) {
   }
   uint16_t* dst = p.out + bh * D + lane * DPL;
   if constexpr (DPL == 2)
-    *reinterpret_cast<uint32_t*>(dst) = pack_bf16x2(acc[0], acc[1]);
+    *reinterpret_cast<uint32_t*>(dst) = pack2<F16>(acc[0], acc[1]);
   else
-    dst[0] = (uint16_t)f2bf(acc[0]);
+    dst[0] = (uint16_t)cvt16<F16>(acc[0]);
 }
 
 // D = head dim (64 or 128), HT = head tiles of 16, ALIGNED = S is a
@@ -105,7 +105,7 @@ __global__ void __launch_bounds__(256) decode_combine_kernel(DecodeParams p) {
 // the latency.  All loads are raw buffer loads: anything past the tensor
 // reads as zero, and keys past the split end are masked to -inf before the
 // softmax (so their V rows are multiplied by exactly 0).
-template <int D, int HT, bool ALIGNED>
+template <int D, int HT, bool ALIGNED, bool F16>
 __global__ void __launch_bounds__(64 * kWaves) decode_split_kernel(DecodeParams p) {
   constexpr int VEC = D / 16;     // d values per lane per V row, also # of d tiles
   constexpr int DSTEPS = D / 32;  // 32-deep MFMA steps over d
@@ -223,7 +223,8 @@ __global__ void __launch_bounds__(64 * kWaves) decode_split_kernel(DecodeParams 
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
-          for (int ht = 0; ht < HT; ++ht) st_acc[j][ht] = mfma16(kt[j], sm_q[st][ht][lane], st_acc[j][ht]);
+          for (int ht = 0; ht < HT; ++ht)
+            st_acc[j][ht] = mfma16t<F16>(kt[j], sm_q[st][ht][lane], st_acc[j][ht]);
       }
       if (st == DSTEPS - 1) {
         // ---- online softmax (log2 domain); st_acc[j][ht][i] is the score of
@@ -270,10 +271,10 @@ __global__ void __launch_bounds__(64 * kWaves) decode_split_kernel(DecodeParams 
         u32x4_t pf[HT];
 #pragma unroll
         for (int ht = 0; ht < HT; ++ht)
-          pf[ht] = u32x4_t{pack_bf16x2(st_acc[j0][ht][0], st_acc[j0][ht][1]),
-                           pack_bf16x2(st_acc[j0][ht][2], st_acc[j0][ht][3]),
-                           pack_bf16x2(st_acc[j1][ht][0], st_acc[j1][ht][1]),
-                           pack_bf16x2(st_acc[j1][ht][2], st_acc[j1][ht][3])};
+          pf[ht] = u32x4_t{pack2<F16>(st_acc[j0][ht][0], st_acc[j0][ht][1]),
+                           pack2<F16>(st_acc[j0][ht][2], st_acc[j0][ht][3]),
+                           pack2<F16>(st_acc[j1][ht][0], st_acc[j1][ht][1]),
+                           pack2<F16>(st_acc[j1][ht][2], st_acc[j1][ht][3])};
         // transpose: va[u] = V[key_t][VEC r + u] for slots t = 0..7
         u32x4_t va[VEC];
 #pragma unroll
@@ -286,7 +287,7 @@ __global__ void __launch_bounds__(64 * kWaves) decode_split_kernel(DecodeParams 
 #pragma unroll
         for (int u = 0; u < VEC; ++u)
 #pragma unroll
-          for (int ht = 0; ht < HT; ++ht) ot[u][ht] = mfma16(va[u], pf[ht], ot[u][ht]);
+          for (int ht = 0; ht < HT; ++ht) ot[u][ht] = mfma16t<F16>(va[u], pf[ht], ot[u][ht]);
       }
     }
   }
@@ -330,13 +331,13 @@ __global__ void __launch_bounds__(64 * kWaves) decode_split_kernel(DecodeParams 
 
 }
 
-template <int D, int HT>
+template <int D, int HT, bool F16>
 void launch_split(const DecodeParams& p, bool aligned, hipStream_t st) {
   const dim3 grid(p.ns, p.B), block(64 * kWaves);
   if (aligned)
-    hipLaunchKernelGGL((decode_split_kernel<D, HT, true>), grid, block, 0, st, p);
+    hipLaunchKernelGGL((decode_split_kernel<D, HT, true, F16>), grid, block, 0, st, p);
   else
-    hipLaunchKernelGGL((decode_split_kernel<D, HT, false>), grid, block, 0, st, p);
+    hipLaunchKernelGGL((decode_split_kernel<D, HT, false, F16>), grid, block, 0, st, p);
 }
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -344,18 +345,8 @@ size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 
 
-}  // namespace
-
-extern "C" {
-
-size_t loom_hip_flash_decode_workspace_bytes(int64_t B, int64_t H, int64_t D, int64_t S,
-                                             int64_t tile_s) {
-  if (B <= 0 || H <= 0 || D <= 0 || S <= 0 || tile_s <= 0) return 0;
-  const size_t ns = (size_t)cdiv64(S, tile_s);
-  return align256(ns * B * H * sizeof(float)) + ns * B * H * D * sizeof(float);
-}
-
-int loom_hip_flash_decode(const void* k, const void* v, const void* q, void* out,
+template <bool F16>
+int flash_decode_impl(const void* k, const void* v, const void* q, void* out,
                           void* workspace, size_t workspace_bytes, int64_t B, int64_t H,
                           int64_t D, int64_t S, float scale, int64_t tile_b, int64_t tile_s,
                           int64_t tile_n, void* stream, char* err, size_t errlen) {
@@ -402,18 +393,44 @@ int loom_hip_flash_decode(const void* k, const void* v, const void* q, void* out
   if (loom_validate_only()) return loom_ok(err, errlen);
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (D == 128) {
-    if (H > 16) launch_split<128, 2>(p, al, st); else launch_split<128, 1>(p, al, st);
+    if (H > 16) launch_split<128, 2, F16>(p, al, st); else launch_split<128, 1, F16>(p, al, st);
   } else {
-    if (H > 16) launch_split<64, 2>(p, al, st); else launch_split<64, 1>(p, al, st);
+    if (H > 16) launch_split<64, 2, F16>(p, al, st); else launch_split<64, 1, F16>(p, al, st);
   }
   int rc = loom_check_launch(err, errlen, "flash_decode (split)");
   if (rc) return rc;
   const dim3 cgrid((unsigned)cdiv64(B * H, 4)), cblock(256);
   if (D == 128)
-    hipLaunchKernelGGL(decode_combine_kernel<128>, cgrid, cblock, 0, st, p);
+    hipLaunchKernelGGL((decode_combine_kernel<128, F16>), cgrid, cblock, 0, st, p);
   else
-    hipLaunchKernelGGL(decode_combine_kernel<64>, cgrid, cblock, 0, st, p);
+    hipLaunchKernelGGL((decode_combine_kernel<64, F16>), cgrid, cblock, 0, st, p);
   return loom_check_launch(err, errlen, "flash_decode (combine)");
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t loom_hip_flash_decode_workspace_bytes(int64_t B, int64_t H, int64_t D, int64_t S,
+                                             int64_t tile_s) {
+  if (B <= 0 || H <= 0 || D <= 0 || S <= 0 || tile_s <= 0) return 0;
+  const size_t ns = (size_t)cdiv64(S, tile_s);
+  return align256(ns * B * H * sizeof(float)) + ns * B * H * D * sizeof(float);
+}
+
+int loom_hip_flash_decode(const void* k, const void* v, const void* q, void* out,
+                          void* workspace, size_t workspace_bytes, int64_t B, int64_t H,
+                          int64_t D, int64_t S, float scale, int64_t tile_b, int64_t tile_s,
+                          int64_t tile_n, void* stream, char* err, size_t errlen) {
+  return flash_decode_impl<false>(k, v, q, out, workspace, workspace_bytes, B, H, D, S, scale,
+                                  tile_b, tile_s, tile_n, stream, err, errlen);
+}
+int loom_hip_flash_decode_f16(const void* k, const void* v, const void* q, void* out,
+                              void* workspace, size_t workspace_bytes, int64_t B, int64_t H,
+                              int64_t D, int64_t S, float scale, int64_t tile_b, int64_t tile_s,
+                              int64_t tile_n, void* stream, char* err, size_t errlen) {
+  return flash_decode_impl<true>(k, v, q, out, workspace, workspace_bytes, B, H, D, S, scale,
+                                 tile_b, tile_s, tile_n, stream, err, errlen);
 }
 
 }  // extern "C"

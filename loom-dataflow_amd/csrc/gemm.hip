@@ -39,7 +39,7 @@ struct GemmParams {
   int tiles_m, tiles_n, nz;
 };
 
-template <int BM, int BN, int WM, int WN, bool ALIGNED, bool OUT_F32>
+template <int BM, int BN, int WM, int WN, bool ALIGNED, bool OUT_F32, bool H>
 __global__ void __launch_bounds__(64 * WM * WN) gemm_bf16_kernel(GemmParams p) {
   constexpr int NT = 64 * WM * WN;
   constexpr int HALF = NT / 2;
@@ -185,7 +185,7 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_bf16_kernel(GemmParams p) {
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = mfma16(af[i], bfr[j], acc[i][j]);
+        for (int j = 0; j < TN; ++j) acc[i][j] = mfma16t<H>(af[i], bfr[j], acc[i][j]);
     }
   };
 
@@ -215,7 +215,7 @@ __global__ void __launch_bounds__(64 * WM * WN) gemm_bf16_kernel(GemmParams p) {
           if constexpr (OUT_F32)
             static_cast<float*>(p.C)[coff + row * p.ldc + col] = acc[i][j][r];
           else
-            static_cast<uint16_t*>(p.C)[coff + row * p.ldc + col] = (uint16_t)f2bf(acc[i][j][r]);
+            static_cast<uint16_t*>(p.C)[coff + row * p.ldc + col] = (uint16_t)cvt16<H>(acc[i][j][r]);
         }
       }
     }
@@ -260,7 +260,7 @@ LOOM_DEV int a_swz(int row) {
 // separates the next 16 lanes' rows (k + 8) within a 256-byte window.
 LOOM_DEV int b_swz(int k) { return (2 * (k & 3)) ^ (8 * ((k >> 3) & 1)); }
 
-template <int BK, int NS, bool OUT_F32>
+template <int BK, int NS, bool OUT_F32, bool H>
 __global__ void __launch_bounds__(256) gemm_dma_kernel(GemmParams p) {
   constexpr int BM = 256, BN = 256;
   constexpr int A_BYTES = BM * BK * 2, B_BYTES = BK * BN * 2;
@@ -375,7 +375,7 @@ __global__ void __launch_bounds__(256) gemm_dma_kernel(GemmParams p) {
         const u32x2_t hi = lds_read_tr16(q + 4 * 512);
         const u32x4_t bf = u32x4_t{lo[0], lo[1], hi[0], hi[1]};
 #pragma unroll
-        for (int tm = 0; tm < 8; ++tm) acc[tn][tm] = mfma16(bf, af[tm], acc[tn][tm]);
+        for (int tm = 0; tm < 8; ++tm) acc[tn][tm] = mfma16t<H>(bf, af[tm], acc[tn][tm]);
       }
     }
   };
@@ -421,13 +421,14 @@ __global__ void __launch_bounds__(256) gemm_dma_kernel(GemmParams p) {
         *reinterpret_cast<f32x4_t*>(static_cast<float*>(p.C) + (int64_t)z * p.zc + row * p.ldc + col) = v;
       else
         *reinterpret_cast<u32x2_t*>(static_cast<uint16_t*>(p.C) + (int64_t)z * p.zc + row * p.ldc + col) =
-            u32x2_t{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+            u32x2_t{pack2<H>(v[0], v[1]), pack2<H>(v[2], v[3])};
     }
   }
 }
 
 // out[e] = bf16( sum_{s ascending} G[s][e] ) -- the split-0 reduction of
 // examples/split_k_mm_gather/IR/00_from_helion_frontend.mlir:34-51.
+template <bool H>
 __global__ void __launch_bounds__(256) splitk_reduce_vec4(const float* __restrict__ G,
                                                           uint16_t* __restrict__ out,
                                                           int64_t MN, int S) {
@@ -442,11 +443,12 @@ __global__ void __launch_bounds__(256) splitk_reduce_vec4(const float* __restric
       s[2] += v[2];
       s[3] += v[3];
     }
-    u32x2_t o{pack_bf16x2(s[0], s[1]), pack_bf16x2(s[2], s[3])};
+    u32x2_t o{pack2<H>(s[0], s[1]), pack2<H>(s[2], s[3])};
     *reinterpret_cast<u32x2_t*>(out + q * 4) = o;
   }
 }
 
+template <bool H>
 __global__ void __launch_bounds__(256) splitk_reduce_scalar(const float* __restrict__ G,
                                                             uint16_t* __restrict__ out,
                                                             int64_t MN, int S) {
@@ -454,23 +456,23 @@ __global__ void __launch_bounds__(256) splitk_reduce_scalar(const float* __restr
        e += (int64_t)gridDim.x * blockDim.x) {
     float s = G[e];
     for (int k = 1; k < S; ++k) s += G[(int64_t)k * MN + e];
-    out[e] = (uint16_t)f2bf(s);
+    out[e] = (uint16_t)cvt16<H>(s);
   }
 }
 
-template <int BM, int BN, int WM, int WN>
+template <int BM, int BN, int WM, int WN, bool H>
 hipError_t launch_tile(const GemmParams& p, bool aligned, bool out_f32, hipStream_t st) {
   const dim3 grid((unsigned)((int64_t)p.tiles_m * p.tiles_n * p.nz)), block(64 * WM * WN);
   if (aligned) {
     if (out_f32)
-      hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, WM, WN, true, true>), grid, block, 0, st, p);
+      hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, WM, WN, true, true, H>), grid, block, 0, st, p);
     else
-      hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, WM, WN, true, false>), grid, block, 0, st, p);
+      hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, WM, WN, true, false, H>), grid, block, 0, st, p);
   } else {
     if (out_f32)
-      hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, WM, WN, false, true>), grid, block, 0, st, p);
+      hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, WM, WN, false, true, H>), grid, block, 0, st, p);
     else
-      hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, WM, WN, false, false>), grid, block, 0, st, p);
+      hipLaunchKernelGGL((gemm_bf16_kernel<BM, BN, WM, WN, false, false, H>), grid, block, 0, st, p);
   }
   return hipGetLastError();
 }
@@ -488,24 +490,25 @@ bool tile_supported(int64_t tm, int64_t tn) {
 #define LOOM_GEMM_DMA_NS 4
 #endif
 
+template <bool H>
 hipError_t launch_gemm(GemmParams p, int64_t tile_m, int64_t tile_n, bool aligned, bool out_f32,
                        hipStream_t st) {
   p.tiles_m = (int)cdiv64(p.M, tile_m);
   p.tiles_n = (int)cdiv64(p.N, tile_n);
-  if (tile_m == 64) return launch_tile<64, 64, 1, 2>(p, aligned, out_f32, st);
-  if (tile_m == 128) return launch_tile<128, 128, 2, 2>(p, aligned, out_f32, st);
+  if (tile_m == 64) return launch_tile<64, 64, 1, 2, H>(p, aligned, out_f32, st);
+  if (tile_m == 128) return launch_tile<128, 128, 2, 2, H>(p, aligned, out_f32, st);
   // 256x256: the LDS-DMA kernel needs whole BK steps in every K range
   constexpr int BK = LOOM_GEMM_DMA_BK, NS = LOOM_GEMM_DMA_NS;
   const bool dma = aligned && p.k_total % BK == 0 && (!p.split || p.k_slab % BK == 0);
   if (dma) {
     const dim3 grid((unsigned)((int64_t)p.tiles_m * p.tiles_n * p.nz)), block(256);
     if (out_f32)
-      hipLaunchKernelGGL((gemm_dma_kernel<BK, NS, true>), grid, block, 0, st, p);
+      hipLaunchKernelGGL((gemm_dma_kernel<BK, NS, true, H>), grid, block, 0, st, p);
     else
-      hipLaunchKernelGGL((gemm_dma_kernel<BK, NS, false>), grid, block, 0, st, p);
+      hipLaunchKernelGGL((gemm_dma_kernel<BK, NS, false, H>), grid, block, 0, st, p);
     return hipGetLastError();
   }
-  return launch_tile<256, 256, 2, 4>(p, aligned, out_f32, st);
+  return launch_tile<256, 256, 2, 4, H>(p, aligned, out_f32, st);
 }
 
 int check_gemm_common(const void* a, const void* b, const void* c, int64_t M, int64_t N,
@@ -527,11 +530,10 @@ int check_gemm_common(const void* a, const void* b, const void* c, int64_t M, in
   return LOOM_OK;
 }
 
-}  // namespace
 
-extern "C" {
 
-int loom_hip_matmul(const void* x, const void* y, void* out, int64_t M, int64_t N, int64_t K,
+template <bool H>
+int matmul_impl(const void* x, const void* y, void* out, int64_t M, int64_t N, int64_t K,
                     int64_t tile_m, int64_t tile_n, int64_t tile_k, void* stream, char* err,
                     size_t errlen) {
   int rc = check_gemm_common(x, y, out, M, N, K, tile_m, tile_n, tile_k, "matmul", err, errlen);
@@ -551,11 +553,12 @@ int loom_hip_matmul(const void* x, const void* y, void* out, int64_t M, int64_t 
   p.nz = 1;
   const bool al = K % 8 == 0 && N % 8 == 0 && aligned16(x) && aligned16(y);
   if (loom_validate_only()) return loom_ok(err, errlen);
-  (void)launch_gemm(p, tile_m, tile_n, al, false, static_cast<hipStream_t>(stream));
+  (void)launch_gemm<H>(p, tile_m, tile_n, al, false, static_cast<hipStream_t>(stream));
   return loom_check_launch(err, errlen, "matmul");
 }
 
-int loom_hip_batch_matmul(const void* arg0, const void* arg1, void* arg2, int64_t Bt, int64_t M,
+template <bool H>
+int batch_matmul_impl(const void* arg0, const void* arg1, void* arg2, int64_t Bt, int64_t M,
                           int64_t N, int64_t K, int64_t tile_b, int64_t tile_m, int64_t tile_n,
                           int64_t tile_k, void* stream, char* err, size_t errlen) {
   int rc = check_gemm_common(arg0, arg1, arg2, M, N, K, tile_m, tile_n, tile_k, "batch_matmul",
@@ -584,16 +587,13 @@ int loom_hip_batch_matmul(const void* arg0, const void* arg1, void* arg2, int64_
   p.nz = (int)Bt;
   const bool al = K % 8 == 0 && N % 8 == 0 && aligned16(arg0) && aligned16(arg1);
   if (loom_validate_only()) return loom_ok(err, errlen);
-  (void)launch_gemm(p, tile_m, tile_n, al, false, static_cast<hipStream_t>(stream));
+  (void)launch_gemm<H>(p, tile_m, tile_n, al, false, static_cast<hipStream_t>(stream));
   return loom_check_launch(err, errlen, "batch_matmul");
 }
 
-size_t loom_hip_split_k_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t tile_k) {
-  if (M <= 0 || N <= 0 || K <= 0 || tile_k <= 0) return 0;
-  return (size_t)cdiv64(K, tile_k) * (size_t)M * (size_t)N * sizeof(float);
-}
 
-int loom_hip_split_k_matmul_gather(const void* a, const void* b, void* out, void* partials,
+template <bool H>
+int split_k_matmul_gather_impl(const void* a, const void* b, void* out, void* partials,
                                    size_t partials_bytes, int64_t M, int64_t N, int64_t K,
                                    int64_t tile_m, int64_t tile_n, int64_t tile_k, void* stream,
                                    char* err, size_t errlen) {
@@ -629,22 +629,69 @@ int loom_hip_split_k_matmul_gather(const void* a, const void* b, void* out, void
   p.nz = (int)S;
   const bool al = K % 8 == 0 && N % 8 == 0 && tile_k % 8 == 0 && aligned16(a) && aligned16(b);
   if (loom_validate_only()) return loom_ok(err, errlen);
-  (void)launch_gemm(p, tile_m, tile_n, al, true, st);
+  (void)launch_gemm<H>(p, tile_m, tile_n, al, true, st);
   rc = loom_check_launch(err, errlen, "split_k_matmul_gather (slab GEMM)");
   if (rc) return rc;
   const int64_t MN = M * N;
   if (MN % 4 == 0 && aligned16(partials) && (reinterpret_cast<uintptr_t>(out) & 7u) == 0) {
     const int64_t blocks = std::min<int64_t>(cdiv64(MN / 4, 256), 8192);
-    hipLaunchKernelGGL(splitk_reduce_vec4, dim3((unsigned)blocks), dim3(256), 0, st,
+    hipLaunchKernelGGL(splitk_reduce_vec4<H>, dim3((unsigned)blocks), dim3(256), 0, st,
                        static_cast<const float*>(partials), static_cast<uint16_t*>(out), MN,
                        (int)S);
   } else {
     const int64_t blocks = std::min<int64_t>(cdiv64(MN, 256), 8192);
-    hipLaunchKernelGGL(splitk_reduce_scalar, dim3((unsigned)blocks), dim3(256), 0, st,
+    hipLaunchKernelGGL(splitk_reduce_scalar<H>, dim3((unsigned)blocks), dim3(256), 0, st,
                        static_cast<const float*>(partials), static_cast<uint16_t*>(out), MN,
                        (int)S);
   }
   return loom_check_launch(err, errlen, "split_k_matmul_gather (gather-reduce)");
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t loom_hip_split_k_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t tile_k) {
+  if (M <= 0 || N <= 0 || K <= 0 || tile_k <= 0) return 0;
+  return (size_t)cdiv64(K, tile_k) * (size_t)M * (size_t)N * sizeof(float);
+}
+
+int loom_hip_matmul(const void* x, const void* y, void* out, int64_t M, int64_t N, int64_t K,
+                    int64_t tile_m, int64_t tile_n, int64_t tile_k, void* stream, char* err,
+                    size_t errlen) {
+  return matmul_impl<false>(x, y, out, M, N, K, tile_m, tile_n, tile_k, stream, err, errlen);
+}
+int loom_hip_matmul_f16(const void* x, const void* y, void* out, int64_t M, int64_t N, int64_t K,
+                        int64_t tile_m, int64_t tile_n, int64_t tile_k, void* stream, char* err,
+                        size_t errlen) {
+  return matmul_impl<true>(x, y, out, M, N, K, tile_m, tile_n, tile_k, stream, err, errlen);
+}
+int loom_hip_batch_matmul(const void* arg0, const void* arg1, void* arg2, int64_t B, int64_t M,
+                          int64_t N, int64_t K, int64_t tile_b, int64_t tile_m, int64_t tile_n,
+                          int64_t tile_k, void* stream, char* err, size_t errlen) {
+  return batch_matmul_impl<false>(arg0, arg1, arg2, B, M, N, K, tile_b, tile_m, tile_n, tile_k,
+                                  stream, err, errlen);
+}
+int loom_hip_batch_matmul_f16(const void* arg0, const void* arg1, void* arg2, int64_t B,
+                              int64_t M, int64_t N, int64_t K, int64_t tile_b, int64_t tile_m,
+                              int64_t tile_n, int64_t tile_k, void* stream, char* err,
+                              size_t errlen) {
+  return batch_matmul_impl<true>(arg0, arg1, arg2, B, M, N, K, tile_b, tile_m, tile_n, tile_k,
+                                 stream, err, errlen);
+}
+int loom_hip_split_k_matmul_gather(const void* a, const void* b, void* out, void* partials,
+                                   size_t partials_bytes, int64_t M, int64_t N, int64_t K,
+                                   int64_t tile_m, int64_t tile_n, int64_t tile_k, void* stream,
+                                   char* err, size_t errlen) {
+  return split_k_matmul_gather_impl<false>(a, b, out, partials, partials_bytes, M, N, K, tile_m,
+                                           tile_n, tile_k, stream, err, errlen);
+}
+int loom_hip_split_k_matmul_gather_f16(const void* a, const void* b, void* out, void* partials,
+                                       size_t partials_bytes, int64_t M, int64_t N, int64_t K,
+                                       int64_t tile_m, int64_t tile_n, int64_t tile_k,
+                                       void* stream, char* err, size_t errlen) {
+  return split_k_matmul_gather_impl<true>(a, b, out, partials, partials_bytes, M, N, K, tile_m,
+                                          tile_n, tile_k, stream, err, errlen);
 }
 
 }  // extern "C"

@@ -53,7 +53,7 @@ struct MambaParams {
   int tile_m, tile_n, nmt, npt;
 };
 
-template <int PT>  // p tiles of 16 per workgroup (tile_n = 16 PT)
+template <int PT, bool F16>  // p tiles of 16 per workgroup (tile_n = 16 PT); F16: f16 elements
 __global__ void __launch_bounds__(64 * kWaves) mamba_chunk_scan_kernel(MambaParams p) {
   constexpr int TN = 16 * PT;
   constexpr int XROW = kQmax / 8;   // 16-byte chunks per xT row
@@ -152,9 +152,9 @@ __global__ void __launch_bounds__(64 * kWaves) mamba_chunk_scan_kernel(MambaPara
                           pr[e][1][0], pr[e][1][1], pr[e][1][2], pr[e][1][3]};
 #pragma unroll
       for (int z = 0; z < 4; ++z) {
-        const uint32_t hw = pack_bf16x2(v[2 * z], v[2 * z + 1]);
+        const uint32_t hw = pack2<F16>(v[2 * z], v[2 * z + 1]);
         hi[e][z] = hw;
-        lo[e][z] = pack_bf16x2(v[2 * z] - bf2f_lo(hw), v[2 * z + 1] - bf2f_hi(hw));
+        lo[e][z] = pack2<F16>(v[2 * z] - lo16<F16>(hw), v[2 * z + 1] - hi16<F16>(hw));
       }
     }
     transpose8x8(hi, thi);
@@ -228,8 +228,8 @@ __global__ void __launch_bounds__(64 * kWaves) mamba_chunk_scan_kernel(MambaPara
       for (int pt = 0; pt < PT; ++pt) {
         const int pp = pt * 16 + rr;
         const int ch = (ns * 4 + g4) ^ (pp & 7);
-        acc_s[pt] = mfma16(pT[0][pp * PROW + ch], rw.c[ns], acc_s[pt]);
-        acc_s[pt] = mfma16(pT[1][pp * PROW + ch], rw.c[ns], acc_s[pt]);
+        acc_s[pt] = mfma16t<F16>(pT[0][pp * PROW + ch], rw.c[ns], acc_s[pt]);
+        acc_s[pt] = mfma16t<F16>(pT[1][pp * PROW + ch], rw.c[ns], acc_s[pt]);
       }
     }
     const float dAm = am < Q ? s_dA[am] : 0.f;
@@ -254,7 +254,7 @@ __global__ void __launch_bounds__(64 * kWaves) mamba_chunk_scan_kernel(MambaPara
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const uint32_t word = rw.cb[ks][e >> 1];
-          const float cbf = (e & 1) ? bf2f_hi(word) : bf2f_lo(word);
+          const float cbf = (e & 1) ? hi16<F16>(word) : lo16<F16>(word);
           wv[e] = cbf * (e < 4 ? u0[e] : u1[e - 4]) * vm;
         }
       } else {
@@ -266,7 +266,7 @@ __global__ void __launch_bounds__(64 * kWaves) mamba_chunk_scan_kernel(MambaPara
         for (int e = 0; e < 8; ++e) {
           const int k = kb + e;
           const uint32_t word = rw.cb[ks][e >> 1];
-          const float cbf = (e & 1) ? bf2f_hi(word) : bf2f_lo(word);
+          const float cbf = (e & 1) ? hi16<F16>(word) : lo16<F16>(word);
           const float dAk = e < 4 ? dA0[e] : dA1[e - 4];
           const float dtk = e < 4 ? dt0[e] : dt1[e - 4];
           float w = (k <= am && k < Q) ? cbf * fast_exp2(dAm - dAk) * dtk : 0.f;
@@ -277,16 +277,16 @@ __global__ void __launch_bounds__(64 * kWaves) mamba_chunk_scan_kernel(MambaPara
       u32x4_t ahi, alo;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const uint32_t hw = pack_bf16x2(wv[2 * i], wv[2 * i + 1]);
+        const uint32_t hw = pack2<F16>(wv[2 * i], wv[2 * i + 1]);
         ahi[i] = hw;
-        alo[i] = pack_bf16x2(wv[2 * i] - bf2f_lo(hw), wv[2 * i + 1] - bf2f_hi(hw));
+        alo[i] = pack2<F16>(wv[2 * i] - lo16<F16>(hw), wv[2 * i + 1] - hi16<F16>(hw));
       }
 #pragma unroll
       for (int pt = 0; pt < PT; ++pt) {
         const int pp = pt * 16 + rr;
         const u32x4_t xb = xT[pp * XROW + ((ks * 4 + g4) ^ (pp & 7))];
-        acc[pt] = mfma16(xb, ahi, acc[pt]);
-        acc[pt] = mfma16(xb, alo, acc[pt]);
+        acc[pt] = mfma16t<F16>(xb, ahi, acc[pt]);
+        acc[pt] = mfma16t<F16>(xb, alo, acc[pt]);
       }
     }
 
@@ -298,24 +298,21 @@ __global__ void __launch_bounds__(64 * kWaves) mamba_chunk_scan_kernel(MambaPara
         const f32x4_t o = acc_s[pt] * em + acc[pt];
         if (pg < P)
           *reinterpret_cast<u32x2_t*>(og + (int64_t)am * P + pg) =
-              u32x2_t{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+              u32x2_t{pack2<F16>(o[0], o[1]), pack2<F16>(o[2], o[3])};
       }
     }
   }
 }
 
-template <int PT>
+template <int PT, bool F16>
 void launch_mamba(const MambaParams& p, hipStream_t st) {
   const int64_t nblocks = (int64_t)p.Bb * p.nc * p.H * p.nmt * p.npt;
-  hipLaunchKernelGGL((mamba_chunk_scan_kernel<PT>), dim3((unsigned)nblocks), dim3(64 * kWaves), 0,
+  hipLaunchKernelGGL((mamba_chunk_scan_kernel<PT, F16>), dim3((unsigned)nblocks), dim3(64 * kWaves), 0,
                      st, p);
 }
 
-}  // namespace
-
-extern "C" {
-
-int loom_hip_helion_mamba2_chunk_scan_kernel(
+template <bool F16>
+int chunk_scan_impl(
     const void* cb, const void* x, const void* dt, const void* dA_cumsum, const void* C,
     const void* D, const void* prev_states_T, void* out, int64_t batch, int64_t nchunks,
     int64_t nheads, int64_t ngroups, int64_t chunk_size, int64_t headdim, int64_t dstate,
@@ -375,10 +372,35 @@ int loom_hip_helion_mamba2_chunk_scan_kernel(
   p.npt = (int)npt;
   if (loom_validate_only()) return loom_ok(err, errlen);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (tile_n == 64) launch_mamba<4>(p, st);
-  else if (tile_n == 32) launch_mamba<2>(p, st);
-  else launch_mamba<1>(p, st);
+  if (tile_n == 64) launch_mamba<4, F16>(p, st);
+  else if (tile_n == 32) launch_mamba<2, F16>(p, st);
+  else launch_mamba<1, F16>(p, st);
   return loom_check_launch(err, errlen, fn);
+}
+
+}  // namespace
+
+extern "C" {
+
+int loom_hip_helion_mamba2_chunk_scan_kernel(
+    const void* cb, const void* x, const void* dt, const void* dA_cumsum, const void* C,
+    const void* D, const void* prev_states_T, void* out, int64_t batch, int64_t nchunks,
+    int64_t nheads, int64_t ngroups, int64_t chunk_size, int64_t headdim, int64_t dstate,
+    int64_t tile_b, int64_t tile_h, int64_t tile_c, int64_t tile_m, int64_t tile_n,
+    int64_t tile_k, void* stream, char* err, size_t errlen) {
+  return chunk_scan_impl<false>(cb, x, dt, dA_cumsum, C, D, prev_states_T, out, batch, nchunks,
+                                nheads, ngroups, chunk_size, headdim, dstate, tile_b, tile_h,
+                                tile_c, tile_m, tile_n, tile_k, stream, err, errlen);
+}
+int loom_hip_helion_mamba2_chunk_scan_kernel_f16(
+    const void* cb, const void* x, const void* dt, const void* dA_cumsum, const void* C,
+    const void* D, const void* prev_states_T, void* out, int64_t batch, int64_t nchunks,
+    int64_t nheads, int64_t ngroups, int64_t chunk_size, int64_t headdim, int64_t dstate,
+    int64_t tile_b, int64_t tile_h, int64_t tile_c, int64_t tile_m, int64_t tile_n,
+    int64_t tile_k, void* stream, char* err, size_t errlen) {
+  return chunk_scan_impl<true>(cb, x, dt, dA_cumsum, C, D, prev_states_T, out, batch, nchunks,
+                               nheads, ngroups, chunk_size, headdim, dstate, tile_b, tile_h,
+                               tile_c, tile_m, tile_n, tile_k, stream, err, errlen);
 }
 
 }  // extern "C"

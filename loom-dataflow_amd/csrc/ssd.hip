@@ -75,6 +75,7 @@ __global__ void __launch_bounds__(64) ssd_cumsum_kernel(const float* __restrict_
 // ---------------------------------------------------------------------------
 // cb = C B^T, lower triangle
 // ---------------------------------------------------------------------------
+template <bool F16>
 __global__ void __launch_bounds__(64) ssd_cb_kernel(const uint16_t* __restrict__ Bm,
                                                     const uint16_t* __restrict__ Cm,
                                                     uint16_t* __restrict__ cb, int nc, int G,
@@ -110,7 +111,7 @@ __global__ void __launch_bounds__(64) ssd_cb_kernel(const uint16_t* __restrict__
         const int n = 32 * ks + 8 * gq;
         const u32x4_t bf = n < N ? *reinterpret_cast<const u32x4_t*>(Bc + (int64_t)(16 * jt + r) * N + n)
                                  : u32x4_t{0u, 0u, 0u, 0u};
-        acc = mfma16(bf, cf[ks], acc);        // D[j][i] = sum_n B[j][n] C[i][n]
+        acc = mfma16t<F16>(bf, cf[ks], acc);  // D[j][i] = sum_n B[j][n] C[i][n]
       }
     }
     // lane holds cb[i0 + r][16 jt + 4 gq + e]
@@ -120,7 +121,7 @@ __global__ void __launch_bounds__(64) ssd_cb_kernel(const uint16_t* __restrict__
         if (4 * gq + e > r) acc[e] = 0.f;
     }
     *reinterpret_cast<u32x2_t*>(orow) =
-        u32x2_t{pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3])};
+        u32x2_t{pack2<F16>(acc[0], acc[1]), pack2<F16>(acc[2], acc[3])};
   }
 }
 
@@ -151,7 +152,7 @@ struct SsdStateParams {
 
 // SHARED_PT: P / 16 divides the wave count, so all tiles of a wave share
 // one p tile and the w-scaled x operand is built once per k step.
-template <int TPW, bool SHARED_PT>
+template <int TPW, bool SHARED_PT, bool F16>
 __global__ void __launch_bounds__(64 * kSsdWaves) ssd_state_kernel(SsdStateParams p) {
   __shared__ __attribute__((aligned(1024))) char smem[kSsdRing + 1024];
   __shared__ __attribute__((aligned(16))) float s_w[2][128];  // w of units u, u+1 (by parity)
@@ -261,14 +262,14 @@ __global__ void __launch_bounds__(64 * kSsdWaves) ssd_state_kernel(SsdStateParam
     const u32x2_t xlo = lds_read_tr16(qx), xhi = lds_read_tr16(qx + 16 * XR);
     const f32x4_t w0 = *reinterpret_cast<const f32x4_t*>(wv + k0);
     const f32x4_t w1 = *reinterpret_cast<const f32x4_t*>(wv + k0 + 16);
-    const float v[8] = {bf2f_lo(xlo[0]) * w0[0], bf2f_hi(xlo[0]) * w0[1],
-                        bf2f_lo(xlo[1]) * w0[2], bf2f_hi(xlo[1]) * w0[3],
-                        bf2f_lo(xhi[0]) * w1[0], bf2f_hi(xhi[0]) * w1[1],
-                        bf2f_lo(xhi[1]) * w1[2], bf2f_hi(xhi[1]) * w1[3]};
+    const float v[8] = {lo16<F16>(xlo[0]) * w0[0], hi16<F16>(xlo[0]) * w0[1],
+                        lo16<F16>(xlo[1]) * w0[2], hi16<F16>(xlo[1]) * w0[3],
+                        lo16<F16>(xhi[0]) * w1[0], hi16<F16>(xhi[0]) * w1[1],
+                        lo16<F16>(xhi[1]) * w1[2], hi16<F16>(xhi[1]) * w1[3]};
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      vh[e] = pack_bf16x2(v[2 * e], v[2 * e + 1]);
-      vl[e] = pack_bf16x2(v[2 * e] - bf2f_lo(vh[e]), v[2 * e + 1] - bf2f_hi(vh[e]));
+      vh[e] = pack2<F16>(v[2 * e], v[2 * e + 1]);
+      vl[e] = pack2<F16>(v[2 * e] - lo16<F16>(vh[e]), v[2 * e + 1] - hi16<F16>(vh[e]));
     }
   };
 
@@ -307,8 +308,8 @@ __global__ void __launch_bounds__(64 * kSsdWaves) ssd_state_kernel(SsdStateParam
           const lds_char_t* qb = bs + (k0 + a4) * BR + (2 * nt + (c4 >> 1)) * 16 + (c4 & 1) * 8;
           const u32x2_t blo = lds_read_tr16(qb), bhi = lds_read_tr16(qb + 16 * BR);
           const u32x4_t bf = u32x4_t{blo[0], blo[1], bhi[0], bhi[1]};
-          R[t] = mfma16(xh, bf, R[t]);
-          R[t] = mfma16(xl, bf, R[t]);
+          R[t] = mfma16t<F16>(xh, bf, R[t]);
+          R[t] = mfma16t<F16>(xl, bf, R[t]);
         }
       }
     }
@@ -337,14 +338,14 @@ __global__ void __launch_bounds__(64 * kSsdWaves) ssd_state_kernel(SsdStateParam
   }
 }
 
-template <int TPW>
+template <int TPW, bool F16>
 void launch_state(const SsdStateParams& p, int grid_x, int grid_y, hipStream_t st) {
   const int ptiles = p.P / 16;
   if (kSsdWaves % ptiles == 0)
-    hipLaunchKernelGGL((ssd_state_kernel<TPW, true>), dim3((unsigned)grid_x, (unsigned)grid_y),
+    hipLaunchKernelGGL((ssd_state_kernel<TPW, true, F16>), dim3((unsigned)grid_x, (unsigned)grid_y),
                        dim3(64 * kSsdWaves), 0, st, p);
   else
-    hipLaunchKernelGGL((ssd_state_kernel<TPW, false>), dim3((unsigned)grid_x, (unsigned)grid_y),
+    hipLaunchKernelGGL((ssd_state_kernel<TPW, false, F16>), dim3((unsigned)grid_x, (unsigned)grid_y),
                        dim3(64 * kSsdWaves), 0, st, p);
 }
 
@@ -393,7 +394,12 @@ int loom_hip_ssd_chunk_cumsum(const void* dt, const void* A, void* dA_cumsum, in
   return loom_check_launch(err, errlen, "ssd_chunk_cumsum");
 }
 
-int loom_hip_ssd_bmm_chunk(const void* B, const void* C, void* cb, int64_t batch, int64_t nchunks,
+}  // extern "C"
+
+namespace {
+
+template <bool F16>
+int bmm_chunk_impl(const void* B, const void* C, void* cb, int64_t batch, int64_t nchunks,
                            int64_t ngroups, int64_t chunk_size, int64_t dstate, void* stream,
                            char* err, size_t errlen) {
   if (!B || !C || !cb) return loom_fail(err, errlen, LOOM_EINVAL, "ssd_bmm_chunk: null tensor pointer");
@@ -403,7 +409,7 @@ int loom_hip_ssd_bmm_chunk(const void* B, const void* C, void* cb, int64_t batch
   if (!aligned16(B) || !aligned16(C) || (reinterpret_cast<uintptr_t>(cb) & 7u))
     return loom_fail(err, errlen, LOOM_EINVAL, "ssd_bmm_chunk: B, C 16-byte and cb 8-byte aligned");
   if (loom_validate_only()) return loom_ok(err, errlen);
-  hipLaunchKernelGGL(ssd_cb_kernel, dim3((unsigned)(batch * nchunks * ngroups), (unsigned)(chunk_size / 16)),
+  hipLaunchKernelGGL(ssd_cb_kernel<F16>, dim3((unsigned)(batch * nchunks * ngroups), (unsigned)(chunk_size / 16)),
                      dim3(64), 0, static_cast<hipStream_t>(stream),
                      static_cast<const uint16_t*>(B), static_cast<const uint16_t*>(C),
                      static_cast<uint16_t*>(cb), (int)nchunks, (int)ngroups,
@@ -411,7 +417,8 @@ int loom_hip_ssd_bmm_chunk(const void* B, const void* C, void* cb, int64_t batch
   return loom_check_launch(err, errlen, "ssd_bmm_chunk");
 }
 
-int loom_hip_ssd_chunk_state_passing(const void* x, const void* dt, const void* dA_cumsum,
+template <bool F16>
+int state_passing_impl(const void* x, const void* dt, const void* dA_cumsum,
                                      const void* B, void* prev_states_T, int64_t batch,
                                      int64_t nchunks, int64_t nheads, int64_t ngroups,
                                      int64_t chunk_size, int64_t headdim, int64_t dstate,
@@ -469,13 +476,14 @@ int loom_hip_ssd_chunk_state_passing(const void* x, const void* dt, const void* 
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int gx = (int)(batch * nheads), gy = (int)(dstate / nb);
   if (loom_validate_only()) return loom_ok(err, errlen);
-  if (tpw <= 1) launch_state<1>(p, gx, gy, st);
-  else if (tpw <= 2) launch_state<2>(p, gx, gy, st);
-  else launch_state<4>(p, gx, gy, st);
+  if (tpw <= 1) launch_state<1, F16>(p, gx, gy, st);
+  else if (tpw <= 2) launch_state<2, F16>(p, gx, gy, st);
+  else launch_state<4, F16>(p, gx, gy, st);
   return loom_check_launch(err, errlen, "ssd_chunk_state_passing");
 }
 
-int loom_hip_ssd_prologue(const void* x, const void* dt, const void* A, const void* B,
+template <bool F16>
+int prologue_impl(const void* x, const void* dt, const void* A, const void* B,
                           const void* C, void* dA_cumsum, void* cb, void* prev_states_T,
                           int64_t batch, int64_t nchunks, int64_t nheads, int64_t ngroups,
                           int64_t chunk_size, int64_t headdim, int64_t dstate, void* stream,
@@ -486,12 +494,61 @@ int loom_hip_ssd_prologue(const void* x, const void* dt, const void* A, const vo
   rc = loom_hip_ssd_chunk_cumsum(dt, A, dA_cumsum, batch, nchunks, nheads, chunk_size, stream,
                                  err, errlen);
   if (rc) return rc;
-  rc = loom_hip_ssd_bmm_chunk(B, C, cb, batch, nchunks, ngroups, chunk_size, dstate, stream, err,
+  rc = bmm_chunk_impl<F16>(B, C, cb, batch, nchunks, ngroups, chunk_size, dstate, stream, err,
                               errlen);
   if (rc) return rc;
-  return loom_hip_ssd_chunk_state_passing(x, dt, dA_cumsum, B, prev_states_T, batch, nchunks,
+  return state_passing_impl<F16>(x, dt, dA_cumsum, B, prev_states_T, batch, nchunks,
                                           nheads, ngroups, chunk_size, headdim, dstate, stream,
                                           err, errlen);
+}
+
+}  // namespace
+
+extern "C" {
+
+int loom_hip_ssd_bmm_chunk(const void* B, const void* C, void* cb, int64_t batch, int64_t nchunks,
+                           int64_t ngroups, int64_t chunk_size, int64_t dstate, void* stream,
+                           char* err, size_t errlen) {
+  return bmm_chunk_impl<false>(B, C, cb, batch, nchunks, ngroups, chunk_size, dstate, stream, err,
+                               errlen);
+}
+int loom_hip_ssd_bmm_chunk_f16(const void* B, const void* C, void* cb, int64_t batch,
+                               int64_t nchunks, int64_t ngroups, int64_t chunk_size,
+                               int64_t dstate, void* stream, char* err, size_t errlen) {
+  return bmm_chunk_impl<true>(B, C, cb, batch, nchunks, ngroups, chunk_size, dstate, stream, err,
+                              errlen);
+}
+int loom_hip_ssd_chunk_state_passing(const void* x, const void* dt, const void* dA_cumsum,
+                                     const void* B, void* prev_states_T, int64_t batch,
+                                     int64_t nchunks, int64_t nheads, int64_t ngroups,
+                                     int64_t chunk_size, int64_t headdim, int64_t dstate,
+                                     void* stream, char* err, size_t errlen) {
+  return state_passing_impl<false>(x, dt, dA_cumsum, B, prev_states_T, batch, nchunks, nheads,
+                                   ngroups, chunk_size, headdim, dstate, stream, err, errlen);
+}
+int loom_hip_ssd_chunk_state_passing_f16(const void* x, const void* dt, const void* dA_cumsum,
+                                         const void* B, void* prev_states_T, int64_t batch,
+                                         int64_t nchunks, int64_t nheads, int64_t ngroups,
+                                         int64_t chunk_size, int64_t headdim, int64_t dstate,
+                                         void* stream, char* err, size_t errlen) {
+  return state_passing_impl<true>(x, dt, dA_cumsum, B, prev_states_T, batch, nchunks, nheads,
+                                  ngroups, chunk_size, headdim, dstate, stream, err, errlen);
+}
+int loom_hip_ssd_prologue(const void* x, const void* dt, const void* A, const void* B,
+                          const void* C, void* dA_cumsum, void* cb, void* prev_states_T,
+                          int64_t batch, int64_t nchunks, int64_t nheads, int64_t ngroups,
+                          int64_t chunk_size, int64_t headdim, int64_t dstate, void* stream,
+                          char* err, size_t errlen) {
+  return prologue_impl<false>(x, dt, A, B, C, dA_cumsum, cb, prev_states_T, batch, nchunks,
+                              nheads, ngroups, chunk_size, headdim, dstate, stream, err, errlen);
+}
+int loom_hip_ssd_prologue_f16(const void* x, const void* dt, const void* A, const void* B,
+                              const void* C, void* dA_cumsum, void* cb, void* prev_states_T,
+                              int64_t batch, int64_t nchunks, int64_t nheads, int64_t ngroups,
+                              int64_t chunk_size, int64_t headdim, int64_t dstate, void* stream,
+                              char* err, size_t errlen) {
+  return prologue_impl<true>(x, dt, A, B, C, dA_cumsum, cb, prev_states_T, batch, nchunks,
+                             nheads, ngroups, chunk_size, headdim, dstate, stream, err, errlen);
 }
 
 }  // extern "C"

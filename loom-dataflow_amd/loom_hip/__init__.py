@@ -49,6 +49,12 @@ _SIGS = {
     "loom_hip_ssd_chunk_state_passing": [_vp] * 5 + [_i64] * 7 + [_vp, *_ERR],
     "loom_hip_ssd_prologue": [_vp] * 8 + [_i64] * 7 + [_vp, *_ERR],
 }
+# f16 twins: same arguments, 16-bit tensors in IEEE binary16
+for _name in ("loom_hip_matmul", "loom_hip_batch_matmul", "loom_hip_split_k_matmul_gather",
+              "loom_hip_attention", "loom_hip_flash_decode",
+              "loom_hip_helion_mamba2_chunk_scan_kernel", "loom_hip_ssd_bmm_chunk",
+              "loom_hip_ssd_chunk_state_passing", "loom_hip_ssd_prologue"):
+    _SIGS[_name + "_f16"] = _SIGS[_name]
 for _name, _args in _SIGS.items():
     _fn = getattr(_lib, _name)
     _fn.argtypes = _args
@@ -68,6 +74,8 @@ _lib.loom_hip_dispatch.argtypes = [ctypes.c_char_p, ctypes.POINTER(_vp), ctypes.
                                    ctypes.POINTER(_i64), ctypes.c_int, _f32, ctypes.c_int,
                                    _vp, _sz, _vp, *_ERR]
 _lib.loom_hip_dispatch.restype = ctypes.c_int
+_lib.loom_hip_dispatch_f16.argtypes = _lib.loom_hip_dispatch.argtypes
+_lib.loom_hip_dispatch_f16.restype = ctypes.c_int
 _lib.loom_hip_check_variant.argtypes = [ctypes.c_char_p, ctypes.POINTER(_i64), ctypes.c_int, *_ERR]
 _lib.loom_hip_check_variant.restype = ctypes.c_int
 for _fn in ("loom_hip_constraint_scope", "loom_hip_preferred_block_sizes"):
@@ -78,7 +86,7 @@ for _fn in ("loom_hip_constraint_scope", "loom_hip_preferred_block_sizes"):
 EXPORTED = tuple(_SIGS) + ("loom_hip_split_k_workspace_bytes",
                            "loom_hip_flash_decode_workspace_bytes", "loom_hip_version",
                            "loom_hip_materialize_variants", "loom_hip_parse_variant",
-                           "loom_hip_dispatch", "loom_hip_check_variant",
+                           "loom_hip_dispatch", "loom_hip_dispatch_f16", "loom_hip_check_variant",
                            "loom_hip_constraint_scope", "loom_hip_preferred_block_sizes")
 
 #: block-size symbols in the slot order of loom_hip_parse_variant's tiles[]
@@ -121,7 +129,16 @@ def _need(t: torch.Tensor, name: str, dtype: torch.dtype, ndim: int) -> int:
     return t.data_ptr()
 
 
-_bf16, _fp32 = torch.bfloat16, torch.float32
+_bf16, _f16, _fp32 = torch.bfloat16, torch.float16, torch.float32
+
+
+def _elt(t):
+    """16-bit element type of a kernel call, from one of its 16-bit tensors:
+    (torch dtype, entry-point suffix).  bf16 and f16 (the reference's own
+    element type) are built."""
+    if isinstance(t, torch.Tensor) and t.dtype == _f16:
+        return _f16, "_f16"
+    return _bf16, ""
 
 
 # ---------------------------------------------------------------------------
@@ -130,31 +147,33 @@ _bf16, _fp32 = torch.bfloat16, torch.float32
 
 def matmul(x, y, out=None, *, tile_m=128, tile_n=128, tile_k=64):
     """@matmul (examples/mm/IR/00_from_helion_frontend.mlir:2): out = x . y."""
+    _e, _sfx = _elt(x)
     M, K = x.shape
     N = y.shape[1]
     if y.shape[0] != K:
         raise ValueError(f"matmul: inner dims differ: {tuple(x.shape)} . {tuple(y.shape)}")
     if out is None:
-        out = torch.empty((M, N), dtype=_bf16, device=x.device)
+        out = torch.empty((M, N), dtype=_e, device=x.device)
     if tuple(out.shape) != (M, N):
         raise ValueError("matmul: out shape mismatch")
-    _call("loom_hip_matmul", _need(x, "x", _bf16, 2), _need(y, "y", _bf16, 2),
-          _need(out, "out", _bf16, 2), M, N, K, tile_m, tile_n, tile_k, _stream(x))
+    _call("loom_hip_matmul" + _sfx, _need(x, "x", _e, 2), _need(y, "y", _e, 2),
+          _need(out, "out", _e, 2), M, N, K, tile_m, tile_n, tile_k, _stream(x))
     return out
 
 
 def batch_matmul(arg0, arg1, arg2=None, *, tile_b=1, tile_m=256, tile_n=256, tile_k=64):
     """@batch_matmul (examples/bmm_2Dmesh/IR/00_from_helion_frontend.mlir:4)."""
+    _e, _sfx = _elt(arg0)
     B, M, K = arg0.shape
     N = arg1.shape[2]
     if tuple(arg1.shape[:2]) != (B, K):
         raise ValueError("batch_matmul: arg1 shape mismatch")
     if arg2 is None:
-        arg2 = torch.empty((B, M, N), dtype=_bf16, device=arg0.device)
+        arg2 = torch.empty((B, M, N), dtype=_e, device=arg0.device)
     if tuple(arg2.shape) != (B, M, N):
         raise ValueError("batch_matmul: arg2 shape mismatch")
-    _call("loom_hip_batch_matmul", _need(arg0, "arg0", _bf16, 3), _need(arg1, "arg1", _bf16, 3),
-          _need(arg2, "arg2", _bf16, 3), B, M, N, K, tile_b, tile_m, tile_n, tile_k,
+    _call("loom_hip_batch_matmul" + _sfx, _need(arg0, "arg0", _e, 3), _need(arg1, "arg1", _e, 3),
+          _need(arg2, "arg2", _e, 3), B, M, N, K, tile_b, tile_m, tile_n, tile_k,
           _stream(arg0))
     return arg2
 
@@ -168,17 +187,18 @@ def split_k_matmul_gather(a, b, out=None, partials=None, *, tile_m=64, tile_n=64
 
     Returns (out [M,N] bf16, partials [S,M,N] fp32 -- the gathered K-slab
     products, S = ceil(K / tile_k))."""
+    _e, _sfx = _elt(a)
     M, K = a.shape
     N = b.shape[1]
     if b.shape[0] != K:
         raise ValueError("split_k_matmul_gather: inner dims differ")
     S = -(-K // tile_k) if tile_k > 0 else 0
     if out is None:
-        out = torch.empty((M, N), dtype=_bf16, device=a.device)
+        out = torch.empty((M, N), dtype=_e, device=a.device)
     if partials is None:
         partials = torch.empty((max(S, 1), M, N), dtype=_fp32, device=a.device)
-    _call("loom_hip_split_k_matmul_gather", _need(a, "a", _bf16, 2), _need(b, "b", _bf16, 2),
-          _need(out, "out", _bf16, 2), _need(partials, "partials", _fp32, 3),
+    _call("loom_hip_split_k_matmul_gather" + _sfx, _need(a, "a", _e, 2), _need(b, "b", _e, 2),
+          _need(out, "out", _e, 2), _need(partials, "partials", _fp32, 3),
           partials.numel() * 4, M, N, K, tile_m, tile_n, tile_k, _stream(a))
     return out, partials
 
@@ -189,6 +209,7 @@ def attention(k, v, q, out=None, *, scale=None, causal=False, tile_b=1, tile_m=2
 
     k [BH,D,Skv] (keys transposed), v [BH,Skv,D], q [BH,Sq,D] -> out [BH,Sq,D].
     ``scale`` defaults to 1/sqrt(D)."""
+    _e, _sfx = _elt(k)
     BH, D, Skv = k.shape
     Sq = q.shape[1]
     if tuple(v.shape) != (BH, Skv, D) or tuple(q.shape) != (BH, Sq, D):
@@ -196,9 +217,9 @@ def attention(k, v, q, out=None, *, scale=None, causal=False, tile_b=1, tile_m=2
     if scale is None:
         scale = 1.0 / math.sqrt(D)
     if out is None:
-        out = torch.empty((BH, Sq, D), dtype=_bf16, device=q.device)
-    _call("loom_hip_attention", _need(k, "k", _bf16, 3), _need(v, "v", _bf16, 3),
-          _need(q, "q", _bf16, 3), _need(out, "out", _bf16, 3), BH, Sq, Skv, D,
+        out = torch.empty((BH, Sq, D), dtype=_e, device=q.device)
+    _call("loom_hip_attention" + _sfx, _need(k, "k", _e, 3), _need(v, "v", _e, 3),
+          _need(q, "q", _e, 3), _need(out, "out", _e, 3), BH, Sq, Skv, D,
           float(scale), int(bool(causal)), tile_b, tile_m, tile_n, _stream(q))
     return out
 
@@ -219,6 +240,7 @@ def flash_decode(k, v, q, out=None, workspace=None, *, scale=None, tile_b=1, til
 
     k [B,D,S] (transposed), v [B,S,D], q [B,H,D] -> out [B,H,D].  With
     ``return_partials`` also returns the gathered (lse [ns,B,H], o [ns,B,H,D])."""
+    _e, _sfx = _elt(k)
     B, D, S = k.shape
     H = q.shape[1]
     if tuple(v.shape) != (B, S, D) or tuple(q.shape) != (B, H, D):
@@ -226,14 +248,14 @@ def flash_decode(k, v, q, out=None, workspace=None, *, scale=None, tile_b=1, til
     if scale is None:
         scale = 1.0 / math.sqrt(D)
     if out is None:
-        out = torch.empty((B, H, D), dtype=_bf16, device=q.device)
+        out = torch.empty((B, H, D), dtype=_e, device=q.device)
     if workspace is None:
         workspace = flash_decode_workspace(B, H, D, S, tile_s, q.device)
     if workspace.device != q.device or workspace.dtype != torch.uint8 or \
             not workspace.is_contiguous():
         raise ValueError("flash_decode: workspace must be a contiguous uint8 tensor")
-    _call("loom_hip_flash_decode", _need(k, "k", _bf16, 3), _need(v, "v", _bf16, 3),
-          _need(q, "q", _bf16, 3), _need(out, "out", _bf16, 3), workspace.data_ptr(),
+    _call("loom_hip_flash_decode" + _sfx, _need(k, "k", _e, 3), _need(v, "v", _e, 3),
+          _need(q, "q", _e, 3), _need(out, "out", _e, 3), workspace.data_ptr(),
           workspace.numel(), B, H, D, S, float(scale), tile_b, tile_s, tile_n, _stream(q))
     if not return_partials:
         return out
@@ -250,6 +272,7 @@ def helion_mamba2_chunk_scan_kernel(cb, x, dt, dA_cumsum, C, D, prev_states_T, o
                                     tile_k=64):
     """@helion_mamba2_chunk_scan_kernel
     (examples/mamba_chunk_scan/IR/00_from_helion_frontend.mlir:4)."""
+    _e, _sfx = _elt(x)
     b, nc, G, Q, _ = cb.shape
     _, H, L, P = x.shape
     N = C.shape[-1]
@@ -258,12 +281,12 @@ def helion_mamba2_chunk_scan_kernel(cb, x, dt, dA_cumsum, C, D, prev_states_T, o
             or tuple(prev_states_T.shape) != (b, nc, H, N, P):
         raise ValueError("helion_mamba2_chunk_scan_kernel: argument shapes disagree")
     if out is None:
-        out = torch.empty((b, H, L, P), dtype=_bf16, device=x.device)
-    _call("loom_hip_helion_mamba2_chunk_scan_kernel", _need(cb, "cb", _bf16, 5),
-          _need(x, "x", _bf16, 4), _need(dt, "dt", _fp32, 4),
-          _need(dA_cumsum, "dA_cumsum", _fp32, 4), _need(C, "C", _bf16, 4),
+        out = torch.empty((b, H, L, P), dtype=_e, device=x.device)
+    _call("loom_hip_helion_mamba2_chunk_scan_kernel" + _sfx, _need(cb, "cb", _e, 5),
+          _need(x, "x", _e, 4), _need(dt, "dt", _fp32, 4),
+          _need(dA_cumsum, "dA_cumsum", _fp32, 4), _need(C, "C", _e, 4),
           _need(D, "D", _fp32, 1), _need(prev_states_T, "prev_states_T", _fp32, 5),
-          _need(out, "out", _bf16, 4), b, nc, H, G, Q, P, N, tile_b, tile_h, tile_c,
+          _need(out, "out", _e, 4), b, nc, H, G, Q, P, N, tile_b, tile_h, tile_c,
           tile_m, tile_n, tile_k, _stream(x))
     return out
 
@@ -276,6 +299,7 @@ def ssd_prologue(x, dt, A, B, C, chunk_size, *, dA_cumsum=None, cb=None, prev_st
     """x [b,H,L,P] bf16, dt [b,H,L] fp32 (post-softplus), A [H] fp32,
     B, C [b,G,L,N] bf16 -> (dt [b,H,c,Q] (a view of dt), dA_cumsum [b,H,c,Q],
     cb [b,c,G,Q,Q] bf16, prev_states_T [b,c,H,N,P] fp32)."""
+    _e, _sfx = _elt(x)
     b, H, L, P = x.shape
     G, N = B.shape[1], B.shape[3]
     Q = int(chunk_size)
@@ -289,12 +313,12 @@ def ssd_prologue(x, dt, A, B, C, chunk_size, *, dA_cumsum=None, cb=None, prev_st
     if dA_cumsum is None:
         dA_cumsum = torch.empty((b, H, nc, Q), dtype=_fp32, device=dev)
     if cb is None:
-        cb = torch.empty((b, nc, G, Q, Q), dtype=_bf16, device=dev)
+        cb = torch.empty((b, nc, G, Q, Q), dtype=_e, device=dev)
     if prev_states_T is None:
         prev_states_T = torch.empty((b, nc, H, N, P), dtype=_fp32, device=dev)
-    _call("loom_hip_ssd_prologue", _need(x, "x", _bf16, 4), _need(dt, "dt", _fp32, 3),
-          _need(A, "A", _fp32, 1), _need(B, "B", _bf16, 4), _need(C, "C", _bf16, 4),
-          _need(dA_cumsum, "dA_cumsum", _fp32, 4), _need(cb, "cb", _bf16, 5),
+    _call("loom_hip_ssd_prologue" + _sfx, _need(x, "x", _e, 4), _need(dt, "dt", _fp32, 3),
+          _need(A, "A", _fp32, 1), _need(B, "B", _e, 4), _need(C, "C", _e, 4),
+          _need(dA_cumsum, "dA_cumsum", _fp32, 4), _need(cb, "cb", _e, 5),
           _need(prev_states_T, "prev_states_T", _fp32, 5), b, nc, H, G, Q, P, N, _stream(x))
     return dt.view(b, H, nc, Q), dA_cumsum, cb, prev_states_T
 
@@ -389,9 +413,9 @@ def dispatch(variant: str, *tensors, workspace=None, scale=None, causal=False):
     ws_ptr = workspace.data_ptr() if workspace is not None else None
     ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
     err = ctypes.create_string_buffer(512)
-    rc = _lib.loom_hip_dispatch(variant.encode(), tarr, len(ptrs), darr, len(dims),
-                                float(scale), int(bool(causal)), ws_ptr, ws_bytes,
-                                _stream(tensors[0]), err, len(err))
+    disp = _lib.loom_hip_dispatch_f16 if _elt(tensors[0])[0] == _f16 else _lib.loom_hip_dispatch
+    rc = disp(variant.encode(), tarr, len(ptrs), darr, len(dims), float(scale),
+              int(bool(causal)), ws_ptr, ws_bytes, _stream(tensors[0]), err, len(err))
     if rc != 0:
         raise LoomHipError("loom_hip_dispatch", rc, err.value.decode(errors="replace"))
     return tensors[-1], workspace

@@ -47,13 +47,14 @@ def lib():
             "loom_oracle_flash_decode": [_ptr] * 6 + [_i64] * 4 + [_f32] + [_i64] * 3,
             "loom_oracle_mamba_chunk_scan": [_ptr] * 8 + [_i64] * 10,
             "loom_oracle_mamba_prologue": [_ptr] * 9 + [_i64] * 7,
-            "loom_oracle_bf16_to_f32": [_ptr, _ptr, _i64],
-            "loom_oracle_f32_to_bf16": [_ptr, _ptr, _i64],
+            "loom_oracle_widen16": [_ptr, _ptr, _i64],
+            "loom_oracle_round16": [_ptr, _ptr, _i64],
+            "loom_oracle_set_element_type": [ctypes.c_int],
         }.items():
             fn = getattr(_lib, name)
             fn.argtypes = args
-            fn.restype = ctypes.c_int if name != "loom_oracle_bf16_to_f32" and \
-                name != "loom_oracle_f32_to_bf16" else None
+            fn.restype = None if name in ("loom_oracle_widen16", "loom_oracle_round16",
+                                          "loom_oracle_set_element_type") else ctypes.c_int
         _lib.loom_oracle_num_threads.restype = ctypes.c_int
     return _lib
 
@@ -80,6 +81,52 @@ def from_bf16(h) -> np.ndarray:
     """raw bf16 bits (uint16) -> fp32."""
     h = np.ascontiguousarray(h, dtype=np.uint16)
     return (h.astype(np.uint32) << 16).view(np.float32)
+
+
+def to_f16(a) -> np.ndarray:
+    """fp32 values -> raw IEEE f16 bits (uint16), round-to-nearest-even."""
+    return np.ascontiguousarray(a, dtype=np.float32).astype(np.float16).view(np.uint16)
+
+
+def from_f16(h) -> np.ndarray:
+    """raw IEEE f16 bits (uint16) -> fp32 (exact)."""
+    return np.ascontiguousarray(h, dtype=np.uint16).view(np.float16).astype(np.float32)
+
+
+class element_type:
+    """Context manager selecting the 16-bit format the oracle's functions read
+    and write: ``with oracle.element_type("f16"): ...`` (default "bf16")."""
+
+    def __init__(self, name: str):
+        if name not in ("bf16", "f16"):
+            raise ValueError(f"element type {name!r}: bf16 or f16")
+        self.f16 = name == "f16"
+
+    def __enter__(self):
+        self.prev = lib().loom_oracle_element_type()
+        lib().loom_oracle_set_element_type(int(self.f16))
+        return self
+
+    def __exit__(self, *exc):
+        lib().loom_oracle_set_element_type(self.prev)
+        return False
+
+
+def widen16(h) -> np.ndarray:
+    """raw 16-bit elements -> fp32 through the oracle's C conversion (current
+    element type)."""
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    out = np.empty(h.shape, np.float32)
+    lib().loom_oracle_widen16(_p(h), _p(out), h.size)
+    return out
+
+
+def round16(a) -> np.ndarray:
+    """fp32 -> raw 16-bit elements through the oracle's C conversion."""
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    out = np.empty(a.shape, np.uint16)
+    lib().loom_oracle_round16(_p(a), _p(out), a.size)
+    return out
 
 
 def _p(a: np.ndarray):

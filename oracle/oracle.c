@@ -15,8 +15,10 @@
  *     reference's initial state (m = -inf, l = 1, acc = 0);
  *   - the mamba k-loop adds one fresh partial product per tile_k step.
  * Deliberate differences from the reference (which computes in f16):
- *   - bf16 storage, fp32 arithmetic everywhere, one bf16 rounding (RNE) per
- *     output element;
+ *   - 16-bit storage in bf16 by default, or in IEEE f16 -- the reference's
+ *     own element type -- after loom_oracle_set_element_type(1); fp32
+ *     arithmetic everywhere (the reference accumulates in f16), one
+ *     round-to-nearest-even per 16-bit output element;
  *   - attention gains a `causal` flag (key j visible to query i iff j <= i);
  *   - mamba applies the Mamba-2 intra-chunk causal mask (k <= m) with a select,
  *     and generalises the reference's hard-coded group index h/8 to
@@ -41,17 +43,20 @@
 #define HOT __attribute__((target_clones("avx512f", "avx2", "default")))
 
 /* ------------------------------------------------------------------------ */
-/* bf16 helpers                                                              */
+/* 16-bit element helpers.  The restated functions read and write their     */
+/* 16-bit tensors through elt2f / f2elt, whose format is bf16 (default) or    */
+/* IEEE binary16 (the reference's own f16), set by                           */
+/* loom_oracle_set_element_type.  Both round to nearest even.                 */
 /* ------------------------------------------------------------------------ */
 
-static inline float bf2f(uint16_t h) {
+static inline float bf16_bits_to_f32(uint16_t h) {
   uint32_t u = (uint32_t)h << 16;
   float f;
   memcpy(&f, &u, 4);
   return f;
 }
 
-static inline uint16_t f2bf(float f) {
+static inline uint16_t f32_to_bf16_bits(float f) {
   uint32_t u;
   memcpy(&u, &f, 4);
   if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
@@ -59,17 +64,66 @@ static inline uint16_t f2bf(float f) {
   return (uint16_t)(u >> 16);
 }
 
+/* binary16 -> fp32, exact (IEEE 754-2008 3.6: 1 sign, 5 exponent bits with
+   bias 15, 10 fraction bits; exponent 0 = subnormal, 31 = inf/NaN) */
+static inline float f16_bits_to_f32(uint16_t h) {
+  const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  const uint32_t e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
+  uint32_t u;
+  if (e == 0) {
+    const float v = ldexpf((float)m, -24); /* m * 2^-24, exact */
+    return sign ? -v : v;
+  }
+  if (e == 31) u = sign | 0x7f800000u | (m << 13);
+  else u = sign | ((e + 112u) << 23) | (m << 13); /* rebias 15 -> 127 */
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+/* fp32 -> binary16, round to nearest even; overflow to +-inf, NaN quieted */
+static inline uint16_t f32_to_f16_bits(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  const uint16_t sign = (uint16_t)((u >> 16) & 0x8000u);
+  const uint32_t a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return (uint16_t)(sign | 0x7e00u | ((a >> 13) & 0x3ffu));
+  /* 65520 = 65504 + half an ulp and above rounds to infinity */
+  if (a >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u);
+  if (a >= 0x38800000u) { /* normal: |f| >= 2^-14 */
+    const uint32_t r = a + 0xfffu + ((a >> 13) & 1u); /* round the 13 dropped bits */
+    return (uint16_t)(sign | ((r - 0x38000000u) >> 13)); /* rebias 127 -> 15 */
+  }
+  /* subnormal (or zero): an integer multiple of 2^-24; |f| * 2^24 < 1024
+     is exact, rintf rounds it to nearest even */
+  float af;
+  memcpy(&af, &a, 4);
+  return (uint16_t)(sign | (uint16_t)rintf(af * 16777216.0f));
+}
+
+static int g_elem_f16 = 0;
+
+EXPORT void loom_oracle_set_element_type(int f16) { g_elem_f16 = f16 != 0; }
+EXPORT int loom_oracle_element_type(void) { return g_elem_f16; }
+
+static inline float elt2f(uint16_t h) {
+  return g_elem_f16 ? f16_bits_to_f32(h) : bf16_bits_to_f32(h);
+}
+static inline uint16_t f2elt(float f) {
+  return g_elem_f16 ? f32_to_f16_bits(f) : f32_to_bf16_bits(f);
+}
+
 static inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 static inline int64_t min64(int64_t a, int64_t b) { return a < b ? a : b; }
 
-EXPORT void loom_oracle_bf16_to_f32(const uint16_t *in, float *out, int64_t n) {
+EXPORT void loom_oracle_widen16(const uint16_t *in, float *out, int64_t n) {
 #pragma omp parallel for schedule(static)
-  for (int64_t i = 0; i < n; ++i) out[i] = bf2f(in[i]);
+  for (int64_t i = 0; i < n; ++i) out[i] = elt2f(in[i]);
 }
 
-EXPORT void loom_oracle_f32_to_bf16(const float *in, uint16_t *out, int64_t n) {
+EXPORT void loom_oracle_round16(const float *in, uint16_t *out, int64_t n) {
 #pragma omp parallel for schedule(static)
-  for (int64_t i = 0; i < n; ++i) out[i] = f2bf(in[i]);
+  for (int64_t i = 0; i < n; ++i) out[i] = f2elt(in[i]);
 }
 
 EXPORT int loom_oracle_num_threads(void) {
@@ -120,7 +174,7 @@ static void gemm_range(const float *A, int64_t lda, const float *B, int64_t ldb,
         for (int64_t j = 0; j < nb; ++j) {
           const float v = acc[i * GB_N + j];
           if (out_f32) out_f32[(i0 + i) * ldo + j0 + j] = v;
-          if (out_bf16) out_bf16[(i0 + i) * ldo + j0 + j] = f2bf(v);
+          if (out_bf16) out_bf16[(i0 + i) * ldo + j0 + j] = f2elt(v);
         }
     }
   }
@@ -143,8 +197,8 @@ EXPORT int loom_oracle_matmul(const uint16_t *x, const uint16_t *y, uint16_t *ou
   float *A = (float *)malloc(sizeof(float) * M * K);
   float *B = (float *)malloc(sizeof(float) * K * N);
   if (!A || !B) { free(A); free(B); return 2; }
-  loom_oracle_bf16_to_f32(x, A, M * K);
-  loom_oracle_bf16_to_f32(y, B, K * N);
+  loom_oracle_widen16(x, A, M * K);
+  loom_oracle_widen16(y, B, K * N);
   gemm_range(A, K, B, N, M, N, 0, K, NULL, out, N);
   free(A);
   free(B);
@@ -168,8 +222,8 @@ EXPORT int loom_oracle_batch_matmul(const uint16_t *a0, const uint16_t *a1, uint
   float *B = (float *)malloc(sizeof(float) * K * N);
   if (!A || !B) { free(A); free(B); return 2; }
   for (int64_t b = 0; b < Bt; ++b) {
-    loom_oracle_bf16_to_f32(a0 + b * M * K, A, M * K);
-    loom_oracle_bf16_to_f32(a1 + b * K * N, B, K * N);
+    loom_oracle_widen16(a0 + b * M * K, A, M * K);
+    loom_oracle_widen16(a1 + b * K * N, B, K * N);
     gemm_range(A, K, B, N, M, N, 0, K, NULL, a2 + b * M * N, N);
   }
   free(A);
@@ -196,8 +250,8 @@ EXPORT int loom_oracle_split_k_matmul_gather(const uint16_t *a, const uint16_t *
   float *A = (float *)malloc(sizeof(float) * M * K);
   float *B = (float *)malloc(sizeof(float) * K * N);
   if (!A || !B) { free(A); free(B); return 2; }
-  loom_oracle_bf16_to_f32(a, A, M * K);
-  loom_oracle_bf16_to_f32(b, B, K * N);
+  loom_oracle_widen16(a, A, M * K);
+  loom_oracle_widen16(b, B, K * N);
   for (int64_t s = 0; s < S; ++s) {
     const int64_t k0 = s * tile_k, k1 = min64(K, k0 + tile_k);
     gemm_range(A, K, B, N, M, N, k0, k1, partials + s * M * N, NULL, N);
@@ -206,7 +260,7 @@ EXPORT int loom_oracle_split_k_matmul_gather(const uint16_t *a, const uint16_t *
   for (int64_t e = 0; e < M * N; ++e) {
     float acc = 0.0f;
     for (int64_t s = 0; s < S; ++s) acc += partials[s * M * N + e];
-    out[e] = f2bf(acc);
+    out[e] = f2elt(acc);
   }
   free(A);
   free(B);
@@ -288,7 +342,7 @@ EXPORT int loom_oracle_attention(const uint16_t *k, const uint16_t *v, const uin
       float *l = (float *)malloc(sizeof(float) * rows);
       float *P = (float *)malloc(sizeof(float) * tile_n);
       const uint16_t *qb = q + (bh * Sq + i0) * D;
-      for (int64_t e = 0; e < rows * D; ++e) Q[e] = bf2f(qb[e]);
+      for (int64_t e = 0; e < rows * D; ++e) Q[e] = elt2f(qb[e]);
       for (int64_t i = 0; i < rows; ++i) { m[i] = -INFINITY; l[i] = 1.0f; }
       const int64_t nkt = cdiv(Skv, tile_n);
       for (int64_t kt = 0; kt < nkt; ++kt) {
@@ -296,11 +350,11 @@ EXPORT int loom_oracle_attention(const uint16_t *k, const uint16_t *v, const uin
         if (causal && j0 > i0 + rows - 1) break; /* every key of the tile is masked */
         for (int64_t d = 0; d < D; ++d) {
           const uint16_t *kr = k + (bh * D + d) * Skv + j0;
-          for (int64_t n = 0; n < nk; ++n) Kt[d * tile_n + n] = bf2f(kr[n]);
+          for (int64_t n = 0; n < nk; ++n) Kt[d * tile_n + n] = elt2f(kr[n]);
         }
         for (int64_t n = 0; n < nk; ++n) {
           const uint16_t *vr = v + (bh * Skv + j0 + n) * D;
-          for (int64_t d = 0; d < D; ++d) Vt[n * D + d] = bf2f(vr[d]);
+          for (int64_t d = 0; d < D; ++d) Vt[n * D + d] = elt2f(vr[d]);
         }
         for (int64_t i = 0; i < rows; ++i) {
           float *si = S + i * tile_n;
@@ -318,7 +372,7 @@ EXPORT int loom_oracle_attention(const uint16_t *k, const uint16_t *v, const uin
       }
       uint16_t *ob = out + (bh * Sq + i0) * D;
       for (int64_t i = 0; i < rows; ++i)
-        for (int64_t d = 0; d < D; ++d) ob[i * D + d] = f2bf(acc[i * D + d] / l[i]);
+        for (int64_t d = 0; d < D; ++d) ob[i * D + d] = f2elt(acc[i * D + d] / l[i]);
       free(Q); free(S); free(Vt); free(Kt); free(acc); free(m); free(l); free(P);
     }
   }
@@ -355,18 +409,18 @@ EXPORT int loom_oracle_flash_decode(const uint16_t *k, const uint16_t *v, const 
       float *m = (float *)malloc(sizeof(float) * H);
       float *l = (float *)malloc(sizeof(float) * H);
       float *P = (float *)malloc(sizeof(float) * tile_n);
-      for (int64_t e = 0; e < H * D; ++e) Q[e] = bf2f(q[b * H * D + e]);
+      for (int64_t e = 0; e < H * D; ++e) Q[e] = elt2f(q[b * H * D + e]);
       for (int64_t h = 0; h < H; ++h) { m[h] = -INFINITY; l[h] = 1.0f; }
       const int64_t s0 = s * tile_s, s1 = min64(S, s0 + tile_s);
       for (int64_t j0 = s0; j0 < s1; j0 += tile_n) {
         const int64_t nk = min64(tile_n, s1 - j0);
         for (int64_t d = 0; d < D; ++d) {
           const uint16_t *kr = k + (b * D + d) * S + j0;
-          for (int64_t n = 0; n < nk; ++n) Kt[d * tile_n + n] = bf2f(kr[n]);
+          for (int64_t n = 0; n < nk; ++n) Kt[d * tile_n + n] = elt2f(kr[n]);
         }
         for (int64_t n = 0; n < nk; ++n) {
           const uint16_t *vr = v + (b * S + j0 + n) * D;
-          for (int64_t d = 0; d < D; ++d) Vt[n * D + d] = bf2f(vr[d]);
+          for (int64_t d = 0; d < D; ++d) Vt[n * D + d] = elt2f(vr[d]);
         }
         for (int64_t h = 0; h < H; ++h) {
           float *sh = Sc + h * tile_n;
@@ -403,7 +457,7 @@ EXPORT int loom_oracle_flash_decode(const uint16_t *k, const uint16_t *v, const 
         const float *os = o_ws + ((s * B + b) * H + h) * D;
         for (int64_t d = 0; d < Dc; ++d) o[d] += os[d] * w;
       }
-      for (int64_t d = 0; d < Dc; ++d) out[(b * H + h) * D + d] = f2bf(o[d]);
+      for (int64_t d = 0; d < Dc; ++d) out[(b * H + h) * D + d] = f2elt(o[d]);
     }
   }
   return 0;
@@ -463,7 +517,7 @@ EXPORT int loom_oracle_mamba_chunk_scan(const uint16_t *cb, const uint16_t *x, c
               for (int64_t j = 0; j < cols; ++j) {
                 float s = 0.0f;
                 for (int64_t n = 0; n < N; ++n)
-                  s += bf2f(Cc[(m0 + i) * N + n]) * pv[n * P + p0 + j];
+                  s += elt2f(Cc[(m0 + i) * N + n]) * pv[n * P + p0 + j];
                 acc[i * tile_n + j] = s * e;
               }
             }
@@ -478,7 +532,7 @@ EXPORT int loom_oracle_mamba_chunk_scan(const uint16_t *cb, const uint16_t *x, c
                   float w = 0.0f;
                   if (ki <= mi) {
                     const float decay = expf(dAc[mi] - dAc[ki]);
-                    w = bf2f(cbc[mi * Q + ki]) * decay;
+                    w = elt2f(cbc[mi * Q + ki]) * decay;
                     w = w * dtc[ki];
                   }
                   W[i * tile_k + kk] = w;
@@ -488,7 +542,7 @@ EXPORT int loom_oracle_mamba_chunk_scan(const uint16_t *cb, const uint16_t *x, c
                 for (int64_t j = 0; j < cols; ++j) {
                   float s = 0.0f;
                   for (int64_t kk = 0; kk < nk; ++kk)
-                    s += W[i * tile_k + kk] * bf2f(xc[(k0 + kk) * P + p0 + j]);
+                    s += W[i * tile_k + kk] * elt2f(xc[(k0 + kk) * P + p0 + j]);
                   part[i * tile_n + j] = s;
                 }
               for (int64_t i = 0; i < rows; ++i)
@@ -496,8 +550,8 @@ EXPORT int loom_oracle_mamba_chunk_scan(const uint16_t *cb, const uint16_t *x, c
             }
             for (int64_t i = 0; i < rows; ++i)
               for (int64_t j = 0; j < cols; ++j) {
-                const float xv = bf2f(xc[(m0 + i) * P + p0 + j]);
-                oc[(m0 + i) * P + p0 + j] = f2bf(acc[i * tile_n + j] + xv * Dh[h]);
+                const float xv = elt2f(xc[(m0 + i) * P + p0 + j]);
+                oc[(m0 + i) * P + p0 + j] = f2elt(acc[i * tile_n + j] + xv * Dh[h]);
               }
           }
         }
@@ -556,9 +610,9 @@ EXPORT int loom_oracle_mamba_prologue(const uint16_t *x, const float *dt, const 
             float s = 0.0f;
             if (j <= i)
               for (int64_t n = 0; n < N; ++n)
-                s += bf2f(C[((b * G + g) * L + c * Q + i) * N + n]) *
-                     bf2f(Bm[((b * G + g) * L + c * Q + j) * N + n]);
-            cb[(((b * nc + c) * G + g) * Q + i) * Q + j] = f2bf(s);
+                s += elt2f(C[((b * G + g) * L + c * Q + i) * N + n]) *
+                     elt2f(Bm[((b * G + g) * L + c * Q + j) * N + n]);
+            cb[(((b * nc + c) * G + g) * Q + i) * Q + j] = f2elt(s);
           }
   /* chunk states and the sequential inter-chunk pass */
 #pragma omp parallel for collapse(2) schedule(dynamic)
@@ -586,8 +640,8 @@ EXPORT int loom_oracle_mamba_prologue(const uint16_t *x, const float *dt, const 
           const uint16_t *Br = Bm + ((b * G + g) * L + c * Q + kk) * N;
           const uint16_t *xr = x + ((b * Hh + h) * L + c * Q + kk) * P;
           for (int64_t n = 0; n < N; ++n) {
-            const float bw = bf2f(Br[n]) * w[kk];
-            for (int64_t p = 0; p < P; ++p) st[n * P + p] += bw * bf2f(xr[p]);
+            const float bw = elt2f(Br[n]) * w[kk];
+            for (int64_t p = 0; p < P; ++p) st[n * P + p] += bw * elt2f(xr[p]);
           }
         }
       }

@@ -257,3 +257,82 @@ def test_mamba_tile_invariance(golden):
     for t in [(4, 8, 4), (16, 16, 3), (8, 5, 32)]:
         o, _ = _mamba_chain(g, t)
         assert_close(from_bf16(o), from_bf16(ref), atol=1e-3, rtol=2 * RT, what=str(t))
+
+
+# ------------------------------------------------------------- f16 element mode
+# The oracle's f16 conversions are written from the IEEE 754 binary16 layout;
+# numpy's float16 (an independent implementation) pins them: every one of the
+# 65536 patterns widens identically, and rounding agrees on every float32
+# class -- normals, the subnormal range and its boundary, halfway cases,
+# overflow to infinity at 65520, zeros, infinities and NaN.
+
+def test_f16_widen_exhaustive():
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    with oracle.element_type("f16"):
+        got = oracle.widen16(h)
+    ref = h.view(np.float16).astype(np.float32)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan)
+    np.testing.assert_array_equal(got[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+
+
+@pytest.mark.filterwarnings("ignore::RuntimeWarning")
+def test_f16_round_matches_numpy():
+    rng = np.random.default_rng(5)
+    parts = [
+        (rng.standard_normal(200000) * 10.0 ** rng.integers(-9, 6, 200000)).astype(np.float32),
+        rng.uniform(-70000, 70000, 100000).astype(np.float32),
+        # halfway points between consecutive f16 values, normal and subnormal
+        (np.arange(0, 65535, dtype=np.uint32).astype(np.uint16).view(np.float16)
+         .astype(np.float64)[:-1] + np.diff(np.arange(0, 65535, dtype=np.uint32).astype(np.uint16)
+                                             .view(np.float16).astype(np.float64)) / 2)
+        .astype(np.float32),
+        np.array([0.0, -0.0, 65504.0, 65519.996, 65520.0, -65520.0, 2.0 ** -14, 2.0 ** -24,
+                  2.0 ** -25, 3 * 2.0 ** -26, 2.0 ** -26, np.inf, -np.inf], np.float32),
+    ]
+    with np.errstate(invalid="ignore", over="ignore"):
+        x = np.concatenate([p[np.isfinite(p)] for p in parts[:3]] + [parts[3]]).astype(np.float32)
+    with oracle.element_type("f16"):
+        got = oracle.round16(x)
+    ref = x.astype(np.float16).view(np.uint16)
+    np.testing.assert_array_equal(got, ref)
+    with oracle.element_type("f16"):
+        assert np.isnan(oracle.round16(np.array([np.nan], np.float32)).view(np.float16)[0])
+
+
+def test_element_type_is_scoped():
+    x = np.array([1.0 / 3.0], np.float32)
+    with oracle.element_type("f16"):
+        assert oracle.round16(x)[0] == np.float16(1 / 3).view(np.uint16)
+    assert oracle.round16(x)[0] == oracle.to_bf16(x)[0]
+
+
+def test_f16_matmul_and_attention_against_float64():
+    """The restated functions in f16 mode: inputs widen from f16, outputs
+    round to f16 (checked against float64 brute force of the same f16 values)."""
+    rng = np.random.default_rng(6)
+    x = oracle.to_f16(rng.standard_normal((40, 72)))
+    y = oracle.to_f16(rng.standard_normal((72, 24)))
+    with oracle.element_type("f16"):
+        out = oracle.from_f16(oracle.matmul(x, y, 16, 16, 32))
+    ref = oracle.from_f16(x).astype(np.float64) @ oracle.from_f16(y).astype(np.float64)
+    np.testing.assert_allclose(out, ref, rtol=2e-3, atol=2e-3)
+    # integer-valued operands: every product and sum exact, one rounding
+    xi = oracle.to_f16(rng.integers(-4, 5, (32, 64)).astype(np.float32))
+    yi = oracle.to_f16(rng.integers(-4, 5, (64, 16)).astype(np.float32))
+    with oracle.element_type("f16"):
+        oi = oracle.matmul(xi, yi, 16, 16, 16)
+    exact = oracle.from_f16(xi).astype(np.int64) @ oracle.from_f16(yi).astype(np.int64)
+    np.testing.assert_array_equal(oi, oracle.to_f16(exact.astype(np.float32)))
+    BH, S, D = 2, 48, 32
+    k = oracle.to_f16(rng.standard_normal((BH, D, S)))
+    v = oracle.to_f16(rng.standard_normal((BH, S, D)))
+    q = oracle.to_f16(rng.standard_normal((BH, S, D)))
+    with oracle.element_type("f16"):
+        o = oracle.from_f16(oracle.attention(k, v, q, 1 / np.sqrt(D), True, 1, 16, 16))
+    kf, vf, qf = (oracle.from_f16(t).astype(np.float64) for t in (k, v, q))
+    s = np.einsum("bqd,bdk->bqk", qf, kf) / np.sqrt(D)
+    s[:, np.triu_indices(S, 1)[0], np.triu_indices(S, 1)[1]] = -np.inf
+    p = np.exp(s - s.max(-1, keepdims=True))
+    ref = np.einsum("bqk,bkd->bqd", p / p.sum(-1, keepdims=True), vf)
+    np.testing.assert_allclose(o, ref, rtol=2e-3, atol=2e-3)
