@@ -16,6 +16,9 @@ of one call each, inputs resident in HBM.  It carries
                 operands never stay in the 256 MB Infinity Cache between
                 calls, with its roofline fraction.
 
+Before timing, each measurement runs its own call untimed for --settle-ms of
+GPU time (clocks take on the order of 100 ms of load to settle).
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
                        [--kernels all|none|mm,bmm,...]
 """
@@ -39,8 +42,10 @@ TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic.json")
 def parse():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--settle-ms", type=float, default=150.0,
+                    help="untimed GPU work before each measurement (clocks and power settle)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--kernels", default="all", help="per-kernel table: all, none or a list")
     ap.add_argument("--iters", type=int, default=20, help="timed calls per kernel in the table")
@@ -67,6 +72,25 @@ def median(xs):
     xs = sorted(xs)
     n = len(xs)
     return xs[n // 2] if n % 2 else 0.5 * (xs[n // 2 - 1] + xs[n // 2])
+
+
+def settle(torch, fn, ms):
+    """Run fn(i) back to back, untimed, until about `ms` of GPU time has
+    passed: MI355X clocks take on the order of 100 ms of sustained load to
+    settle, and a measurement started cold reads up to 20% slow."""
+    if ms <= 0:
+        return
+    s = torch.cuda.current_stream()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    done, i = 0.0, 0
+    while done < ms and i < 100000:
+        a.record(s)
+        for _ in range(8):
+            fn(i)
+            i += 1
+        b.record(s)
+        torch.cuda.synchronize()
+        done += a.elapsed_time(b)
 
 
 def time_back_to_back(torch, fn, iters):
@@ -286,6 +310,7 @@ def main():
 
     cases = make_cases(torch, lh)
     head = cases["bmm"]()
+    settle(torch, head["fn"], args.settle_ms)
     for i in range(args.warmup):
         head["fn"](i)
     torch.cuda.synchronize()
@@ -312,6 +337,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "settle_ms": args.settle_ms,
         "ms_per_step": round(ms_step, 5),
         "higher_is_better": True,
         "scaling": "weak",
@@ -324,7 +350,7 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                     "traffic": traffic_for("gemm_dma_kernel<32,4,false>")},
+                     "traffic": traffic_for("gemm_pipe_kernel<false,false>")},
     }
     a0_a1 = None
     if not args.no_cpu:
@@ -345,8 +371,7 @@ def main():
         table = {}
         for name in names:
             case = cases[name]()
-            for i in range(2):
-                case["fn"](i)
+            settle(torch, case["fn"], args.settle_ms / 3)
             ms = time_back_to_back(torch, case["fn"], args.iters)
             table[name] = report(case, ms)
             print(f"# {name}: {table[name]}", file=sys.stderr, flush=True)

@@ -254,6 +254,59 @@ LOOM_DEV u32x2_t lds_read_tr16(const lds_char_t* p) {
                    (__attribute__((address_space(3))) s16x4_t*)(p)));
 }
 
+// ---------------------------------------------------------------------------
+// MFMAs with the accumulator pinned to AGPRs.  Written as inline assembly
+// because, with 64 accumulator chains live across an unrolled loop, the
+// register allocator otherwise splits some of them into VGPRs and copies
+// them back and forth around every MFMA.  The compiler's hazard recognizer
+// does not see these instructions: callers let the MFMAs retire (s_nop)
+// before reading an accumulator with any other instruction, and after
+// writing one before the first MFMA that reads it.
+// ---------------------------------------------------------------------------
+template <bool H>
+LOOM_DEV void mfma_agpr(f32x4_t& acc, const u32x4_t& a, const u32x4_t& b) {
+  if constexpr (H)
+    asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+  else
+    asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+// The same MFMA with one LDS-DMA load (global_load_lds_dwordx4, scalar base
+// + per-lane 32-bit byte offset, 16 bytes per lane to lds + 16 lane) folded
+// around it: M0 is written before the MFMA, which supplies the wait state
+// M0 needs before the load reads it.
+template <bool H>
+LOOM_DEV void mfma_agpr_dma(f32x4_t& acc, const u32x4_t& a, const u32x4_t& b, uint32_t lds,
+                            uint32_t voff, const void* sbase) {
+  if constexpr (H)
+    asm volatile(
+        "s_mov_b32 m0, %3\n\t"
+        "v_mfma_f32_16x16x32_f16 %0, %1, %2, %0\n\t"
+        "global_load_lds_dwordx4 %4, %5"
+        : "+a"(acc)
+        : "v"(a), "v"(b), "s"(lds), "v"(voff), "s"(sbase)
+        : "memory", "m0");
+  else
+    asm volatile(
+        "s_mov_b32 m0, %3\n\t"
+        "v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0\n\t"
+        "global_load_lds_dwordx4 %4, %5"
+        : "+a"(acc)
+        : "v"(a), "v"(b), "s"(lds), "v"(voff), "s"(sbase)
+        : "memory", "m0");
+}
+// LDS-DMA load with a scalar base and a per-lane 32-bit byte offset
+LOOM_DEV void dma_load16_s(uint32_t voff, const void* sbase, uint32_t lds) {
+  asm volatile(
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %0, %1"
+      :
+      : "v"(voff), "s"(sbase), "s"(lds)
+      : "memory", "m0");
+}
+// 48 wait states: every MFMA issued before has written its result
+LOOM_DEV void mfma_drain() { asm volatile("s_nop 15\n\ts_nop 15\n\ts_nop 15" ::: "memory"); }
+
 // s_waitcnt vmcnt(n), leaving LDS and export counters alone
 #define LOOM_WAIT_VMCNT(n) \
   __builtin_amdgcn_s_waitcnt(((n) & 15) | ((((n) >> 4) & 3) << 14) | 0x0F70)

@@ -426,6 +426,234 @@ __global__ void __launch_bounds__(256) gemm_dma_kernel(GemmParams p) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// 256x256 tile, software-pipelined: the production path for K ranges that
+// are whole multiples of NS*BK (128).  Same LDS layout, swizzles, operand
+// roles and accumulation order as gemm_dma_kernel (bitwise identical
+// results); what changes is the schedule:
+//   - the MFMA fragments of stage it+1 are read from LDS into a second
+//     register set while the MFMAs of stage it run, one read between every
+//     two MFMAs;
+//   - this wave's DMA for stage it+NS is folded between the MFMAs too (one
+//     per group of eight), with a scalar base per stage and per-lane 32-bit
+//     offsets that stay the same for every stage;
+//   - the accumulators live in AGPRs (inline-asm MFMAs, see mfma_agpr) and
+//     the loop body has no data-dependent branch: past the last stage the
+//     DMA re-reads the last stage into a buffer that is never read again;
+//   - full tiles convert every accumulator first and then store without
+//     bounds checks.
+// One barrier per stage: it publishes stage it+1 (everyone's DMA landed,
+// each wave having waited for its own) and, because every wave waited for
+// its fragment reads of stage it before it, frees stage it's buffer for the
+// DMA of stage it+NS.
+// ---------------------------------------------------------------------------
+template <bool OUT_F32, bool H>
+__global__ void __launch_bounds__(256) gemm_pipe_kernel(GemmParams p) {
+  constexpr int NS = 4, BK = 32, BM = 256, BN = 256;
+  constexpr int A_BYTES = BM * BK * 2, B_BYTES = BK * BN * 2;
+  constexpr int A_INSTR = A_BYTES / 1024 / 4;   // DMA instructions per wave per stage
+  constexpr int B_INSTR = B_BYTES / 1024 / 4;
+  constexpr int LPW = A_INSTR + B_INSTR;
+  static_assert(LPW == 8, "one DMA per group of eight MFMAs");
+  __shared__ __attribute__((aligned(1024))) char smem[NS * (A_BYTES + B_BYTES)];
+  lds_char_t* const lds = (lds_char_t*)smem;
+  auto stageA = [&](int s) { return lds + s * A_BYTES; };
+  auto stageB = [&](int s) { return lds + NS * A_BYTES + s * B_BYTES; };
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+
+  // ---- which tile, which z (XCD-contiguous, grouped by 8 tile rows)
+  const int nblocks = p.tiles_m * p.tiles_n * p.nz;
+  const int bid = xcd_remap(blockIdx.x, nblocks);
+  const int per_z = p.tiles_m * p.tiles_n;
+  const int z = bid / per_z;
+  const int t = bid - z * per_z;
+  constexpr int GM = 8;
+  const int group = t / (GM * p.tiles_n);
+  const int first_m = group * GM;
+  const int gsz = min(p.tiles_m - first_m, GM);
+  const int tin = t - group * GM * p.tiles_n;
+  const int64_t m0 = (int64_t)(first_m + tin % gsz) * BM;
+  const int64_t n0 = (int64_t)(tin / gsz) * BN;
+
+  const uint16_t* A = p.A;
+  const uint16_t* B = p.B;
+  int64_t kb = 0, ke = p.k_total;
+  if (p.split) {
+    kb = (int64_t)z * p.k_slab;
+    ke = min(p.k_total, kb + p.k_slab);
+  } else {
+    A += (int64_t)z * p.za;
+    B += (int64_t)z * p.zb;
+  }
+  const int nk = (int)((ke - kb) / BK);   // the host guarantees nk % NS == 0, nk >= NS
+
+  // ---- per-lane DMA byte offsets (rows / columns past the operand clamped
+  // inside it; what they load is never stored)
+  uint32_t aoff[A_INSTR], boff[B_INSTR];
+#pragma unroll
+  for (int i = 0; i < A_INSTR; ++i) {
+    const int row = (wave * A_INSTR + i) * 16 + lane / 4;
+    const int64_t gm = min<int64_t>(row, p.M - 1 - m0);
+    aoff[i] = (uint32_t)(gm * p.lda * 2 + ((lane % 4) ^ a_swz<BK>(row)) * 16);
+  }
+#pragma unroll
+  for (int i = 0; i < B_INSTR; ++i) {
+    const int row = (wave * B_INSTR + i) * 2 + lane / 32;
+    const int64_t gn = min<int64_t>(((lane % 32) ^ b_swz(row)) * 8, p.N - 8 - n0);
+    boff[i] = (uint32_t)(row * p.ldb * 2 + gn * 2);
+  }
+  const uint16_t* const Abase = A + m0 * p.lda + kb;
+  const uint16_t* const Bbase = B + n0 + kb * p.ldb;
+  const uint32_t la0 = lds_addr(stageA(0)), lb0 = lds_addr(stageB(0));
+  auto issue = [&](int s, int stage) {
+    const uint16_t* ab = Abase + (int64_t)stage * BK;
+    const uint16_t* bb = Bbase + (int64_t)stage * BK * p.ldb;
+#pragma unroll
+    for (int i = 0; i < A_INSTR; ++i)
+      dma_load16_s(aoff[i], ab, la0 + s * A_BYTES + (wave * A_INSTR + i) * 1024);
+#pragma unroll
+    for (int i = 0; i < B_INSTR; ++i)
+      dma_load16_s(boff[i], bb, lb0 + s * B_BYTES + (wave * B_INSTR + i) * 1024);
+  };
+
+  // ---- fragment addresses.  A: one lane offset (tile tm moves by 1 KB; the
+  // swizzle depends on the row's low four bits only).  B: the 16-byte chunk
+  // of tile tn is (2 tn | c4 >> 1) ^ swizzle, i.e. the lane offset XOR
+  // (tn << 5).  Stage bases are immediate offsets.
+  const int wm = wave & 1, wn = wave >> 1;
+  const int lr = lane & 15, lg = lane >> 4;
+  const uint32_t a_lane = (uint32_t)((wm * 128 + lr) * (BK * 2) + ((lg ^ a_swz<BK>(lr)) * 16));
+  uint32_t b_lane[8];
+  {
+    const int a = lr >> 2, c4 = lr & 3;
+    const int k0r = lg * 8 + a;
+    const uint32_t base =
+        (uint32_t)(k0r * 512 + wn * 256 + (((c4 >> 1) ^ b_swz(k0r)) * 16) + (c4 & 1) * 8);
+#pragma unroll
+    for (int tn = 0; tn < 8; ++tn) b_lane[tn] = base ^ (uint32_t)(tn << 5);
+  }
+  auto read_a = [&](int s, int tm) {
+    return *(const __attribute__((address_space(3))) u32x4_t*)(stageA(s) + a_lane + tm * 1024);
+  };
+  auto read_b = [&](int s, int tn, int half) {
+    return lds_read_tr16(stageB(s) + b_lane[tn] + half * 4 * 512);
+  };
+
+  f32x4_t acc[8][8];  // [n tile][m tile]: C^T tiles
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  mfma_drain();
+
+  // ---- prologue: NS stages in flight, fragments of stage 0
+  u32x4_t af[2][8], bfr[2][8];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) issue(s, s);
+  LOOM_WAIT_VMCNT((NS - 1) * LPW);
+  barrier_nofence();
+#pragma unroll
+  for (int q = 0; q < 8; ++q) {
+    af[0][q] = read_a(0, q);
+    const u32x2_t lo = read_b(0, q, 0), hi = read_b(0, q, 1);
+    bfr[0][q] = u32x4_t{lo[0], lo[1], hi[0], hi[1]};
+  }
+
+  // ---- one stage: 64 MFMAs on the current set; per group of eight (tile
+  // tn): the next set's B fragment tn (two transposed reads) and A fragment
+  // tn, and this wave's DMA number tn for stage it+NS
+  auto step = [&](int u, int it, const u32x4_t (&fa)[8], const u32x4_t (&fb)[8], u32x4_t (&na)[8],
+                  u32x4_t (&nb)[8]) {
+    LOOM_WAIT_VMCNT((NS - 2) * LPW);
+    LOOM_WAIT_LGKM0();
+    barrier_nofence();
+    const int sn = (u + 1) % NS;
+    const int sd = min(it + NS, nk - 1);
+    const uint16_t* ab = Abase + (int64_t)sd * BK;
+    const uint16_t* bb = Bbase + (int64_t)sd * BK * p.ldb;
+    u32x2_t lo[8];
+#pragma unroll
+    for (int i = 0; i < 64; ++i) {
+      const int tn = i >> 3, tm = i & 7;
+      if (tm == 4) {
+        if (tn < A_INSTR)
+          mfma_agpr_dma<H>(acc[tn][tm], fb[tn], fa[tm], la0 + u * A_BYTES + (wave * A_INSTR + tn) * 1024,
+                           aoff[tn], ab);
+        else
+          mfma_agpr_dma<H>(acc[tn][tm], fb[tn], fa[tm],
+                           lb0 + u * B_BYTES + (wave * B_INSTR + tn - A_INSTR) * 1024,
+                           boff[tn - A_INSTR], bb);
+      } else {
+        mfma_agpr<H>(acc[tn][tm], fb[tn], fa[tm]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      if (tm == 0) lo[tn] = read_b(sn, tn, 0);
+      if (tm == 2) {
+        const u32x2_t hi = read_b(sn, tn, 1);
+        nb[tn] = u32x4_t{lo[tn][0], lo[tn][1], hi[0], hi[1]};
+      }
+      if (tm == 6) na[tn] = read_a(sn, tn);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  for (int it0 = 0; it0 < nk; it0 += NS) {
+#pragma unroll
+    for (int u = 0; u < NS; ++u)
+      step(u, it0 + u, af[u & 1], bfr[u & 1], af[(u & 1) ^ 1], bfr[(u & 1) ^ 1]);
+  }
+  LOOM_WAIT_VMCNT(0);   // the trailing re-reads land before the workgroup ends
+  mfma_drain();
+
+  // ---- epilogue: acc[tn][tm][i] = C[m][n + i], m = tile row lr, n = 4 lg
+  void* const cz = OUT_F32 ? (void*)(static_cast<float*>(p.C) + (int64_t)z * p.zc)
+                           : (void*)(static_cast<uint16_t*>(p.C) + (int64_t)z * p.zc);
+  const int64_t r0 = m0 + wm * 128 + lr, c0 = n0 + wn * 128 + lg * 4;
+  if (m0 + BM <= p.M && n0 + BN <= p.N) {
+    if constexpr (OUT_F32) {
+      float* cb = static_cast<float*>(cz) + r0 * p.ldc + c0;
+#pragma unroll
+      for (int tm = 0; tm < 8; ++tm)
+#pragma unroll
+        for (int tn = 0; tn < 8; ++tn)
+          *reinterpret_cast<f32x4_t*>(cb + (int64_t)(tm * 16) * p.ldc + tn * 16) = acc[tn][tm];
+    } else {
+      u32x2_t pk[8][8];
+#pragma unroll
+      for (int tn = 0; tn < 8; ++tn)
+#pragma unroll
+        for (int tm = 0; tm < 8; ++tm)
+          pk[tn][tm] = u32x2_t{pack2<H>(acc[tn][tm][0], acc[tn][tm][1]),
+                               pack2<H>(acc[tn][tm][2], acc[tn][tm][3])};
+      uint16_t* cb = static_cast<uint16_t*>(cz) + r0 * p.ldc + c0;
+#pragma unroll
+      for (int tm = 0; tm < 8; ++tm)
+#pragma unroll
+        for (int tn = 0; tn < 8; ++tn)
+          *reinterpret_cast<u32x2_t*>(cb + (int64_t)(tm * 16) * p.ldc + tn * 16) = pk[tn][tm];
+    }
+    return;
+  }
+#pragma unroll
+  for (int tm = 0; tm < 8; ++tm) {
+    __builtin_amdgcn_sched_barrier(0);
+    const int64_t row = r0 + tm * 16;
+    if (row >= p.M) continue;
+#pragma unroll
+    for (int tn = 0; tn < 8; ++tn) {
+      const int64_t col = c0 + tn * 16;
+      if (col >= p.N) continue;
+      const f32x4_t v = acc[tn][tm];
+      if constexpr (OUT_F32)
+        *reinterpret_cast<f32x4_t*>(static_cast<float*>(cz) + row * p.ldc + col) = v;
+      else
+        *reinterpret_cast<u32x2_t*>(static_cast<uint16_t*>(cz) + row * p.ldc + col) =
+            u32x2_t{pack2<H>(v[0], v[1]), pack2<H>(v[2], v[3])};
+    }
+  }
+}
+
 // out[e] = bf16( sum_{s ascending} G[s][e] ) -- the split-0 reduction of
 // examples/split_k_mm_gather/IR/00_from_helion_frontend.mlir:34-51.
 template <bool H>
@@ -497,11 +725,22 @@ hipError_t launch_gemm(GemmParams p, int64_t tile_m, int64_t tile_n, bool aligne
   p.tiles_n = (int)cdiv64(p.N, tile_n);
   if (tile_m == 64) return launch_tile<64, 64, 1, 2, H>(p, aligned, out_f32, st);
   if (tile_m == 128) return launch_tile<128, 128, 2, 2, H>(p, aligned, out_f32, st);
-  // 256x256: the LDS-DMA kernel needs whole BK steps in every K range
+  // 256x256, pipelined: every K range a whole number of 128-deep rounds, and
+  // the per-lane DMA byte offsets within 32 bits
+  const dim3 grid((unsigned)((int64_t)p.tiles_m * p.tiles_n * p.nz)), block(256);
+  const bool pipe = aligned && p.k_total % 128 == 0 && (!p.split || p.k_slab % 128 == 0) &&
+                    p.lda < (1 << 22) && p.ldb < (1 << 22) && p.N >= 8;
+  if (pipe) {
+    if (out_f32)
+      hipLaunchKernelGGL((gemm_pipe_kernel<true, H>), grid, block, 0, st, p);
+    else
+      hipLaunchKernelGGL((gemm_pipe_kernel<false, H>), grid, block, 0, st, p);
+    return hipGetLastError();
+  }
+  // otherwise the LDS-DMA kernel needs whole BK steps in every K range
   constexpr int BK = LOOM_GEMM_DMA_BK, NS = LOOM_GEMM_DMA_NS;
   const bool dma = aligned && p.k_total % BK == 0 && (!p.split || p.k_slab % BK == 0);
   if (dma) {
-    const dim3 grid((unsigned)((int64_t)p.tiles_m * p.tiles_n * p.nz)), block(256);
     if (out_f32)
       hipLaunchKernelGGL((gemm_dma_kernel<BK, NS, true, H>), grid, block, 0, st, p);
     else
