@@ -135,9 +135,9 @@ def make_cases(torch, lh):
     def mm():
         x, y = unif(1024, 1024), unif(1024, 1024)
         out = torch.empty(1024, 1024, dtype=bf, device=cuda)
-        return dict(fn=lambda i: lh.matmul(x, y, out, tile_m=128, tile_n=128, tile_k=64),
+        return dict(fn=lambda i: lh.matmul(x, y, out, tile_m=64, tile_n=64, tile_k=64),
                     flop=2 * 1024 ** 3, bytes=3 * 1024 * 1024 * 2, bound="mfma", sets=1,
-                    desc="mm 1024^3 bf16, tile 128x128 (operands cache resident)")
+                    desc="mm 1024^3 bf16, tile 64x64 (operands cache resident)")
     cases["mm"] = mm
 
     def bmm():
@@ -156,7 +156,7 @@ def make_cases(torch, lh):
         sets = [(randn(512, 16384, std=0.02), randn(16384, 512, std=0.02),
                  torch.empty(512, 512, dtype=bf, device=cuda),
                  torch.empty(16, 512, 512, dtype=torch.float32, device=cuda)) for _ in range(n)]
-        return dict(fn=lambda i: lh.split_k_matmul_gather(*sets[i % n], tile_m=64, tile_n=64,
+        return dict(fn=lambda i: lh.split_k_matmul_gather(*sets[i % n], tile_m=128, tile_n=128,
                                                           tile_k=1024),
                     flop=2 * 512 * 512 * 16384, bytes=nb, bound="hbm", sets=n,
                     desc="split-K 512x512x16384, 16 slabs, fp32 partials")

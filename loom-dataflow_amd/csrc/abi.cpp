@@ -781,11 +781,16 @@ int loom_hip_preferred_block_sizes(const char* func, const int64_t* dims, int nd
     b["tile_m"] = b["tile_n"] = gemm_tile(d[1], d[2], d[0]);
     b["tile_k"] = 64;
   } else if (f == "split_k_matmul_gather") {
-    b["tile_m"] = b["tile_n"] = 64;
-    // enough K slabs to cover the CUs, slabs a multiple of 64 deep
-    const long long tiles = ceil_div(d[0], 64) * ceil_div(d[1], 64);
-    const long long S = std::max(1LL, std::min(ceil_div(kCUs, tiles), ceil_div(d[2], 64)));
-    b["tile_k"] = std::min<long long>(d[2], ceil_div(ceil_div(d[2], S), 64) * 64);
+    // 128x128 tiles (64x64 when M or N is small), enough K slabs to cover
+    // the CUs, slabs a whole number of the pipelined kernel's rounds (256
+    // deep for 128 tiles, 512 for 64) when K allows
+    const long long t = (d[0] >= 128 && d[1] >= 128) ? 128 : 64;
+    const long long round = t == 128 ? 256 : 512;
+    b["tile_m"] = b["tile_n"] = t;
+    const long long tiles = ceil_div(d[0], t) * ceil_div(d[1], t);
+    const long long step = d[2] >= round ? round : 64;
+    const long long S = std::max(1LL, std::min(ceil_div(kCUs, tiles), ceil_div(d[2], step)));
+    b["tile_k"] = std::min<long long>(d[2], ceil_div(ceil_div(d[2], S), step) * step);
   } else if (f == "attention") {
     b["tile_b"] = 1;
     b["tile_m"] = 256;

@@ -427,16 +427,18 @@ __global__ void __launch_bounds__(256) gemm_dma_kernel(GemmParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// 256x256 tile, software-pipelined: the production path for K ranges that
-// are whole multiples of NS*BK (128).  Same LDS layout, swizzles, operand
-// roles and accumulation order as gemm_dma_kernel (bitwise identical
-// results); what changes is the schedule:
+// Square T x T tile (T = 256, 128 or 64), software-pipelined: the production path
+// for K ranges that are whole multiples of NS*BK.  Four waves, each owning a
+// (T/2) x (T/2) block of C^T tiles; A [T][32] and B [32][T] stages arrive by
+// LDS DMA, NS deep (T 256: 4 stages, 128: 8, 64: 16; 128 KB in every case).
+// The LDS layouts, swizzles and operand roles are those of gemm_dma_kernel
+// (and the accumulation order too: results are bitwise identical); what
+// differs is the schedule:
 //   - the MFMA fragments of stage it+1 are read from LDS into a second
-//     register set while the MFMAs of stage it run, one read between every
-//     two MFMAs;
+//     register set while the MFMAs of stage it run, spread between them;
 //   - this wave's DMA for stage it+NS is folded between the MFMAs too (one
-//     per group of eight), with a scalar base per stage and per-lane 32-bit
-//     offsets that stay the same for every stage;
+//     per group of T/32 MFMAs), with a scalar base per stage and per-lane
+//     32-bit offsets that stay the same for every stage;
 //   - the accumulators live in AGPRs (inline-asm MFMAs, see mfma_agpr) and
 //     the loop body has no data-dependent branch: past the last stage the
 //     DMA re-reads the last stage into a buffer that is never read again;
@@ -447,14 +449,35 @@ __global__ void __launch_bounds__(256) gemm_dma_kernel(GemmParams p) {
 // its fragment reads of stage it before it, frees stage it's buffer for the
 // DMA of stage it+NS.
 // ---------------------------------------------------------------------------
-template <bool OUT_F32, bool H>
+template <int T>
+constexpr int pipe_stages() { return T == 256 ? 4 : T == 128 ? 8 : 16; }
+
+// B swizzle of the pipelined kernels.  Rows of 256 bytes or more: b_swz.
+// T = 64 has 128-byte rows (8 chunks), so the row pair separation moves to
+// chunk bit 1: the eight rows one transposed read touches (k..k+3 and
+// k+8..k+11; even and odd rows fall in different 128-byte bank halves) then
+// occupy distinct 32-byte slots.
+template <int T>
+LOOM_DEV int b_swz_t(int k) {
+  if constexpr (T == 64)
+    return (2 * (k & 3)) ^ (2 * ((k >> 3) & 1));
+  else
+    return b_swz(k);
+}
+
+template <int T, bool OUT_F32, bool H>
 __global__ void __launch_bounds__(256) gemm_pipe_kernel(GemmParams p) {
-  constexpr int NS = 4, BK = 32, BM = 256, BN = 256;
-  constexpr int A_BYTES = BM * BK * 2, B_BYTES = BK * BN * 2;
-  constexpr int A_INSTR = A_BYTES / 1024 / 4;   // DMA instructions per wave per stage
+  constexpr int NS = pipe_stages<T>(), BK = 32;
+  constexpr int TT = T / 32;                     // 16-wide tiles per wave dimension
+  constexpr int A_BYTES = T * BK * 2, B_BYTES = BK * T * 2;
+  constexpr int B_ROW = T * 2;                   // bytes per B row in LDS
+  constexpr int A_INSTR = A_BYTES / 1024 / 4;    // DMA instructions per wave per stage
   constexpr int B_INSTR = B_BYTES / 1024 / 4;
   constexpr int LPW = A_INSTR + B_INSTR;
-  static_assert(LPW == 8, "one DMA per group of eight MFMAs");
+  constexpr int B_RPI = 1024 / B_ROW, B_CPR = B_ROW / 16;   // B rows per DMA, chunks per row
+  static_assert(T == 256 || T == 128 || T == 64, "tile");
+  static_assert(LPW == TT, "one DMA per group of TT MFMAs");
+  static_assert(NS % 2 == 0 && (NS - 1) * LPW <= 63, "stages");
   __shared__ __attribute__((aligned(1024))) char smem[NS * (A_BYTES + B_BYTES)];
   lds_char_t* const lds = (lds_char_t*)smem;
   auto stageA = [&](int s) { return lds + s * A_BYTES; };
@@ -474,8 +497,8 @@ __global__ void __launch_bounds__(256) gemm_pipe_kernel(GemmParams p) {
   const int first_m = group * GM;
   const int gsz = min(p.tiles_m - first_m, GM);
   const int tin = t - group * GM * p.tiles_n;
-  const int64_t m0 = (int64_t)(first_m + tin % gsz) * BM;
-  const int64_t n0 = (int64_t)(tin / gsz) * BN;
+  const int64_t m0 = (int64_t)(first_m + tin % gsz) * T;
+  const int64_t n0 = (int64_t)(tin / gsz) * T;
 
   const uint16_t* A = p.A;
   const uint16_t* B = p.B;
@@ -500,8 +523,8 @@ __global__ void __launch_bounds__(256) gemm_pipe_kernel(GemmParams p) {
   }
 #pragma unroll
   for (int i = 0; i < B_INSTR; ++i) {
-    const int row = (wave * B_INSTR + i) * 2 + lane / 32;
-    const int64_t gn = min<int64_t>(((lane % 32) ^ b_swz(row)) * 8, p.N - 8 - n0);
+    const int row = (wave * B_INSTR + i) * B_RPI + lane / B_CPR;
+    const int64_t gn = min<int64_t>(((lane % B_CPR) ^ b_swz_t<T>(row)) * 8, p.N - 8 - n0);
     boff[i] = (uint32_t)(row * p.ldb * 2 + gn * 2);
   }
   const uint16_t* const Abase = A + m0 * p.lda + kb;
@@ -520,52 +543,52 @@ __global__ void __launch_bounds__(256) gemm_pipe_kernel(GemmParams p) {
 
   // ---- fragment addresses.  A: one lane offset (tile tm moves by 1 KB; the
   // swizzle depends on the row's low four bits only).  B: the 16-byte chunk
-  // of tile tn is (2 tn | c4 >> 1) ^ swizzle, i.e. the lane offset XOR
-  // (tn << 5).  Stage bases are immediate offsets.
+  // of tile tn is ((T/16) wn | 2 tn | c4 >> 1) ^ swizzle, i.e. the lane
+  // offset XOR (tn << 5).  Stage bases are immediate offsets.
   const int wm = wave & 1, wn = wave >> 1;
   const int lr = lane & 15, lg = lane >> 4;
-  const uint32_t a_lane = (uint32_t)((wm * 128 + lr) * (BK * 2) + ((lg ^ a_swz<BK>(lr)) * 16));
-  uint32_t b_lane[8];
+  const uint32_t a_lane = (uint32_t)((wm * (T / 2) + lr) * (BK * 2) + ((lg ^ a_swz<BK>(lr)) * 16));
+  uint32_t b_lane[TT];
   {
     const int a = lr >> 2, c4 = lr & 3;
     const int k0r = lg * 8 + a;
-    const uint32_t base =
-        (uint32_t)(k0r * 512 + wn * 256 + (((c4 >> 1) ^ b_swz(k0r)) * 16) + (c4 & 1) * 8);
+    const uint32_t base = (uint32_t)(k0r * B_ROW + (((wn * (T / 16)) | (c4 >> 1)) ^ b_swz_t<T>(k0r)) * 16 +
+                                     (c4 & 1) * 8);
 #pragma unroll
-    for (int tn = 0; tn < 8; ++tn) b_lane[tn] = base ^ (uint32_t)(tn << 5);
+    for (int tn = 0; tn < TT; ++tn) b_lane[tn] = base ^ (uint32_t)(tn << 5);
   }
   auto read_a = [&](int s, int tm) {
     return *(const __attribute__((address_space(3))) u32x4_t*)(stageA(s) + a_lane + tm * 1024);
   };
   auto read_b = [&](int s, int tn, int half) {
-    return lds_read_tr16(stageB(s) + b_lane[tn] + half * 4 * 512);
+    return lds_read_tr16(stageB(s) + b_lane[tn] + half * 4 * B_ROW);
   };
 
-  f32x4_t acc[8][8];  // [n tile][m tile]: C^T tiles
+  f32x4_t acc[TT][TT];  // [n tile][m tile]: C^T tiles
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
+  for (int i = 0; i < TT; ++i)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < TT; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   mfma_drain();
 
   // ---- prologue: NS stages in flight, fragments of stage 0
-  u32x4_t af[2][8], bfr[2][8];
+  u32x4_t af[2][TT], bfr[2][TT];
 #pragma unroll
   for (int s = 0; s < NS; ++s) issue(s, s);
   LOOM_WAIT_VMCNT((NS - 1) * LPW);
   barrier_nofence();
 #pragma unroll
-  for (int q = 0; q < 8; ++q) {
+  for (int q = 0; q < TT; ++q) {
     af[0][q] = read_a(0, q);
     const u32x2_t lo = read_b(0, q, 0), hi = read_b(0, q, 1);
     bfr[0][q] = u32x4_t{lo[0], lo[1], hi[0], hi[1]};
   }
 
-  // ---- one stage: 64 MFMAs on the current set; per group of eight (tile
+  // ---- one stage: TT*TT MFMAs on the current set; per group of TT (tile
   // tn): the next set's B fragment tn (two transposed reads) and A fragment
   // tn, and this wave's DMA number tn for stage it+NS
-  auto step = [&](int u, int it, const u32x4_t (&fa)[8], const u32x4_t (&fb)[8], u32x4_t (&na)[8],
-                  u32x4_t (&nb)[8]) {
+  auto step = [&](int u, int it, const u32x4_t (&fa)[TT], const u32x4_t (&fb)[TT],
+                  u32x4_t (&na)[TT], u32x4_t (&nb)[TT]) {
     LOOM_WAIT_VMCNT((NS - 2) * LPW);
     LOOM_WAIT_LGKM0();
     barrier_nofence();
@@ -573,28 +596,28 @@ __global__ void __launch_bounds__(256) gemm_pipe_kernel(GemmParams p) {
     const int sd = min(it + NS, nk - 1);
     const uint16_t* ab = Abase + (int64_t)sd * BK;
     const uint16_t* bb = Bbase + (int64_t)sd * BK * p.ldb;
-    u32x2_t lo[8];
+    u32x2_t lo[TT];
 #pragma unroll
-    for (int i = 0; i < 64; ++i) {
-      const int tn = i >> 3, tm = i & 7;
-      if (tm == 4) {
+    for (int i = 0; i < TT * TT; ++i) {
+      const int tn = i / TT, tm = i % TT;
+      if (tm == TT / 2) {
         if (tn < A_INSTR)
-          mfma_agpr_dma<H>(acc[tn][tm], fb[tn], fa[tm], la0 + u * A_BYTES + (wave * A_INSTR + tn) * 1024,
-                           aoff[tn], ab);
+          mfma_agpr_dma<H>(acc[tn][tm], fb[tn], fa[tm],
+                           la0 + (u % NS) * A_BYTES + (wave * A_INSTR + tn) * 1024, aoff[tn], ab);
         else
           mfma_agpr_dma<H>(acc[tn][tm], fb[tn], fa[tm],
-                           lb0 + u * B_BYTES + (wave * B_INSTR + tn - A_INSTR) * 1024,
+                           lb0 + (u % NS) * B_BYTES + (wave * B_INSTR + tn - A_INSTR) * 1024,
                            boff[tn - A_INSTR], bb);
       } else {
         mfma_agpr<H>(acc[tn][tm], fb[tn], fa[tm]);
       }
       __builtin_amdgcn_sched_barrier(0);
       if (tm == 0) lo[tn] = read_b(sn, tn, 0);
-      if (tm == 2) {
+      if (tm == TT / 4) {
         const u32x2_t hi = read_b(sn, tn, 1);
         nb[tn] = u32x4_t{lo[tn][0], lo[tn][1], hi[0], hi[1]};
       }
-      if (tm == 6) na[tn] = read_a(sn, tn);
+      if (tm == 3 * TT / 4) na[tn] = read_a(sn, tn);
       __builtin_amdgcn_sched_barrier(0);
     }
   };
@@ -609,39 +632,39 @@ __global__ void __launch_bounds__(256) gemm_pipe_kernel(GemmParams p) {
   // ---- epilogue: acc[tn][tm][i] = C[m][n + i], m = tile row lr, n = 4 lg
   void* const cz = OUT_F32 ? (void*)(static_cast<float*>(p.C) + (int64_t)z * p.zc)
                            : (void*)(static_cast<uint16_t*>(p.C) + (int64_t)z * p.zc);
-  const int64_t r0 = m0 + wm * 128 + lr, c0 = n0 + wn * 128 + lg * 4;
-  if (m0 + BM <= p.M && n0 + BN <= p.N) {
+  const int64_t r0 = m0 + wm * (T / 2) + lr, c0 = n0 + wn * (T / 2) + lg * 4;
+  if (m0 + T <= p.M && n0 + T <= p.N) {
     if constexpr (OUT_F32) {
       float* cb = static_cast<float*>(cz) + r0 * p.ldc + c0;
 #pragma unroll
-      for (int tm = 0; tm < 8; ++tm)
+      for (int tm = 0; tm < TT; ++tm)
 #pragma unroll
-        for (int tn = 0; tn < 8; ++tn)
+        for (int tn = 0; tn < TT; ++tn)
           *reinterpret_cast<f32x4_t*>(cb + (int64_t)(tm * 16) * p.ldc + tn * 16) = acc[tn][tm];
     } else {
-      u32x2_t pk[8][8];
+      u32x2_t pk[TT][TT];
 #pragma unroll
-      for (int tn = 0; tn < 8; ++tn)
+      for (int tn = 0; tn < TT; ++tn)
 #pragma unroll
-        for (int tm = 0; tm < 8; ++tm)
+        for (int tm = 0; tm < TT; ++tm)
           pk[tn][tm] = u32x2_t{pack2<H>(acc[tn][tm][0], acc[tn][tm][1]),
                                pack2<H>(acc[tn][tm][2], acc[tn][tm][3])};
       uint16_t* cb = static_cast<uint16_t*>(cz) + r0 * p.ldc + c0;
 #pragma unroll
-      for (int tm = 0; tm < 8; ++tm)
+      for (int tm = 0; tm < TT; ++tm)
 #pragma unroll
-        for (int tn = 0; tn < 8; ++tn)
+        for (int tn = 0; tn < TT; ++tn)
           *reinterpret_cast<u32x2_t*>(cb + (int64_t)(tm * 16) * p.ldc + tn * 16) = pk[tn][tm];
     }
     return;
   }
 #pragma unroll
-  for (int tm = 0; tm < 8; ++tm) {
+  for (int tm = 0; tm < TT; ++tm) {
     __builtin_amdgcn_sched_barrier(0);
     const int64_t row = r0 + tm * 16;
     if (row >= p.M) continue;
 #pragma unroll
-    for (int tn = 0; tn < 8; ++tn) {
+    for (int tn = 0; tn < TT; ++tn) {
       const int64_t col = c0 + tn * 16;
       if (col >= p.N) continue;
       const f32x4_t v = acc[tn][tm];
@@ -652,6 +675,22 @@ __global__ void __launch_bounds__(256) gemm_pipe_kernel(GemmParams p) {
             u32x2_t{pack2<H>(v[0], v[1]), pack2<H>(v[2], v[3])};
     }
   }
+}
+
+// Launches the pipelined kernel when every K range is a whole number of its
+// NS*32-deep rounds (and the per-lane DMA offsets fit in 32 bits).
+template <int T, bool H>
+bool launch_pipe(const GemmParams& p, bool aligned, bool out_f32, hipStream_t st) {
+  constexpr int round = pipe_stages<T>() * 32;
+  const bool ok = aligned && p.k_total % round == 0 && (!p.split || p.k_slab % round == 0) &&
+                  p.lda < (1 << 22) && p.ldb < (1 << 22) && p.N >= 8;
+  if (!ok) return false;
+  const dim3 grid((unsigned)((int64_t)p.tiles_m * p.tiles_n * p.nz)), block(256);
+  if (out_f32)
+    hipLaunchKernelGGL((gemm_pipe_kernel<T, true, H>), grid, block, 0, st, p);
+  else
+    hipLaunchKernelGGL((gemm_pipe_kernel<T, false, H>), grid, block, 0, st, p);
+  return true;
 }
 
 // out[e] = bf16( sum_{s ascending} G[s][e] ) -- the split-0 reduction of
@@ -723,20 +762,16 @@ hipError_t launch_gemm(GemmParams p, int64_t tile_m, int64_t tile_n, bool aligne
                        hipStream_t st) {
   p.tiles_m = (int)cdiv64(p.M, tile_m);
   p.tiles_n = (int)cdiv64(p.N, tile_n);
-  if (tile_m == 64) return launch_tile<64, 64, 1, 2, H>(p, aligned, out_f32, st);
-  if (tile_m == 128) return launch_tile<128, 128, 2, 2, H>(p, aligned, out_f32, st);
-  // 256x256, pipelined: every K range a whole number of 128-deep rounds, and
-  // the per-lane DMA byte offsets within 32 bits
-  const dim3 grid((unsigned)((int64_t)p.tiles_m * p.tiles_n * p.nz)), block(256);
-  const bool pipe = aligned && p.k_total % 128 == 0 && (!p.split || p.k_slab % 128 == 0) &&
-                    p.lda < (1 << 22) && p.ldb < (1 << 22) && p.N >= 8;
-  if (pipe) {
-    if (out_f32)
-      hipLaunchKernelGGL((gemm_pipe_kernel<true, H>), grid, block, 0, st, p);
-    else
-      hipLaunchKernelGGL((gemm_pipe_kernel<false, H>), grid, block, 0, st, p);
-    return hipGetLastError();
+  if (tile_m == 64) {
+    if (launch_pipe<64, H>(p, aligned, out_f32, st)) return hipGetLastError();
+    return launch_tile<64, 64, 1, 2, H>(p, aligned, out_f32, st);
   }
+  if (tile_m == 128) {
+    if (launch_pipe<128, H>(p, aligned, out_f32, st)) return hipGetLastError();
+    return launch_tile<128, 128, 2, 2, H>(p, aligned, out_f32, st);
+  }
+  if (launch_pipe<256, H>(p, aligned, out_f32, st)) return hipGetLastError();
+  const dim3 grid((unsigned)((int64_t)p.tiles_m * p.tiles_n * p.nz)), block(256);
   // otherwise the LDS-DMA kernel needs whole BK steps in every K range
   constexpr int BK = LOOM_GEMM_DMA_BK, NS = LOOM_GEMM_DMA_NS;
   const bool dma = aligned && p.k_total % BK == 0 && (!p.split || p.k_slab % BK == 0);

@@ -116,8 +116,9 @@ def test_preferred_bindings_at_baseline_shapes():
     assert loom_hip.preferred_block_sizes("attention", (128, 4096, 4096, 128))["tile_m"] == 256
     assert loom_hip.preferred_block_sizes("flash_decode", (32, 32, 128, 8192))["tile_s"] == 1024
     # split-K: enough K slabs for a workgroup per CU (BASELINE itself fixes 16 slabs)
-    tk = loom_hip.preferred_block_sizes("split_k_matmul_gather", (512, 512, 16384))["tile_k"]
-    assert 16384 // tk * (512 // 64) ** 2 >= 256
+    sk = loom_hip.preferred_block_sizes("split_k_matmul_gather", (512, 512, 16384))
+    assert (sk["tile_m"], sk["tile_n"], sk["tile_k"]) == (128, 128, 1024)
+    assert loom_hip.preferred_block_sizes("matmul", (1024, 1024, 1024))["tile_m"] == 64
     m = loom_hip.preferred_block_sizes("helion_mamba2_chunk_scan_kernel", (4, 16, 32, 1, 256, 64, 128))
     assert (m["tile_m"], m["tile_n"]) == (256, 64)
 

@@ -73,6 +73,19 @@ def test_matmul_integer_bit_exact(lh):
         assert np.array_equal(host(lh.matmul(dev(x), dev(y), tile_m=t[0], tile_n=t[1])), ref), t
 
 
+def test_matmul_pipelined_edge_tiles_bit_exact(lh):
+    """K a multiple of the pipelined kernels' rounds (128 / 256 / 512), M and N not a
+    multiple of the tile: clamped DMA rows/columns and the guarded epilogue."""
+    rng = np.random.default_rng(12)
+    for (M, N, K) in [(300, 264, 512), (520, 136, 768), (257, 520, 1024)]:
+        x = to_bf16(rng.integers(-8, 9, (M, K)).astype(np.float32))
+        y = to_bf16(rng.integers(-8, 9, (K, N)).astype(np.float32))
+        ref = oracle.matmul(x, y)
+        for t in [(64, 64), (128, 128), (256, 256)]:
+            got = host(lh.matmul(dev(x), dev(y), tile_m=t[0], tile_n=t[1]))
+            assert np.array_equal(got, ref), (M, N, K, t)
+
+
 def test_matmul_baseline_1024(lh):
     rng = np.random.default_rng(1)
     x = rng_bf16(rng, (1024, 1024), "uniform")
@@ -148,6 +161,21 @@ def test_split_k_baseline_integer_bit_exact(lh):
     exp = np.stack([ai[:, s * 1024:(s + 1) * 1024] @ bi[s * 1024:(s + 1) * 1024] for s in range(16)])
     assert np.array_equal(parts.astype(np.float64), exp)
     assert np.array_equal(host(out), to_bf16(exp.sum(0).astype(np.float32)))
+
+
+def test_split_k_pipelined_integer_bit_exact(lh):
+    """Slabs that are whole rounds of the pipelined 128 and 256 tiles, with an
+    edge tile in M: every fp32 partial and the output bit-exact."""
+    rng = np.random.default_rng(9)
+    ai = rng.integers(-4, 5, (384, 4096)).astype(np.float64)
+    bi = rng.integers(-4, 5, (4096, 256)).astype(np.float64)
+    exp = np.stack([ai[:, s * 1024:(s + 1) * 1024] @ bi[s * 1024:(s + 1) * 1024] for s in range(4)])
+    for t in [(64, 64), (128, 128), (256, 256)]:
+        out, parts = lh.split_k_matmul_gather(dev(to_bf16(ai.astype(np.float32))),
+                                              dev(to_bf16(bi.astype(np.float32))),
+                                              tile_m=t[0], tile_n=t[1], tile_k=1024)
+        assert np.array_equal(parts.cpu().numpy().astype(np.float64), exp), t
+        assert np.array_equal(host(out), to_bf16(exp.sum(0).astype(np.float32))), t
 
 
 def test_split_k_baseline_float(lh):
