@@ -186,16 +186,21 @@ __global__ void __launch_bounds__(64 * kWaves) mamba_chunk_scan_kernel(MambaPara
     u32x4_t c[NSN];
     u32x4_t cb[NKS];
   };
+  // Every load is issued, unneeded ones with an offset past the
+  // descriptor's range (zeros, no memory access): the compiler can then
+  // count the loads younger than the ones it waits for, where a
+  // conditional load makes it wait for all of them, prefetch included.
+  constexpr uint32_t kNone = 0x7ffffff0u;
   auto fetch = [&](int ti, Rows& rw) {
     const int mrow0 = m0 + 16 * tile_of(ti);
     const int am = mrow0 + rr;
     const int kend = min(mrow0 + 16, Q);
 #pragma unroll
     for (int ns = 0; ns < NSN; ++ns)
-      if (ns * 32 < N) rw.c[ns] = buf_load16(rC, (uint32_t)(am * N + ns * 32 + g4 * 8) * 2);
+      rw.c[ns] = buf_load16(rC, ns * 32 < N ? (uint32_t)(am * N + ns * 32 + g4 * 8) * 2 : kNone);
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks)
-      if (ks * 32 < kend) rw.cb[ks] = buf_load16(rCB, (uint32_t)(am * Q + ks * 32 + g4 * 8) * 2);
+      rw.cb[ks] = buf_load16(rCB, ks * 32 < kend ? (uint32_t)(am * Q + ks * 32 + g4 * 8) * 2 : kNone);
   };
 
   // The MFMAs compute out^T tiles (x^T / prevT^T as the row operand, W / C
@@ -203,11 +208,11 @@ __global__ void __launch_bounds__(64 * kWaves) mamba_chunk_scan_kernel(MambaPara
   // out[m = mrow0 + rr][p = 16 pt + 4 g4 + i], four consecutive columns.
   uint16_t* og = p.out + ((int64_t)(b * H + h) * L + (int64_t)c * Q) * P;
   Rows rowbuf[2];
-  if (tile_of(0) < nmt16) fetch(0, rowbuf[0]);
+  fetch(0, rowbuf[0]);
 #pragma unroll
   for (int ti = 0; ti < MAXT; ++ti) {
     if (tile_of(ti) >= nmt16) continue;
-    if (ti + 1 < MAXT && tile_of(ti + 1) < nmt16) fetch(ti + 1, rowbuf[(ti + 1) & 1]);
+    if (ti + 1 < MAXT) fetch(ti + 1, rowbuf[(ti + 1) & 1]);
     const Rows& rw = rowbuf[ti & 1];
     const int mrow0 = m0 + 16 * tile_of(ti);
     const int am = mrow0 + rr;  // this lane's output row
