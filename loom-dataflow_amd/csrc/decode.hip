@@ -110,7 +110,11 @@ __global__ void __launch_bounds__(64 * kWaves) decode_split_kernel(DecodeParams 
   constexpr int VEC = D / 16;     // d values per lane per V row, also # of d tiles
   constexpr int DSTEPS = D / 32;  // 32-deep MFMA steps over d
   constexpr int NSTEPS = DSTEPS + 2;
-  constexpr int R = 2;            // ring slots
+#ifndef LOOM_DECODE_RING
+#define LOOM_DECODE_RING 3
+#endif
+  // ring slots (a divisor of the step count)
+  constexpr int R = NSTEPS % LOOM_DECODE_RING == 0 ? LOOM_DECODE_RING : 2;
   static_assert(NSTEPS % R == 0, "ring must divide the step count");
   constexpr int HP = HT * 16;     // padded head count
   constexpr int ACC_STRIDE = D + 1;
@@ -142,14 +146,19 @@ __global__ void __launch_bounds__(64 * kWaves) decode_split_kernel(DecodeParams 
   }
   __syncthreads();
 
-  // ---- loads of step `st` of the block starting at key `base`
-  auto issue = [&](int base, int st, u32x4_t (&buf)[8]) {
+  // ---- loads of step `st` of the block starting at key `base`.  A block
+  // this wave does not have (valid false) is still issued, at an offset
+  // past the descriptor's range (zeros, no memory access): with every load
+  // unconditional the compiler waits only for the loads it needs, not for
+  // the ones in flight ahead of them.
+  constexpr uint32_t kNone = 0x7ffffff0u;
+  auto issue = [&](int base, int st, u32x4_t (&buf)[8], bool valid) {
     if (st < DSTEPS) {
       // K rows d = 32 st + 8 g + e, keys base + 4 r .. +3
       const uint32_t off = ((uint32_t)(st * 32 + g * 8) * S + base + r * 4) * 2;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const uint32_t o = off + (uint32_t)(e * S) * 2;
+        const uint32_t o = valid ? off + (uint32_t)(e * S) * 2 : kNone;
         if constexpr (ALIGNED) {
           const u32x2_t w = buf_load8(krs, o);
           buf[e] = u32x4_t{w[0], w[1], 0u, 0u};
@@ -166,7 +175,7 @@ __global__ void __launch_bounds__(64 * kWaves) decode_split_kernel(DecodeParams 
 #pragma unroll
       for (int t = 0; t < 8; ++t) {
         const int key = base + 16 * g + 4 * (t & 3) + 2 * c + (t >> 2);
-        const uint32_t o = ((uint32_t)key * D + r * VEC) * 2;
+        const uint32_t o = valid ? ((uint32_t)key * D + r * VEC) * 2 : kNone;
         if constexpr (VEC == 8) {
           buf[t] = buf_load16(vrs, o);
         } else {
@@ -187,8 +196,11 @@ __global__ void __launch_bounds__(64 * kWaves) decode_split_kernel(DecodeParams 
     for (int u = 0; u < VEC; ++u) ot[u][ht] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   }
 
+  // loads run R-1 steps ahead of the math (into the wave's next block at the
+  // end of one)
   u32x4_t ring[R][8];
-  if (wave < nblk) issue(s0 + wave * kBlockKeys, 0, ring[0]);
+#pragma unroll
+  for (int a = 0; a < R - 1; ++a) issue(s0 + wave * kBlockKeys, a, ring[a], wave < nblk);
 
   for (int bi = wave; bi < nblk; bi += kWaves) {
     const int base = s0 + bi * kBlockKeys;
@@ -202,11 +214,11 @@ __global__ void __launch_bounds__(64 * kWaves) decode_split_kernel(DecodeParams 
 
 #pragma unroll
     for (int st = 0; st < NSTEPS; ++st) {
-      // prefetch the next step (the next block's first step at the end)
-      if (st + 1 < NSTEPS)
-        issue(base, st + 1, ring[(st + 1) % R]);
-      else if (has_next)
-        issue(next_base, 0, ring[(st + 1) % R]);
+      // prefetch R-1 steps ahead (into the next block near the end)
+      if (st + R - 1 < NSTEPS)
+        issue(base, st + R - 1, ring[(st + R - 1) % R], true);
+      else
+        issue(next_base, st + R - 1 - NSTEPS, ring[(st + R - 1) % R], has_next);
 
       u32x4_t (&cur)[8] = ring[st % R];
       if (st < DSTEPS) {
