@@ -44,8 +44,18 @@ struct AttnParams {
 // raises it by more than 8 in the log2 domain, which keeps P <= 2^8 and the
 // result exact (numerator and denominator share the stale base).
 // Ks rows (128 B) and Vs rows (2 D bytes) XOR their 16-byte chunk index with
-// 2 (row & 3), so a transposed read's four rows hit distinct banks.
+// k_swz / v_swz so that each 32-lane pass of a transposed read touches 32
+// distinct 16-byte slots of the LDS's 512-byte bank window.
 // ---------------------------------------------------------------------------
+// One pass of a K^T read covers Ks rows d..d+3 and d+8..d+11 (128 B apart:
+// rows d and d+8 share a window position), 32 bytes each: bit 3 of the row
+// flips the chunk pair.
+LOOM_DEV int k_swz(int d) { return 2 * ((d >> 3) & 1); }
+// One pass of a V^T read covers 8 consecutive Vs rows, 32 bytes each; rows r,
+// r^2, r^4, r^6 (D 128: 256-byte rows) or r, r^4 (D 64: 128-byte rows) share
+// a window position: row bits 1-2 pick the chunk pair.
+LOOM_DEV int v_swz(int k) { return 2 * ((k >> 1) & 3); }
+
 template <int D, int QT, int W, bool H>
 __global__ void __launch_bounds__(64 * W) attention_dma_kernel(AttnParams p) {
   constexpr int KB = 64;                        // keys per stage
@@ -100,7 +110,7 @@ __global__ void __launch_bounds__(64 * W) attention_dma_kernel(AttnParams p) {
     for (int i = 0; i < K_INSTR; ++i) {
       const int j = wave * K_INSTR + i;
       const int d = j * 8 + lane / 8;                     // Ks row
-      const int c = (lane % 8) ^ (2 * (d & 3));
+      const int c = (lane % 8) ^ k_swz(d);
       const int key = min(kv0 + c * 8, Skv - 8);
       dma_load16(kg + (int64_t)d * Skv + key, lk + j * 1024);
     }
@@ -108,7 +118,7 @@ __global__ void __launch_bounds__(64 * W) attention_dma_kernel(AttnParams p) {
     for (int i = 0; i < V_INSTR; ++i) {
       const int j = wave * V_INSTR + i;
       const int kr = j * V_ROWS_PER_I + lane / (D / 8);   // Vs row (key)
-      const int c = (lane % (D / 8)) ^ (2 * (kr & 3));
+      const int c = (lane % (D / 8)) ^ v_swz(kr);
       const int key = min(kv0 + kr, Skv - 1);
       dma_load16(vg + (int64_t)key * D + c * 8, lv + j * 1024);
     }
@@ -170,7 +180,7 @@ __global__ void __launch_bounds__(64 * W) attention_dma_kernel(AttnParams p) {
         for (int j = 0; j < 2; ++j) {
           const int jt = 2 * h + j;
           const int d = ds * 32 + g * 8 + a4;               // & 3 == a4
-          const int ch = (2 * jt + (c4 >> 1)) ^ (2 * a4);
+          const int ch = (2 * jt + (c4 >> 1)) ^ k_swz(d);
           const lds_char_t* q = ks + d * (KB * 2) + ch * 16 + (c4 & 1) * 8;
           const u32x2_t lo = lds_read_tr16(q);
           const u32x2_t hi = lds_read_tr16(q + 4 * (KB * 2));
@@ -245,8 +255,8 @@ __global__ void __launch_bounds__(64 * W) attention_dma_kernel(AttnParams p) {
       }
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
-        const int ch = (2 * dt + (c4 >> 1)) ^ (2 * a4);
-        const int k0r = 32 * h + 4 * g + a4;                // & 3 == a4
+        const int k0r = 32 * h + 4 * g + a4;
+        const int ch = (2 * dt + (c4 >> 1)) ^ v_swz(k0r);
         const lds_char_t* q = vs + k0r * VROW + ch * 16 + (c4 & 1) * 8;
         const u32x2_t lo = lds_read_tr16(q);                // keys 32h + 4g + 0..3
         const u32x2_t hi = lds_read_tr16(q + 16 * VROW);    // keys 32h + 16 + 4g + 0..3
