@@ -294,6 +294,35 @@ LOOM_DEV void mfma_agpr_dma(f32x4_t& acc, const u32x4_t& a, const u32x4_t& b, ui
         : "v"(a), "v"(b), "s"(lds), "v"(voff), "s"(sbase)
         : "memory", "m0");
 }
+// The two MFMA forms above starting a fresh accumulator (srcC = 0): the previous
+// contents of acc are neither read nor needed.
+template <bool H>
+LOOM_DEV void mfma_agpr_z(f32x4_t& acc, const u32x4_t& a, const u32x4_t& b) {
+  if constexpr (H)
+    asm volatile("v_mfma_f32_16x16x32_f16 %0, %1, %2, 0" : "=a"(acc) : "v"(a), "v"(b));
+  else
+    asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, 0" : "=a"(acc) : "v"(a), "v"(b));
+}
+template <bool H>
+LOOM_DEV void mfma_agpr_dma_z(f32x4_t& acc, const u32x4_t& a, const u32x4_t& b, uint32_t lds,
+                              uint32_t voff, const void* sbase) {
+  if constexpr (H)
+    asm volatile(
+        "s_mov_b32 m0, %3\n\t"
+        "v_mfma_f32_16x16x32_f16 %0, %1, %2, 0\n\t"
+        "global_load_lds_dwordx4 %4, %5"
+        : "=a"(acc)
+        : "v"(a), "v"(b), "s"(lds), "v"(voff), "s"(sbase)
+        : "memory", "m0");
+  else
+    asm volatile(
+        "s_mov_b32 m0, %3\n\t"
+        "v_mfma_f32_16x16x32_bf16 %0, %1, %2, 0\n\t"
+        "global_load_lds_dwordx4 %4, %5"
+        : "=a"(acc)
+        : "v"(a), "v"(b), "s"(lds), "v"(voff), "s"(sbase)
+        : "memory", "m0");
+}
 // LDS-DMA load with a scalar base and a per-lane 32-bit byte offset
 LOOM_DEV void dma_load16_s(uint32_t voff, const void* sbase, uint32_t lds) {
   asm volatile(

@@ -22,6 +22,12 @@
 // accumulators fed by v_mfma_f32_16x16x32_bf16.
 #include "common.h"
 
+#include <type_traits>
+
+#ifndef LOOM_GEMM_PERSIST
+#define LOOM_GEMM_PERSIST 1
+#endif
+
 namespace {
 
 constexpr int kBK = 64;  // K depth of one LDS stage (8 chunks of 8 bf16)
@@ -452,6 +458,17 @@ __global__ void __launch_bounds__(256) gemm_dma_kernel(GemmParams p) {
 // its fragment reads of stage it before it, frees stage it's buffer for the
 // DMA of stage it+NS.
 // ---------------------------------------------------------------------------
+// Orders every later read of the accumulators after the preceding
+// mfma_drain(): the MFMAs are inline assembly, so nothing else tells the
+// compiler that the drain must come first.
+template <int TT>
+LOOM_DEV void acc_fence(f32x4_t (&acc)[TT][TT]) {
+#pragma unroll
+  for (int i = 0; i < TT; ++i)
+#pragma unroll
+    for (int j = 0; j < TT; ++j) asm volatile("" : "+a"(acc[i][j]));
+}
+
 template <int T>
 constexpr int pipe_stages() { return T == 256 ? 4 : T == 128 ? 8 : 16; }
 
@@ -630,6 +647,7 @@ __global__ void __launch_bounds__(256) gemm_pipe_kernel(GemmParams p) {
   }
   LOOM_WAIT_VMCNT(0);   // the trailing re-reads land before the workgroup ends
   mfma_drain();
+  acc_fence(acc);
 
   // ---- epilogue: acc[tn][tm][i] = C[m][n + i], m = tile row lr, n = 4 lg
   void* const cz = OUT_F32 ? (void*)(static_cast<float*>(p.C) + (int64_t)z * p.zc)
@@ -692,6 +710,259 @@ bool launch_pipe(const GemmParams& p, bool aligned, bool out_f32, hipStream_t st
     hipLaunchKernelGGL((gemm_pipe_kernel<T, true, H>), grid, block, 0, st, p);
   else
     hipLaunchKernelGGL((gemm_pipe_kernel<T, false, H>), grid, block, 0, st, p);
+  return true;
+}
+
+// ---------------------------------------------------------------------------
+// Persistent 256x256 GEMM (bf16 output, whole tiles): one workgroup per CU
+// walks nr tiles with one continuous LDS-DMA stream, so the first stages of
+// tile r+1 load while tile r finishes, and no workgroup launch, set-up or
+// cold pipeline separates the tiles.  Workgroup g (on XCD g % 8) runs the
+// tiles that the one-tile-per-workgroup launch would run on that XCD, in the
+// same rounds: logical tile (g % 8) ntiles/8 + r G/8 + g / 8.
+//
+// Stage slots hold A and B of one 32-deep K step (slot = global step % 4),
+// and a fifth 32 KB region stages C: each tile's epilogue converts the
+// accumulators to bf16 a quarter (two 16-row groups per wave) at a time,
+// writes them row-major into that region (16-byte chunks XOR row & 15) and
+// stores whole 512-byte rows, 16 bytes per lane.  Before the first store
+// every LDS-DMA load issued so far has landed (vmcnt 0), so the stores only
+// add to the count the main loop's vmcnt waits see: those waits stay exact.
+// The first K step of every tile starts its accumulators with srcC = 0.
+// ---------------------------------------------------------------------------
+template <bool H>
+__global__ void __launch_bounds__(256) gemm_persist_kernel(GemmParams p, int nr) {
+  constexpr int T = 256, NS = 4, BK = 32, TT = 8;
+  constexpr int A_BYTES = T * BK * 2, B_BYTES = BK * T * 2, SLOT = A_BYTES + B_BYTES;
+  constexpr int B_ROW = T * 2;
+  constexpr int A_INSTR = A_BYTES / 1024 / 4, B_INSTR = B_BYTES / 1024 / 4;
+  constexpr int LPW = A_INSTR + B_INSTR;
+  constexpr int B_RPI = 1024 / B_ROW, B_CPR = B_ROW / 16;
+  constexpr int E_ROWS = 64;                          // C staging rows of 512 bytes
+  static_assert(LPW == TT && NS == 4, "one DMA per group of TT MFMAs");
+  __shared__ __attribute__((aligned(1024))) char smem[NS * SLOT + E_ROWS * 512];
+  lds_char_t* const lds = (lds_char_t*)smem;
+  lds_char_t* const cst = lds + NS * SLOT;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int G = (int)gridDim.x;
+  const int per_x = p.tiles_m * p.tiles_n * p.nz / 8;
+  const int gx = (int)blockIdx.x % 8, gj = (int)blockIdx.x / 8;
+  const int nk = (int)(p.k_total / BK);   // host: nk % NS == 0, nk >= NS
+  const int total = nr * nk;              // K steps over all of this workgroup's tiles
+
+  auto tile_of = [&](int r, int& z, int64_t& m0, int64_t& n0) {
+    const int l = gx * per_x + r * (G / 8) + gj;
+    const int per_z = p.tiles_m * p.tiles_n;
+    z = l / per_z;
+    const int t = l - z * per_z;
+    constexpr int GM = 8;
+    const int group = t / (GM * p.tiles_n);
+    const int first_m = group * GM;
+    const int gsz = min(p.tiles_m - first_m, GM);
+    const int tin = t - group * GM * p.tiles_n;
+    m0 = (int64_t)(first_m + tin % gsz) * T;
+    n0 = (int64_t)(tin / gsz) * T;
+  };
+  // A / B addresses of global K step q (clamped to the last one: the stream's
+  // trailing loads re-read it into slots nothing reads again)
+  auto step_bases = [&](int q, const uint16_t*& ab, const uint16_t*& bb) {
+    q = min(q, total - 1);
+    const int r = q / nk, s = q - r * nk;
+    int z;
+    int64_t m0, n0;
+    tile_of(r, z, m0, n0);
+    ab = p.A + (int64_t)z * p.za + m0 * p.lda + (int64_t)s * BK;
+    bb = p.B + (int64_t)z * p.zb + n0 + (int64_t)s * BK * p.ldb;
+  };
+
+  uint32_t aoff[A_INSTR], boff[B_INSTR];
+#pragma unroll
+  for (int i = 0; i < A_INSTR; ++i) {
+    const int row = (wave * A_INSTR + i) * 16 + lane / 4;
+    aoff[i] = (uint32_t)(row * p.lda * 2 + ((lane % 4) ^ a_swz<BK>(row)) * 16);
+  }
+#pragma unroll
+  for (int i = 0; i < B_INSTR; ++i) {
+    const int row = (wave * B_INSTR + i) * B_RPI + lane / B_CPR;
+    boff[i] = (uint32_t)(row * p.ldb * 2 + ((lane % B_CPR) ^ b_swz(row)) * 16);
+  }
+  const uint32_t l0 = lds_addr(lds);
+  auto issue = [&](int slot, const uint16_t* ab, const uint16_t* bb) {
+#pragma unroll
+    for (int i = 0; i < A_INSTR; ++i)
+      dma_load16_s(aoff[i], ab, l0 + slot * SLOT + (wave * A_INSTR + i) * 1024);
+#pragma unroll
+    for (int i = 0; i < B_INSTR; ++i)
+      dma_load16_s(boff[i], bb, l0 + slot * SLOT + A_BYTES + (wave * B_INSTR + i) * 1024);
+  };
+
+  const int wm = wave & 1, wn = wave >> 1;
+  const int lr = lane & 15, lg = lane >> 4;
+  const uint32_t a_lane = (uint32_t)((wm * (T / 2) + lr) * (BK * 2) + ((lg ^ a_swz<BK>(lr)) * 16));
+  uint32_t b_lane[TT];
+  {
+    const int a = lr >> 2, c4 = lr & 3;
+    const int k0r = lg * 8 + a;
+    const uint32_t base =
+        (uint32_t)(k0r * B_ROW + (((wn * (T / 16)) | (c4 >> 1)) ^ b_swz(k0r)) * 16 + (c4 & 1) * 8);
+#pragma unroll
+    for (int tn = 0; tn < TT; ++tn) b_lane[tn] = base ^ (uint32_t)(tn << 5);
+  }
+  auto read_a = [&](int s, int tm) {
+    return *(const __attribute__((address_space(3))) u32x4_t*)(lds + s * SLOT + a_lane + tm * 1024);
+  };
+  auto read_b = [&](int s, int tn, int half) {
+    return lds_read_tr16(lds + s * SLOT + A_BYTES + b_lane[tn] + half * 4 * B_ROW);
+  };
+
+  // per-lane byte offset of the epilogue's 16-byte stores within a tile
+  const uint32_t st_lane =
+      (uint32_t)((((wave >> 1) * 128 + (wave & 1) * 16 + (lane >> 5)) * p.ldc + (lane & 31) * 8) * 2);
+
+  f32x4_t acc[TT][TT];  // [n tile][m tile]: C^T tiles; every tile's first step sets them
+  u32x4_t af[2][TT], bfr[2][TT];
+
+  // ---- prologue: global steps 0..NS-1, fragments of step 0
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    const uint16_t *ab, *bb;
+    step_bases(s, ab, bb);
+    issue(s, ab, bb);
+  }
+  LOOM_WAIT_VMCNT((NS - 1) * LPW);
+  barrier_nofence();
+#pragma unroll
+  for (int q = 0; q < TT; ++q) {
+    af[0][q] = read_a(0, q);
+    const u32x2_t lo = read_b(0, q, 0), hi = read_b(0, q, 1);
+    bfr[0][q] = u32x4_t{lo[0], lo[1], hi[0], hi[1]};
+  }
+
+  // ---- one K step (slot u): TT*TT MFMAs on the current fragments; per group
+  // of TT (tile tn) the next step's fragments and this wave's DMA number tn of
+  // global step +NS into slot u
+  auto step = [&](auto firstc, int u, const uint16_t* ab, const uint16_t* bb,
+                  const u32x4_t (&fa)[TT], const u32x4_t (&fb)[TT], u32x4_t (&na)[TT],
+                  u32x4_t (&nb)[TT]) {
+    constexpr bool FIRST = decltype(firstc)::value;
+    LOOM_WAIT_VMCNT((NS - 2) * LPW);
+    LOOM_WAIT_LGKM0();
+    barrier_nofence();
+    const int sn = (u + 1) % NS;
+    u32x2_t lo[TT];
+#pragma unroll
+    for (int i = 0; i < TT * TT; ++i) {
+      const int tn = i / TT, tm = i % TT;
+      if (tm == TT / 2) {
+        const uint32_t dst = tn < A_INSTR ? l0 + u * SLOT + (wave * A_INSTR + tn) * 1024
+                                          : l0 + u * SLOT + A_BYTES + (wave * B_INSTR + tn - A_INSTR) * 1024;
+        const uint32_t voff = tn < A_INSTR ? aoff[tn] : boff[tn - A_INSTR];
+        const uint16_t* sb = tn < A_INSTR ? ab : bb;
+        if constexpr (FIRST)
+          mfma_agpr_dma_z<H>(acc[tn][tm], fb[tn], fa[tm], dst, voff, sb);
+        else
+          mfma_agpr_dma<H>(acc[tn][tm], fb[tn], fa[tm], dst, voff, sb);
+      } else {
+        if constexpr (FIRST)
+          mfma_agpr_z<H>(acc[tn][tm], fb[tn], fa[tm]);
+        else
+          mfma_agpr<H>(acc[tn][tm], fb[tn], fa[tm]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      if (tm == 0) lo[tn] = read_b(sn, tn, 0);
+      if (tm == TT / 4) {
+        const u32x2_t hi = read_b(sn, tn, 1);
+        nb[tn] = u32x4_t{lo[tn][0], lo[tn][1], hi[0], hi[1]};
+      }
+      if (tm == 3 * TT / 4) na[tn] = read_a(sn, tn);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  // NS steps starting at global step q0 (a multiple of NS: the DMA targets,
+  // steps q0+NS .. q0+2NS-1, lie in one tile)
+  auto group = [&](auto firstc, int q0) {
+    const uint16_t *ab, *bb;
+    step_bases(q0 + NS, ab, bb);
+    const bool clamped = q0 + NS >= total;
+#pragma unroll
+    for (int u = 0; u < NS; ++u) {
+      const uint16_t* abu = clamped ? ab : ab + u * BK;
+      const uint16_t* bbu = clamped ? bb : bb + (int64_t)u * BK * p.ldb;
+      if (u == 0)
+        step(firstc, u, abu, bbu, af[0], bfr[0], af[1], bfr[1]);
+      else
+        step(std::false_type{}, u, abu, bbu, af[u & 1], bfr[u & 1], af[(u & 1) ^ 1],
+             bfr[(u & 1) ^ 1]);
+    }
+  };
+
+  for (int r = 0; r < nr; ++r) {
+    group(std::true_type{}, r * nk);
+    for (int q0 = r * nk + NS; q0 < (r + 1) * nk; q0 += NS) group(std::false_type{}, q0);
+
+    // ---- epilogue of tile r
+    LOOM_WAIT_VMCNT(0);
+    mfma_drain();
+    acc_fence(acc);
+    int z;
+    int64_t m0, n0;
+    tile_of(r, z, m0, n0);
+    char* const cb = reinterpret_cast<char*>(static_cast<uint16_t*>(p.C) + (int64_t)z * p.zc + m0 * p.ldc + n0);
+    // staging addresses: accumulator tile (tn, tm = 2 qt + h) of this lane
+    // goes to row 32 wm + 16 h + lr, chunk (16 wn + 2 tn + lg / 2) ^ lr, i.e.
+    // e_lane ^ (tn << 5) + 8 KB h; store row rho = 16 wave + 2 i + lane / 32
+    // (tile row 128 (wave / 2) + 32 qt + 16 (wave & 1) + 2 i + lane / 32) is
+    // read at r_lane ^ (i << 5) + 1 KB i
+    uint32_t e_lane = (uint32_t)((wm * 32 + lr) * 512 + (((wn * 16 + (lg >> 1)) ^ lr) * 16) + (lg & 1) * 8);
+    uint32_t r_lane = (uint32_t)((wave * 16 + (lane >> 5)) * 512 + (((lane & 31) ^ (lane >> 5)) * 16));
+    asm volatile("" : "+v"(e_lane), "+v"(r_lane));   // computed here, not hoisted and kept live
+#pragma unroll
+    for (int qt = 0; qt < TT / 2; ++qt) {
+#pragma unroll
+      for (int tn = 0; tn < TT; ++tn)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int tm = 2 * qt + h;
+          *(__attribute__((address_space(3))) u32x2_t*)(cst + ((e_lane ^ (uint32_t)(tn << 5)) + h * 8192)) =
+              u32x2_t{pack2<H>(acc[tn][tm][0], acc[tn][tm][1]), pack2<H>(acc[tn][tm][2], acc[tn][tm][3])};
+        }
+      LOOM_WAIT_LGKM0();
+      barrier_nofence();
+#pragma unroll
+      for (int i = 0; i < E_ROWS / 8; ++i) {
+        const u32x4_t v =
+            *(const __attribute__((address_space(3))) u32x4_t*)(cst + ((r_lane ^ (uint32_t)(i << 5)) + i * 1024));
+        char* const sb = cb + (int64_t)(qt * 32 + i * 2) * p.ldc * 2;
+        *reinterpret_cast<u32x4_t*>(sb + st_lane) = v;
+      }
+      LOOM_WAIT_LGKM0();
+      barrier_nofence();
+    }
+  }
+}
+
+// Launches the persistent kernel when every tile is whole, the tiles divide
+// evenly over one workgroup per CU (at least two each) and the pipelined
+// kernel's conditions hold; the caller falls back otherwise.
+template <bool H>
+bool launch_persist(const GemmParams& p, bool aligned, bool out_f32, hipStream_t st) {
+  static int cus = -1;
+  if (cus < 0) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+      n = 0;
+    cus = n;
+  }
+  const int64_t ntiles = (int64_t)p.tiles_m * p.tiles_n * p.nz;
+  const bool ok = LOOM_GEMM_PERSIST && aligned && !out_f32 && !p.split && cus >= 8 && cus % 8 == 0 &&
+                  p.M % 256 == 0 && p.N % 256 == 0 && p.k_total % 128 == 0 && ntiles % cus == 0 &&
+                  ntiles / cus >= 2 && p.lda < (1 << 22) && p.ldb < (1 << 22) && p.ldc < (1 << 22);
+  if (!ok) return false;
+  hipLaunchKernelGGL((gemm_persist_kernel<H>), dim3((unsigned)cus), dim3(256), 0, st, p,
+                     (int)(ntiles / cus));
   return true;
 }
 
@@ -772,6 +1043,7 @@ hipError_t launch_gemm(GemmParams p, int64_t tile_m, int64_t tile_n, bool aligne
     if (launch_pipe<128, H>(p, aligned, out_f32, st)) return hipGetLastError();
     return launch_tile<128, 128, 2, 2, H>(p, aligned, out_f32, st);
   }
+  if (launch_persist<H>(p, aligned, out_f32, st)) return hipGetLastError();
   if (launch_pipe<256, H>(p, aligned, out_f32, st)) return hipGetLastError();
   const dim3 grid((unsigned)((int64_t)p.tiles_m * p.tiles_n * p.nz)), block(256);
   // otherwise the LDS-DMA kernel needs whole BK steps in every K range

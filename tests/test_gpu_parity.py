@@ -119,6 +119,30 @@ def test_batch_matmul_baseline(lh):
         assert_close(from_bf16(out[b][rows]), from_bf16(ref), **GEMM_TOL, what=f"bmm batch {b}")
 
 
+def test_batch_matmul_persistent_bit_exact(lh):
+    """Shapes whose 256x256 tiles divide evenly over the CUs, two or more per CU (the
+    persistent kernel on a 256-CU part): integer-valued inputs, every output element
+    exact.  K 128 gives one DMA round per tile (the next tile's loads start in the
+    tile's first round); K 512 four."""
+    rng = np.random.default_rng(21)
+    for (B, M, N, K) in [(16, 2048, 2048, 128), (8, 2048, 2048, 512), (4, 4096, 2048, 256)]:
+        a0 = to_bf16(rng.integers(-4, 5, (B, M, K)).astype(np.float32))
+        a1 = to_bf16(rng.integers(-4, 5, (B, K, N)).astype(np.float32))
+        out = host(lh.batch_matmul(dev(a0), dev(a1), tile_m=256, tile_n=256))
+        for b in range(B):
+            assert np.array_equal(out[b], oracle.matmul(a0[b], a1[b])), (B, M, N, K, b)
+
+
+def test_matmul_persistent_bit_exact(lh):
+    """matmul 8192 x 4096 x 256 (512 tiles of 256x256): sampled rows exact."""
+    rng = np.random.default_rng(22)
+    x = to_bf16(rng.integers(-4, 5, (8192, 256)).astype(np.float32))
+    y = to_bf16(rng.integers(-4, 5, (256, 4096)).astype(np.float32))
+    out = host(lh.matmul(dev(x), dev(y), tile_m=256, tile_n=256))
+    rows = np.sort(np.random.default_rng(6).choice(8192, 512, replace=False))
+    assert np.array_equal(out[rows], oracle.matmul(np.ascontiguousarray(x[rows]), y))
+
+
 # ------------------------------------------------------------------ split-K
 
 def test_split_k_integer_partials_bit_exact(lh, golden):
