@@ -336,6 +336,15 @@ LOOM_DEV void dma_load16_s(uint32_t voff, const void* sbase, uint32_t lds) {
 // 48 wait states: every MFMA issued before has written its result
 LOOM_DEV void mfma_drain() { asm volatile("s_nop 15\n\ts_nop 15\n\ts_nop 15" ::: "memory"); }
 
+// Store of a final output that this kernel never reads back: non-temporal,
+// so the written lines do not displace operands that other workgroups of the
+// same XCD still read through L2 (a GEMM's C tiles would otherwise fill every
+// L2 at each tile boundary and slow the K steps that follow).
+template <class V>
+LOOM_DEV void store_stream(V* p, const V& v) {
+  __builtin_nontemporal_store(v, p);
+}
+
 // s_waitcnt vmcnt(n), leaving LDS and export counters alone
 #define LOOM_WAIT_VMCNT(n) \
   __builtin_amdgcn_s_waitcnt(((n) & 15) | ((((n) >> 4) & 3) << 14) | 0x0F70)

@@ -674,7 +674,7 @@ __global__ void __launch_bounds__(256) gemm_pipe_kernel(GemmParams p) {
       for (int tm = 0; tm < TT; ++tm)
 #pragma unroll
         for (int tn = 0; tn < TT; ++tn)
-          *reinterpret_cast<u32x2_t*>(cb + (int64_t)(tm * 16) * p.ldc + tn * 16) = pk[tn][tm];
+          store_stream(reinterpret_cast<u32x2_t*>(cb + (int64_t)(tm * 16) * p.ldc + tn * 16), pk[tn][tm]);
     }
     return;
   }
@@ -691,8 +691,8 @@ __global__ void __launch_bounds__(256) gemm_pipe_kernel(GemmParams p) {
       if constexpr (OUT_F32)
         *reinterpret_cast<f32x4_t*>(static_cast<float*>(cz) + row * p.ldc + col) = v;
       else
-        *reinterpret_cast<u32x2_t*>(static_cast<uint16_t*>(cz) + row * p.ldc + col) =
-            u32x2_t{pack2<H>(v[0], v[1]), pack2<H>(v[2], v[3])};
+        store_stream(reinterpret_cast<u32x2_t*>(static_cast<uint16_t*>(cz) + row * p.ldc + col),
+                     u32x2_t{pack2<H>(v[0], v[1]), pack2<H>(v[2], v[3])});
     }
   }
 }
@@ -750,7 +750,6 @@ __global__ void __launch_bounds__(256) gemm_persist_kernel(GemmParams p, int nr)
   const int per_x = p.tiles_m * p.tiles_n * p.nz / 8;
   const int gx = (int)blockIdx.x % 8, gj = (int)blockIdx.x / 8;
   const int nk = (int)(p.k_total / BK);   // host: nk % NS == 0, nk >= NS
-  const int total = nr * nk;              // K steps over all of this workgroup's tiles
 
   auto tile_of = [&](int r, int& z, int64_t& m0, int64_t& n0) {
     const int l = gx * per_x + r * (G / 8) + gj;
@@ -765,16 +764,14 @@ __global__ void __launch_bounds__(256) gemm_persist_kernel(GemmParams p, int nr)
     m0 = (int64_t)(first_m + tin % gsz) * T;
     n0 = (int64_t)(tin / gsz) * T;
   };
-  // A / B addresses of global K step q (clamped to the last one: the stream's
-  // trailing loads re-read it into slots nothing reads again)
-  auto step_bases = [&](int q, const uint16_t*& ab, const uint16_t*& bb) {
-    q = min(q, total - 1);
-    const int r = q / nk, s = q - r * nk;
+  // A, B and C of tile r at k = 0
+  auto tile_ptrs = [&](int r, const uint16_t*& a, const uint16_t*& b, char*& c) {
     int z;
     int64_t m0, n0;
     tile_of(r, z, m0, n0);
-    ab = p.A + (int64_t)z * p.za + m0 * p.lda + (int64_t)s * BK;
-    bb = p.B + (int64_t)z * p.zb + n0 + (int64_t)s * BK * p.ldb;
+    a = p.A + (int64_t)z * p.za + m0 * p.lda;
+    b = p.B + (int64_t)z * p.zb + n0;
+    c = reinterpret_cast<char*>(static_cast<uint16_t*>(p.C) + (int64_t)z * p.zc + m0 * p.ldc + n0);
   };
 
   uint32_t aoff[A_INSTR], boff[B_INSTR];
@@ -824,13 +821,12 @@ __global__ void __launch_bounds__(256) gemm_persist_kernel(GemmParams p, int nr)
   f32x4_t acc[TT][TT];  // [n tile][m tile]: C^T tiles; every tile's first step sets them
   u32x4_t af[2][TT], bfr[2][TT];
 
-  // ---- prologue: global steps 0..NS-1, fragments of step 0
+  // ---- prologue: K steps 0..NS-1 of tile 0, fragments of step 0
+  const uint16_t *ar, *br;
+  char* cr;
+  tile_ptrs(0, ar, br, cr);
 #pragma unroll
-  for (int s = 0; s < NS; ++s) {
-    const uint16_t *ab, *bb;
-    step_bases(s, ab, bb);
-    issue(s, ab, bb);
-  }
+  for (int s = 0; s < NS; ++s) issue(s, ar + s * BK, br + (int64_t)s * BK * p.ldb);
   LOOM_WAIT_VMCNT((NS - 1) * LPW);
   barrier_nofence();
 #pragma unroll
@@ -880,36 +876,49 @@ __global__ void __launch_bounds__(256) gemm_persist_kernel(GemmParams p, int nr)
       __builtin_amdgcn_sched_barrier(0);
     }
   };
-  // NS steps starting at global step q0 (a multiple of NS: the DMA targets,
-  // steps q0+NS .. q0+2NS-1, lie in one tile)
-  auto group = [&](auto firstc, int q0) {
-    const uint16_t *ab, *bb;
-    step_bases(q0 + NS, ab, bb);
-    const bool clamped = q0 + NS >= total;
+  // NS steps; the DMA of step u loads K step (ab + u sa, bb + u sb), i.e. NS
+  // steps ahead: this tile's next NS steps, or in the tile's last NS steps the
+  // next tile's first NS (after the last tile: the last step again, sa = sb = 0)
+  auto group = [&](auto firstc, const uint16_t* ab, const uint16_t* bb, int64_t sa, int64_t sb) {
 #pragma unroll
     for (int u = 0; u < NS; ++u) {
-      const uint16_t* abu = clamped ? ab : ab + u * BK;
-      const uint16_t* bbu = clamped ? bb : bb + (int64_t)u * BK * p.ldb;
       if (u == 0)
-        step(firstc, u, abu, bbu, af[0], bfr[0], af[1], bfr[1]);
+        step(firstc, u, ab, bb, af[0], bfr[0], af[1], bfr[1]);
       else
-        step(std::false_type{}, u, abu, bbu, af[u & 1], bfr[u & 1], af[(u & 1) ^ 1],
+        step(std::false_type{}, u, ab + u * sa, bb + u * sb, af[u & 1], bfr[u & 1], af[(u & 1) ^ 1],
              bfr[(u & 1) ^ 1]);
     }
   };
 
+  const int ng = nk / NS;
   for (int r = 0; r < nr; ++r) {
-    group(std::true_type{}, r * nk);
-    for (int q0 = r * nk + NS; q0 < (r + 1) * nk; q0 += NS) group(std::false_type{}, q0);
+    const uint16_t *an, *bn;
+    char* cn;
+    int64_t sa = BK, sb = (int64_t)BK * p.ldb;
+    if (r + 1 < nr) {
+      tile_ptrs(r + 1, an, bn, cn);
+    } else {
+      an = ar + (nk - 1) * BK;
+      bn = br + (int64_t)(nk - 1) * BK * p.ldb;
+      cn = cr;
+      sa = 0;
+      sb = 0;
+    }
+    const int64_t ga = NS * BK, gb = (int64_t)NS * BK * p.ldb;   // one group of K steps
+    const bool one = ng == 1;
+    group(std::true_type{}, one ? an : ar + ga, one ? bn : br + gb, one ? sa : BK,
+          one ? sb : (int64_t)BK * p.ldb);
+    for (int g = 1; g < ng; ++g) {
+      const bool last = g == ng - 1;
+      group(std::false_type{}, last ? an : ar + (g + 1) * ga, last ? bn : br + (g + 1) * gb,
+            last ? sa : BK, last ? sb : (int64_t)BK * p.ldb);
+    }
 
     // ---- epilogue of tile r
     LOOM_WAIT_VMCNT(0);
     mfma_drain();
     acc_fence(acc);
-    int z;
-    int64_t m0, n0;
-    tile_of(r, z, m0, n0);
-    char* const cb = reinterpret_cast<char*>(static_cast<uint16_t*>(p.C) + (int64_t)z * p.zc + m0 * p.ldc + n0);
+    char* const cb = cr;
     // staging addresses: accumulator tile (tn, tm = 2 qt + h) of this lane
     // goes to row 32 wm + 16 h + lr, chunk (16 wn + 2 tn + lg / 2) ^ lr, i.e.
     // e_lane ^ (tn << 5) + 8 KB h; store row rho = 16 wave + 2 i + lane / 32
@@ -935,11 +944,14 @@ __global__ void __launch_bounds__(256) gemm_persist_kernel(GemmParams p, int nr)
         const u32x4_t v =
             *(const __attribute__((address_space(3))) u32x4_t*)(cst + ((r_lane ^ (uint32_t)(i << 5)) + i * 1024));
         char* const sb = cb + (int64_t)(qt * 32 + i * 2) * p.ldc * 2;
-        *reinterpret_cast<u32x4_t*>(sb + st_lane) = v;
+        store_stream(reinterpret_cast<u32x4_t*>(sb + st_lane), v);
       }
       LOOM_WAIT_LGKM0();
       barrier_nofence();
     }
+    ar = an;
+    br = bn;
+    cr = cn;
   }
 }
 
