@@ -339,7 +339,8 @@ LOOM_DEV void mfma_drain() { asm volatile("s_nop 15\n\ts_nop 15\n\ts_nop 15" :::
 // Store of a final output that this kernel never reads back: non-temporal,
 // so the written lines do not displace operands that other workgroups of the
 // same XCD still read through L2 (a GEMM's C tiles would otherwise fill every
-// L2 at each tile boundary and slow the K steps that follow).
+// L2 at each tile boundary and slow the K steps that follow).  Meant for
+// whole-line writes: 8-byte pieces of lines stored this way measured slower.
 template <class V>
 LOOM_DEV void store_stream(V* p, const V& v) {
   __builtin_nontemporal_store(v, p);

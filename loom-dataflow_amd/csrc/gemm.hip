@@ -674,7 +674,7 @@ __global__ void __launch_bounds__(256) gemm_pipe_kernel(GemmParams p) {
       for (int tm = 0; tm < TT; ++tm)
 #pragma unroll
         for (int tn = 0; tn < TT; ++tn)
-          store_stream(reinterpret_cast<u32x2_t*>(cb + (int64_t)(tm * 16) * p.ldc + tn * 16), pk[tn][tm]);
+          *reinterpret_cast<u32x2_t*>(cb + (int64_t)(tm * 16) * p.ldc + tn * 16) = pk[tn][tm];
     }
     return;
   }
@@ -691,8 +691,8 @@ __global__ void __launch_bounds__(256) gemm_pipe_kernel(GemmParams p) {
       if constexpr (OUT_F32)
         *reinterpret_cast<f32x4_t*>(static_cast<float*>(cz) + row * p.ldc + col) = v;
       else
-        store_stream(reinterpret_cast<u32x2_t*>(static_cast<uint16_t*>(cz) + row * p.ldc + col),
-                     u32x2_t{pack2<H>(v[0], v[1]), pack2<H>(v[2], v[3])});
+        *reinterpret_cast<u32x2_t*>(static_cast<uint16_t*>(cz) + row * p.ldc + col) =
+            u32x2_t{pack2<H>(v[0], v[1]), pack2<H>(v[2], v[3])};
     }
   }
 }
