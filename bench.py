@@ -350,7 +350,7 @@ def main():
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                     "traffic": traffic_for("gemm_pipe_kernel<256,false,false>")},
+                     "traffic": traffic_for("gemm_persist_kernel<false>")},
     }
     a0_a1 = None
     if not args.no_cpu:
