@@ -272,6 +272,22 @@ def test_attention_baseline_heads(lh, tile_m):
         assert_close(from_bf16(out[h:h + 1]), from_bf16(ref), **ATTN_TOL, what=f"head {h}")
 
 
+@pytest.mark.parametrize("causal,BH,Sq,Skv,D", [(True, 48, 2816, 2816, 128),
+                                                  (False, 132, 1024, 1000, 64)])
+def test_attention_tile256_many_items(lh, causal, BH, Sq, Skv, D):
+    """tile_m 256 with 528 (b, h, query tile) workgroups, two rounds and a partial
+    third on a 256-CU part: causal items of 4..44 KV blocks, or ragged Skv with
+    masked edge blocks.  Three heads vs the oracle."""
+    rng = np.random.default_rng(31)
+    k, v, q = rng_bf16(rng, (BH, D, Skv)), rng_bf16(rng, (BH, Skv, D)), rng_bf16(rng, (BH, Sq, D))
+    out = host(lh.attention(dev(k), dev(v), dev(q), causal=causal, tile_m=256, tile_n=64))
+    assert np.isfinite(from_bf16(out)).all()
+    for h in (0, BH // 2 - 1, BH - 1):
+        ref = oracle.attention(k[h:h + 1], v[h:h + 1], q[h:h + 1], 1 / math.sqrt(D), causal, 1,
+                               128, 64)
+        assert_close(from_bf16(out[h:h + 1]), from_bf16(ref), **ATTN_TOL, what=f"head {h}")
+
+
 # ------------------------------------------------------------- flash_decode
 
 @pytest.mark.parametrize("name,tile_s", [("decode_ragged", 64), ("decode_ragged", 200),
