@@ -7,19 +7,23 @@
 //   @split_k_matmul_gather  examples/split_k_mm_gather/IR/00_from_helion_frontend.mlir:2-56
 // Operands are row-major: A [M,K], B [K,N], C [M,N] (per batch for bmm).
 //
-// Kernel shape: one workgroup per (tile_m x tile_n) output tile, the grid
-// flattened over (z, tile) with z = batch (bmm) or K-slab (split-K).  The
-// K loop stages 64-deep A and B tiles through LDS, double buffered, one
-// barrier per step:
-//   - half of the threads copy A rows (16-byte chunks, coalesced);
-//   - the other half copy B as 8x8 blocks (eight 16-byte row loads), transpose
-//     each block in registers and store B^T, so both MFMA operands are read
-//     as one 16-byte LDS load per lane (k contiguous);
-//   - LDS rows are 128 bytes with the 16-byte chunk index XOR-swizzled by
-//     (row & 7), which keeps the MFMA operand reads and the transposed B
-//     stores free of bank conflicts without padding.
-// Each wave owns a (tile_m/WM) x (tile_n/WN) sub-tile of 16x16 fp32
-// accumulators fed by v_mfma_f32_16x16x32_bf16.
+// Kernels, fastest first (launch_gemm picks the first whose conditions hold):
+//   gemm_persist_kernel  256x256 tiles, bf16 out, whole tiles dividing evenly
+//                        over one workgroup per CU (>= 2 each): persistent,
+//                        one LDS-DMA stream across tiles, C staged through LDS
+//                        and stored as whole rows.
+//   gemm_pipe_kernel<T>  T x T tiles (256, 128, 64), one per workgroup,
+//                        software-pipelined LDS-DMA stages with the MFMA
+//                        fragments of the next stage read during this one.
+//   gemm_dma_kernel      256x256 tiles, LDS-DMA stages, K a multiple of 32.
+//   gemm_bf16_kernel     any shape: register-staged 64-deep tiles (half of the
+//                        threads copy A rows, the other half copy 8x8 blocks of
+//                        B, transpose them in registers and store B^T), LDS rows
+//                        of 128 bytes XOR-swizzled by (row & 7).
+// All compute C^T tiles with v_mfma_f32_16x16x32_bf16 (B^T as the row
+// operand, A^T as the column operand), fp32 accumulate, the grid flattened
+// over (z, tile) with z = batch (bmm) or K-slab (split-K) and remapped so
+// each XCD owns a contiguous range of tiles.
 #include "common.h"
 
 #include <type_traits>
