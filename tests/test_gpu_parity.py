@@ -86,6 +86,22 @@ def test_matmul_pipelined_edge_tiles_bit_exact(lh):
             assert np.array_equal(got, ref), (M, N, K, t)
 
 
+def test_matmul_tile64_whole_tiles_bit_exact(lh):
+    """64x64 tiles on whole-tile shapes (the pipelined 64-tile kernel with its
+    16-stage ring): integer-valued inputs, every element exact; also batched."""
+    rng = np.random.default_rng(13)
+    for (M, N, K) in [(1024, 1024, 1024), (512, 192, 2048), (64, 64, 512)]:
+        x = to_bf16(rng.integers(-8, 9, (M, K)).astype(np.float32))
+        y = to_bf16(rng.integers(-8, 9, (K, N)).astype(np.float32))
+        got = host(lh.matmul(dev(x), dev(y), tile_m=64, tile_n=64))
+        assert np.array_equal(got, oracle.matmul(x, y)), (M, N, K)
+    a0 = to_bf16(rng.integers(-8, 9, (3, 256, 512)).astype(np.float32))
+    a1 = to_bf16(rng.integers(-8, 9, (3, 512, 128)).astype(np.float32))
+    out = host(lh.batch_matmul(dev(a0), dev(a1), tile_m=64, tile_n=64))
+    for b in range(3):
+        assert np.array_equal(out[b], oracle.matmul(a0[b], a1[b])), b
+
+
 def test_matmul_baseline_1024(lh):
     rng = np.random.default_rng(1)
     x = rng_bf16(rng, (1024, 1024), "uniform")
