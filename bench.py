@@ -108,6 +108,26 @@ def time_back_to_back(torch, fn, iters):
     return a.elapsed_time(b) / iters
 
 
+def per_call_ms(torch, fn, iters):
+    """GPU time (ms) of each of `iters` back-to-back calls, from a HIP event
+    recorded between consecutive calls on the launch stream (a marker in the
+    stream: the calls still run back to back)."""
+    s = torch.cuda.current_stream()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(iters + 1)]
+    torch.cuda.synchronize()
+    ev[0].record(s)
+    for i in range(iters):
+        fn(i)
+        ev[i + 1].record(s)
+    torch.cuda.synchronize()
+    return [ev[i].elapsed_time(ev[i + 1]) for i in range(iters)]
+
+
+def quantile(xs, q):
+    xs = sorted(xs)
+    return xs[min(len(xs) - 1, max(0, int(round(q * (len(xs) - 1)))))]
+
+
 # --------------------------------------------------------------------------
 # BASELINE configurations.  Each case holds enough independent copies of its
 # inputs that consecutive calls read more than three times the Infinity
@@ -240,7 +260,10 @@ def make_cases(torch, lh):
     return cases
 
 
-def report(case, ms):
+def report(case, ms, calls=None):
+    """`ms`: mean per call from one event pair around a burst (the figure the
+    rates use); `calls`: per-call times of a second burst, summarised as
+    median / p10 / p90."""
     s = ms / 1e3
     tflops = case["flop"] / s / 1e12
     gbs = case["bytes"] / s / 1e9
@@ -248,9 +271,14 @@ def report(case, ms):
         frac = tflops / PEAK_BF16_TFLOPS
     else:
         frac = gbs / PEAK_HBM_GBS
-    return {"desc": case["desc"], "ms": round(ms, 5), "tflops": round(tflops, 2),
-            "gbs": round(gbs, 1), "bound": case["bound"], "roofline_frac": round(frac, 4),
-            "input_copies": case["sets"]}
+    out = {"desc": case["desc"], "ms": round(ms, 5), "tflops": round(tflops, 2),
+           "gbs": round(gbs, 1), "bound": case["bound"], "roofline_frac": round(frac, 4),
+           "input_copies": case["sets"]}
+    if calls:
+        out["ms_median"] = round(median(calls), 5)
+        out["ms_p10"] = round(quantile(calls, 0.1), 5)
+        out["ms_p90"] = round(quantile(calls, 0.9), 5)
+    return out
 
 
 def cpu_baseline(torch, a0, a1, budget_s=12.0):
@@ -373,7 +401,8 @@ def main():
             case = cases[name]()
             settle(torch, case["fn"], args.settle_ms / 3)
             ms = time_back_to_back(torch, case["fn"], args.iters)
-            table[name] = report(case, ms)
+            calls = per_call_ms(torch, case["fn"], args.iters)
+            table[name] = report(case, ms, calls)
             print(f"# {name}: {table[name]}", file=sys.stderr, flush=True)
             del case
             torch.cuda.empty_cache()
