@@ -124,6 +124,14 @@ __global__ void __launch_bounds__(64 * W) attention_dma_kernel(AttnParams p) {
     }
   };
 
+  const int kv_end = p.causal ? min(Skv, q0 + BQ) : Skv;
+  const int nblk = (kv_end + KB - 1) / KB;
+  // the first NS-1 KV blocks start loading before Q, so their latency and
+  // Q's overlap (the compiler's wait for Q then also covers these DMAs)
+#pragma unroll
+  for (int s = 0; s < NS - 1; ++s)
+    if (s < nblk) issue(s, s);
+
   // ---- Q^T operands: lane holds q[q0w + 16 qt + r][32 ds + 8 g .. +7] times
   // scale * log2(e), rounded to bf16, so scores come out in the log2 domain
   const int q0w = q0 + 16 * QT * wave;
@@ -153,9 +161,6 @@ __global__ void __launch_bounds__(64 * W) attention_dma_kernel(AttnParams p) {
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) ot[dt][qt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   }
-
-  const int kv_end = p.causal ? min(Skv, q0 + BQ) : Skv;
-  const int nblk = (kv_end + KB - 1) / KB;
 
   auto compute = [&](int s, int blk) {
     const int kv0 = blk * KB;
@@ -267,10 +272,8 @@ __global__ void __launch_bounds__(64 * W) attention_dma_kernel(AttnParams p) {
     }
   };
 
-  // ---- pipeline: NS stages, waits placed by hand (see gemm.hip)
-#pragma unroll
-  for (int s = 0; s < NS - 1; ++s)
-    if (s < nblk) issue(s, s);
+  // ---- pipeline: NS stages (the first NS-1 issued above), waits placed by
+  // hand as in gemm.hip
   for (int it0 = 0; it0 < nblk; it0 += NS) {
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
