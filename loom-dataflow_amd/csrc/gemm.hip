@@ -26,6 +26,7 @@
 // each XCD owns a contiguous range of tiles.
 #include "common.h"
 
+#include <atomic>
 #include <type_traits>
 
 #ifndef LOOM_GEMM_PERSIST
@@ -962,16 +963,26 @@ __global__ void __launch_bounds__(256) gemm_persist_kernel(GemmParams p, int nr)
 // Launches the persistent kernel when every tile is whole, the tiles divide
 // evenly over one workgroup per CU (at least two each) and the pipelined
 // kernel's conditions hold; the caller falls back otherwise.
+// CU count of the current device, cached per device (0 when unknown: the
+// persistent kernel is then not used).
+int device_cus() {
+  static std::atomic<int> cache[64];   // count + 1; 0 = not queried yet
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  if (dev < 0 || dev >= 64) return 0;
+  int c = cache[dev].load(std::memory_order_relaxed);
+  if (c == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) n = 0;
+    c = n + 1;
+    cache[dev].store(c, std::memory_order_relaxed);
+  }
+  return c - 1;
+}
+
 template <bool H>
 bool launch_persist(const GemmParams& p, bool aligned, bool out_f32, hipStream_t st) {
-  static int cus = -1;
-  if (cus < 0) {
-    int dev = 0, n = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-      n = 0;
-    cus = n;
-  }
+  const int cus = device_cus();
   const int64_t ntiles = (int64_t)p.tiles_m * p.tiles_n * p.nz;
   const bool ok = LOOM_GEMM_PERSIST && aligned && !out_f32 && !p.split && cus >= 8 && cus % 8 == 0 &&
                   p.M % 256 == 0 && p.N % 256 == 0 && p.k_total % 128 == 0 && ntiles % cus == 0 &&
