@@ -132,6 +132,7 @@ constexpr int kSsdQmax = 256, kSsdPmax = 256, kSsdNB = 64, kSsdWaves = 8;
 constexpr int kSsdStageMax = 36 * 1024;      // bytes per pipeline stage
 constexpr int kSsdRing = 4 * kSsdStageMax;   // LDS for the stage ring
 constexpr int kSsdNSMax = 8;                 // stages at most
+constexpr int kSsdMaxLpw = 5;                // DMA copies per wave per unit at most
 
 // A chunk is processed in units of QS keys (QS divides Q; a chunk whose Q
 // is not a multiple of 32 is one unit zero-weighted up to QSP rows).  Unit u
@@ -146,7 +147,7 @@ struct SsdStateParams {
   int H, G, nc, Q, P, N, nb;
   int QS, QSP, upc;          // keys per unit, LDS rows per unit, units per chunk
   int xbytes, bbytes;        // per stage
-  int ninstr, lpw;           // DMA instructions per unit, per wave (padded)
+  int ninstr, lpw;           // DMA copies per unit; the most any wave issues
   int ns;                    // stages in the ring (3 .. 8)
 };
 
@@ -154,8 +155,8 @@ struct SsdStateParams {
 // one p tile and the w-scaled x operand is built once per k step.
 template <int TPW, bool SHARED_PT, bool F16>
 __global__ void __launch_bounds__(64 * kSsdWaves) ssd_state_kernel(SsdStateParams p) {
-  __shared__ __attribute__((aligned(1024))) char smem[kSsdRing + 1024];
-  __shared__ __attribute__((aligned(16))) float s_w[2][128];  // w of units u, u+1 (by parity)
+  __shared__ __attribute__((aligned(1024))) char smem[kSsdRing];
+  __shared__ __attribute__((aligned(16))) float s_w[kSsdWaves][128];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = lane & 15, gq = lane >> 4, a4 = r >> 2, c4 = r & 3;
@@ -175,37 +176,52 @@ __global__ void __launch_bounds__(64 * kSsdWaves) ssd_state_kernel(SsdStateParam
   const float* dAg = p.dA + (int64_t)bh * nc * Q;
   const float* dtg = p.dt + (int64_t)bh * nc * Q;
   lds_char_t* const sm = (lds_char_t*)smem;
-  const uint32_t scratch = lds_addr(sm + kSsdRing);
   const int NS = p.ns;
 
   // ---- DMA of unit u into stage s; rows past the unit's keys are clamped
-  // (their weight is forced to zero)
-  auto issue = [&](int s, int u) {
+  // (their weight is forced to zero).  Copy j of the unit belongs to wave
+  // j % 8, so wave w issues nlw = ceil((ninstr - w) / 8) copies per unit,
+  // its slots i = 0 .. nlw-1 (j = w + 8 i).  A slot's source offset within
+  // the unit and its LDS offset within the stage are the same for every
+  // unit: computed once here.
+  const int nlw = (p.ninstr - wave + kSsdWaves - 1) / kSsdWaves;
+  int goff[kSsdMaxLpw], loff[kSsdMaxLpw], kind[kSsdMaxLpw];  // kind: 0 x, 1 B, 2 dA|dt, 3 dA tail
+#pragma unroll
+  for (int i = 0; i < kSsdMaxLpw; ++i) {
+    const int j = wave + kSsdWaves * i;
+    if (j < xinstr) {
+      const int e = (j * 64 + lane) * 8;          // element offset in the [QSP][P] unit
+      goff[i] = min(e / P, QS - 1) * P + e % P;
+      loff[i] = j * 1024;
+      kind[i] = 0;
+    } else if (j < xinstr + binstr) {
+      const int idx = (j - xinstr) * 64 + lane;
+      goff[i] = min(idx / (nb / 8), QS - 1) * N + (idx % (nb / 8)) * 8;
+      loff[i] = p.xbytes + (j - xinstr) * 1024;
+      kind[i] = 1;
+    } else {
+      goff[i] = min(4 * (lane & 31), QS - 4);
+      loff[i] = p.xbytes + p.bbytes + (j == xinstr + binstr ? 0 : 1024);
+      kind[i] = j == xinstr + binstr ? 2 : 3;
+    }
+  }
+  // slots [i0, i1) of unit u
+  auto issue = [&](int s, int u, int i0, int i1) {
     const int c = u / upc, ko = (u % upc) * QS;
     const int64_t key0 = (int64_t)c * Q + ko;   // first key of the unit within (b, h)
     const uint32_t base = lds_addr(sm + s * stage_bytes);
-    for (int i = 0; i < p.lpw; ++i) {
-      const int j = wave + kSsdWaves * i;
-      if (j < xinstr) {
-        const int e = (j * 64 + lane) * 8;        // element offset in the [QSP][P] unit
-        const int k = min(e / P, QS - 1), col = e % P;
-        dma_load16(xg + (key0 + k) * P + col, base + j * 1024);
-      } else if (j < xinstr + binstr) {
-        const int idx = (j - xinstr) * 64 + lane;
-        const int k = min(idx / (nb / 8), QS - 1), col = (idx % (nb / 8)) * 8;
-        dma_load16(bgp + (key0 + k) * N + col, base + p.xbytes + (j - xinstr) * 1024);
-      } else if (j == xinstr + binstr) {
-        const int half = lane >> 5, k = min(4 * (lane & 31), QS - 4);
-        dma_load16((half ? dtg : dAg) + key0 + k, base + p.xbytes + p.bbytes);
-      } else if (j == xinstr + binstr + 1) {
-        dma_load16(dAg + (int64_t)c * Q + Q - 4, base + p.xbytes + p.bbytes + 1024);
-      } else {
-        dma_load16(xg, scratch);                  // padding: every wave issues lpw copies
-      }
+#pragma unroll
+    for (int i = 0; i < kSsdMaxLpw; ++i) {
+      if (i < i0 || i >= i1) continue;
+      const uint32_t la = base + loff[i];
+      if (kind[i] == 0) dma_load16(xg + key0 * P + goff[i], la);
+      else if (kind[i] == 1) dma_load16(bgp + key0 * N + goff[i], la);
+      else if (kind[i] == 2) dma_load16((lane >> 5 ? dtg : dAg) + key0 + goff[i], la);
+      else dma_load16(dAg + (int64_t)c * Q + Q - 4, la);
     }
   };
   auto wait_units = [&](int younger, int stores) {
-    const int n = younger * p.lpw + stores;
+    const int n = younger * nlw + stores;
     switch (n) {
       case 0: LOOM_WAIT_VMCNT(0); break;
       case 1: LOOM_WAIT_VMCNT(1); break;
@@ -240,36 +256,55 @@ __global__ void __launch_bounds__(64 * kSsdWaves) ssd_state_kernel(SsdStateParam
   f32x4_t R[TPW];
 #pragma unroll
   for (int t = 0; t < TPW; ++t) R[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  // ---- w_c[k] = exp(dA[c, Q-1] - dA[c, k]) dt[c, k] of unit u (stage s)
-  // into s_w[u & 1], one key per thread; zero past the unit's keys
-  auto make_w = [&](int s, int u) {
-    const int ko = (u % upc) * QS;
-    if (tid < QSP) {
-      const float* dAs = reinterpret_cast<const float*>(smem + s * stage_bytes + p.xbytes + p.bbytes);
-      const float last = dAs[256 + 3];
-      float w = 0.f;
-      if (tid < QS && ko + tid < Q)
-        w = fast_exp2((last - dAs[tid]) * 1.4426950408889634f) * dAs[128 + tid];
-      s_w[u & 1][tid] = w;
-    }
+  const int nst = min(TPW, max(0, (tiles - wave + kSsdWaves - 1) / kSsdWaves));  // tiles of this wave
+  // w_c[k] = exp(dA[c, Q-1] - dA[c, k]) dt[c, k] of the current unit (zero
+  // past its QS keys), one copy per wave in s_w[wave]: a wave writes and
+  // reads only its own row, so no barrier is involved.  dAs: the stage's dA
+  // (keys 0..127), dt (128..255) and dA[c, Q-4 .. Q-1] (256..259).
+  float* const sw = s_w[wave];
+  auto make_w = [&](const float* dAs) {
+    const float last = dAs[256 + 3];
+    for (int i = lane; i < QSP; i += 64)
+      sw[i] = i < QS ? fast_exp2((last - dAs[i]) * 1.4426950408889634f) * dAs[128 + i] : 0.f;
+    LOOM_WAIT_LGKM0();
+    __asm__ volatile("" ::: "memory");
   };
 
-  // x^T operand of p tile pt at k step ks, scaled by w and split into
-  // bf16 hi + lo (the products keep ~16 significant bits)
-  auto x_operand = [&](const lds_char_t* xs, const float* wv, int pt, int k0, u32x4_t& vh,
-                       u32x4_t& vl) {
-    const lds_char_t* qx = xs + (k0 + a4) * XR + (2 * pt + (c4 >> 1)) * 16 + (c4 & 1) * 8;
-    const u32x2_t xlo = lds_read_tr16(qx), xhi = lds_read_tr16(qx + 16 * XR);
-    const f32x4_t w0 = *reinterpret_cast<const f32x4_t*>(wv + k0);
-    const f32x4_t w1 = *reinterpret_cast<const f32x4_t*>(wv + k0 + 16);
-    const float v[8] = {lo16<F16>(xlo[0]) * w0[0], hi16<F16>(xlo[0]) * w0[1],
-                        lo16<F16>(xlo[1]) * w0[2], hi16<F16>(xlo[1]) * w0[3],
-                        lo16<F16>(xhi[0]) * w1[0], hi16<F16>(xhi[0]) * w1[1],
-                        lo16<F16>(xhi[1]) * w1[2], hi16<F16>(xhi[1]) * w1[3]};
+  // x^T operand (keys k0 + 0..3 from x0, k0 + 16..19 from x1) scaled by w
+  // and split into bf16 hi + lo: the products keep ~16 significant bits
+  auto scale_x = [&](const u32x2_t& x0, const u32x2_t& x1, const f32x4_t& w0, const f32x4_t& w1,
+                     u32x4_t& vh, u32x4_t& vl) {
+    const float v[8] = {lo16<F16>(x0[0]) * w0[0], hi16<F16>(x0[0]) * w0[1],
+                        lo16<F16>(x0[1]) * w0[2], hi16<F16>(x0[1]) * w0[3],
+                        lo16<F16>(x1[0]) * w1[0], hi16<F16>(x1[0]) * w1[1],
+                        lo16<F16>(x1[1]) * w1[2], hi16<F16>(x1[1]) * w1[3]};
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       vh[e] = pack2<F16>(v[2 * e], v[2 * e + 1]);
       vl[e] = pack2<F16>(v[2 * e] - lo16<F16>(vh[e]), v[2 * e + 1] - hi16<F16>(vh[e]));
+    }
+  };
+  // MFMA operands of one 32-key step: x^T of p tile pt, w, and B of the
+  // wave's n tiles (n = 16 nt + r); tiles past the wave's count read tile
+  // tiles-1 (in range, results unused)
+  struct Ops {
+    u32x2_t x0, x1;
+    f32x4_t w0, w1;
+    u32x2_t b0[TPW], b1[TPW];
+  };
+  auto load_ops = [&](const lds_char_t* xs, const lds_char_t* bs, int ks, int pt, Ops& o) {
+    const int k0 = 32 * ks + 4 * gq;          // this lane's keys: k0 + 0..3, k0 + 16..19
+    const lds_char_t* qx = xs + (k0 + a4) * XR + (2 * pt + (c4 >> 1)) * 16 + (c4 & 1) * 8;
+    o.x0 = lds_read_tr16(qx);
+    o.x1 = lds_read_tr16(qx + 16 * XR);
+    o.w0 = *reinterpret_cast<const f32x4_t*>(sw + k0);
+    o.w1 = *reinterpret_cast<const f32x4_t*>(sw + k0 + 16);
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) {
+      const int nt = min(wave + kSsdWaves * t, tiles - 1) / ptiles;
+      const lds_char_t* qb = bs + (k0 + a4) * BR + (2 * nt + (c4 >> 1)) * 16 + (c4 & 1) * 8;
+      o.b0[t] = lds_read_tr16(qb);
+      o.b1[t] = lds_read_tr16(qb + 16 * BR);
     }
   };
 
@@ -277,10 +312,15 @@ __global__ void __launch_bounds__(64 * kSsdWaves) ssd_state_kernel(SsdStateParam
     const int c = u / upc, part = u % upc;
     const lds_char_t* xs = sm + s * stage_bytes;
     const lds_char_t* bs = xs + p.xbytes;
-    const float* wv = s_w[u & 1];
+    const float* dAs = reinterpret_cast<const float*>(smem + s * stage_bytes + p.xbytes + p.bbytes);
+    // the DMA of unit u+NS-1 (into the stage unit u-1 used) is issued in two
+    // halves between this unit's steps, so the address units work through
+    // it while the waves compute
+    const bool pre = u + NS - 1 < nu;
+    const int sn = (u + NS - 1) % NS, un = u + NS - 1, half = (nlw + 1) / 2;
+    make_w(dAs);
     if (part == 0) {
       // prev(c) out, then R = exp(dA[c, Q-1]) R; states(c) accumulate below
-      const float* dAs = reinterpret_cast<const float*>(smem + s * stage_bytes + p.xbytes + p.bbytes);
       const float decay = fast_exp2(dAs[256 + 3] * 1.4426950408889634f);
       float* outc = p.prevT + (((int64_t)(b * nc + c) * H + h) * N + n0) * P;
 #pragma unroll
@@ -293,46 +333,68 @@ __global__ void __launch_bounds__(64 * kSsdWaves) ssd_state_kernel(SsdStateParam
         }
       }
     }
-#pragma unroll 4
-    for (int ks = 0; ks < QSP / 32; ++ks) {
-      const int k0 = 32 * ks + 4 * gq;          // this lane's keys: k0 + 0..3, k0 + 16..19
-      u32x4_t xh, xl;
-      if (SHARED_PT && wave < tiles) x_operand(xs, wv, wave % ptiles, k0, xh, xl);
+    const int nks = QSP / 32;
+    if constexpr (SHARED_PT) {
+      // all tiles of the wave share p tile wave % ptiles: one scaled x
+      // operand per step; the next step's operands are read while this
+      // step's MFMAs run
+      const int ptw = wave % ptiles;
+      Ops cur;
+      load_ops(xs, bs, 0, ptw, cur);
+      for (int ks = 0; ks < nks; ++ks) {
+        Ops nxt;
+        load_ops(xs, bs, min(ks + 1, nks - 1), ptw, nxt);
+        u32x4_t xh, xl;
+        scale_x(cur.x0, cur.x1, cur.w0, cur.w1, xh, xl);
 #pragma unroll
-      for (int t = 0; t < TPW; ++t) {
-        const int tt = wave + kSsdWaves * t;
-        if (tt < tiles) {
-          const int pt = tt % ptiles, nt = tt / ptiles;
-          if (!SHARED_PT) x_operand(xs, wv, pt, k0, xh, xl);
-          // B operand: n = 16 nt + r, same keys
-          const lds_char_t* qb = bs + (k0 + a4) * BR + (2 * nt + (c4 >> 1)) * 16 + (c4 & 1) * 8;
-          const u32x2_t blo = lds_read_tr16(qb), bhi = lds_read_tr16(qb + 16 * BR);
-          const u32x4_t bf = u32x4_t{blo[0], blo[1], bhi[0], bhi[1]};
-          R[t] = mfma16t<F16>(xh, bf, R[t]);
-          R[t] = mfma16t<F16>(xl, bf, R[t]);
+        for (int t = 0; t < TPW; ++t) {
+          if (t < nst) {
+            const u32x4_t bf = u32x4_t{cur.b0[t][0], cur.b0[t][1], cur.b1[t][0], cur.b1[t][1]};
+            R[t] = mfma16t<F16>(xh, bf, R[t]);
+            R[t] = mfma16t<F16>(xl, bf, R[t]);
+          }
+        }
+        if (ks == 0 && pre) issue(sn, un, 0, half);
+        cur = nxt;
+      }
+      if (pre) issue(sn, un, half, nlw);
+    } else {
+      if (pre) issue(sn, un, 0, nlw);
+      for (int ks = 0; ks < nks; ++ks) {
+        const int k0 = 32 * ks + 4 * gq;
+#pragma unroll
+        for (int t = 0; t < TPW; ++t) {
+          const int tt = wave + kSsdWaves * t;
+          if (tt < tiles) {
+            const int pt = tt % ptiles, nt = tt / ptiles;
+            const lds_char_t* qx = xs + (k0 + a4) * XR + (2 * pt + (c4 >> 1)) * 16 + (c4 & 1) * 8;
+            u32x4_t xh, xl;
+            scale_x(lds_read_tr16(qx), lds_read_tr16(qx + 16 * XR),
+                    *reinterpret_cast<const f32x4_t*>(sw + k0),
+                    *reinterpret_cast<const f32x4_t*>(sw + k0 + 16), xh, xl);
+            const lds_char_t* qb = bs + (k0 + a4) * BR + (2 * nt + (c4 >> 1)) * 16 + (c4 & 1) * 8;
+            const u32x2_t blo = lds_read_tr16(qb), bhi = lds_read_tr16(qb + 16 * BR);
+            const u32x4_t bf = u32x4_t{blo[0], blo[1], bhi[0], bhi[1]};
+            R[t] = mfma16t<F16>(xh, bf, R[t]);
+            R[t] = mfma16t<F16>(xl, bf, R[t]);
+          }
         }
       }
     }
   };
 
-  // ---- pipeline: units issued NS-1 ahead.  Iteration u waits for units u
-  // and u+1, so w of unit u+1 can be built (into the other s_w buffer) while
-  // unit u computes; the barrier of iteration u+1 publishes it.  The DMA
-  // after the barrier of iteration u reuses the stage of unit u-1, finished
-  // before that barrier.  prev stores issued by compute(u) are younger than
-  // the DMAs in flight, so the next wait leaves them outstanding too.
-  const int nst = min(TPW, max(0, (tiles - wave + kSsdWaves - 1) / kSsdWaves));
-  for (int u = 0; u < NS - 1 && u < nu; ++u) issue(u, u);
-  wait_units(min(NS - 2, nu - 1), 0);
-  barrier_nofence();
-  make_w(0, 0);
+  // ---- pipeline: units issued NS-1 ahead.  Iteration u waits for unit u
+  // only, so NS-1 units are in flight while it waits.  The DMA issued by
+  // compute(u), after the barrier of iteration u, reuses the stage of unit
+  // u-1, whose reads every wave finished before that barrier.  prev stores
+  // issued by compute(u) are younger than unit u+NS-2's DMA, so the next
+  // wait (for unit u+1) leaves them outstanding too.
+  for (int u = 0; u < NS - 1 && u < nu; ++u) issue(u, u, 0, nlw);
   int stores = 0;
   for (int u = 0; u < nu; ++u) {
-    wait_units(max(0, min(NS - 3, nu - 2 - u)), stores);
-    LOOM_WAIT_LGKM0();                        // s_w writes visible after the barrier
+    wait_units(max(0, min(NS - 2, nu - 1 - u)), stores);
+    LOOM_WAIT_LGKM0();                        // this wave's reads of unit u-1's stage done
     barrier_nofence();
-    if (u + NS - 1 < nu) issue((u + NS - 1) % NS, u + NS - 1);
-    if (u + 1 < nu) make_w((u + 1) % NS, u + 1);
     compute(u % NS, u);
     stores = (u % upc == 0) ? nst : 0;
   }
@@ -446,33 +508,39 @@ int state_passing_impl(const void* x, const void* dt, const void* dA_cumsum,
   p.prevT = static_cast<float*>(prev_states_T);
   p.H = (int)nheads; p.G = (int)ngroups; p.nc = (int)nchunks; p.Q = (int)chunk_size;
   p.P = (int)headdim; p.N = (int)dstate; p.nb = nb;
-  // unit: the largest of 128, 64, 32 keys dividing Q whose stage fits; a Q
-  // that is not a multiple of 32 is one unit padded to the next 32
-  p.QS = 0;
-  for (int qs : {128, 64, 32})
-    if (p.Q % qs == 0 && qs * (p.P + nb) * 2 + 2048 <= kSsdStageMax) { p.QS = qs; break; }
-  if (p.QS == 0 && p.Q % 32 != 0 && p.Q < 128) p.QS = p.Q;
-  p.QSP = (p.QS + 31) & ~31;
-  if (p.QS == 0 || p.QSP * (p.P + nb) * 2 + 2048 > kSsdStageMax)
+  // unit: the largest of 128, 64 and 32 keys dividing Q whose stage fits
+  // (each unit costs a barrier and a wait, and the copies in flight per
+  // workgroup, not the ring depth, bound the stream: 128-key units measured
+  // faster than 64-key units with twice the stages); a Q that is not a
+  // multiple of 32 is one unit padded to the next 32.  Stages: as many as
+  // fit while the wait count stays encodable.
+  auto plan = [&](int qs, SsdStateParams& q) {
+    q.QS = qs;
+    q.QSP = (qs + 31) & ~31;
+    q.upc = q.Q / qs;
+    q.xbytes = (q.QSP * q.P * 2 + 1023) & ~1023;  // whole 1 KB DMA copies
+    q.bbytes = (q.QSP * nb * 2 + 1023) & ~1023;
+    q.ninstr = q.xbytes / 1024 + q.bbytes / 1024 + 2;
+    q.lpw = (q.ninstr + kSsdWaves - 1) / kSsdWaves;
+    if (q.lpw > kSsdMaxLpw) return -1;
+    if (q.xbytes + q.bbytes + 2048 > kSsdStageMax) return -1;
+    q.ns = std::min(kSsdNSMax, kSsdRing / (q.xbytes + q.bbytes + 2048));
+    while (q.ns > 3 && q.lpw * (q.ns - 2) + tpw > 24) --q.ns;
+    if (q.ns < 3 || q.lpw * (q.ns - 2) + tpw > 24) return -1;
+    return (q.ns - 1) * (q.xbytes + q.bbytes);
+  };
+  int best = -1;
+  for (int qs : {128, 64, 32}) {
+    if (p.Q % qs) continue;
+    SsdStateParams q = p;
+    if ((best = plan(qs, q)) >= 0) { p = q; break; }
+  }
+  if (best < 0 && p.Q % 32 != 0 && p.Q < 128) best = plan(p.Q, p);
+  if (best < 0)
     return loom_fail(err, errlen, LOOM_EUNSUP,
                      "ssd_chunk_state_passing: chunk_size %lld with headdim %lld does not fit "
                      "an LDS stage",
                      (long long)chunk_size, (long long)headdim);
-  p.upc = p.Q / p.QS;
-  p.xbytes = p.QSP * p.P * 2;
-  p.bbytes = p.QSP * nb * 2;
-  if (p.xbytes % 1024 || p.bbytes % 1024) {
-    // rows of fewer than 1 KB per 32 keys: pad the unit to whole DMA copies
-    p.xbytes = (p.xbytes + 1023) & ~1023;
-    p.bbytes = (p.bbytes + 1023) & ~1023;
-  }
-  p.ninstr = p.xbytes / 1024 + p.bbytes / 1024 + 2;
-  p.lpw = (p.ninstr + kSsdWaves - 1) / kSsdWaves;
-  // as many stages as fit, while the wait count stays encodable
-  p.ns = std::min(kSsdNSMax, kSsdRing / (p.xbytes + p.bbytes + 2048));
-  while (p.ns > 3 && p.lpw * (p.ns - 2) + tpw > 24) --p.ns;
-  if (p.ns < 3 || p.lpw * (p.ns - 2) + tpw > 24)
-    return loom_fail(err, errlen, LOOM_EUNSUP, "ssd_chunk_state_passing: stage too large");
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int gx = (int)(batch * nheads), gy = (int)(dstate / nb);
   if (loom_validate_only()) return loom_ok(err, errlen);
