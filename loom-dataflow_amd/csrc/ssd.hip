@@ -18,10 +18,12 @@
 // gfx950 mapping:
 //   ssd_cumsum_kernel  one wave per (b,h,c): per-lane serial sums, then a
 //                      wave prefix scan of the lane totals (DPP shuffles).
-//   ssd_cb_kernel      one wave per (b,c,g, 16-row band): MFMA D = B . C^T
-//                      over n, straight from global memory (both operands
-//                      are n-contiguous rows); the transposed tile gives each
-//                      lane four consecutive j of one row i (8-byte stores).
+//   ssd_cb_kernel      one wave per (b,c,g, 16-row band, four 16-column
+//                      tiles): MFMA D = B . C^T over n, straight from global
+//                      memory (both operands are n-contiguous rows), every
+//                      load issued before the first MFMA; the transposed
+//                      tile gives each lane four consecutive j of one row i
+//                      (8-byte stores).
 //   ssd_state_kernel   one workgroup per (b, h, 64-wide n block) walks the
 //                      chunks in order, keeping prev_states in the MFMA
 //                      accumulators: per chunk it stores prev(c), scales by
@@ -75,6 +77,7 @@ __global__ void __launch_bounds__(64) ssd_cumsum_kernel(const float* __restrict_
 // ---------------------------------------------------------------------------
 // cb = C B^T, lower triangle
 // ---------------------------------------------------------------------------
+constexpr int kCbTiles = 4;  // 16x16 output tiles per wave (one row band)
 template <bool F16>
 __global__ void __launch_bounds__(64) ssd_cb_kernel(const uint16_t* __restrict__ Bm,
                                                     const uint16_t* __restrict__ Cm,
@@ -82,6 +85,7 @@ __global__ void __launch_bounds__(64) ssd_cb_kernel(const uint16_t* __restrict__
                                                     int L, int Q, int N) {
   const int bcg = blockIdx.x;                  // (b*nc + c)*G + g
   const int it = blockIdx.y;                   // 16-row band of i
+  const int jt0 = kCbTiles * blockIdx.z;       // first 16-column tile of j
   const int lane = threadIdx.x, r = lane & 15, gq = lane >> 4;
   const int g = bcg % G, c = (bcg / G) % nc, b = bcg / (G * nc);
   const int64_t rowbase = ((int64_t)(b * G + g) * L + (int64_t)c * Q);
@@ -90,35 +94,40 @@ __global__ void __launch_bounds__(64) ssd_cb_kernel(const uint16_t* __restrict__
   uint16_t* out = cb + (int64_t)bcg * Q * Q;
   const int i0 = 16 * it;
   const int nks = (N + 31) / 32;
-  // C^T operand: lane holds C[i0 + r][32 ks + 8 gq .. + 7] (zero past N)
-  u32x4_t cf[4];
+  const int njt = min(kCbTiles, Q / 16 - jt0);
+  // every operand load is issued before the first MFMA: one memory latency
+  // per wave.  C^T operand: lane holds C[i0 + r][32 ks + 8 gq .. + 7], B
+  // operand of tile j: B[16 (jt0 + j) + r][same n] (zero past N; tiles
+  // above the diagonal are not loaded)
+  u32x4_t cf[4], bf[kCbTiles][4];
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) {
     const int n = 32 * ks + 8 * gq;
-    cf[ks] = (ks < nks && n < N) ? *reinterpret_cast<const u32x4_t*>(Cc + (int64_t)(i0 + r) * N + n)
-                                 : u32x4_t{0u, 0u, 0u, 0u};
+    const bool live = ks < nks && n < N && jt0 <= it;
+    cf[ks] = live ? *reinterpret_cast<const u32x4_t*>(Cc + (int64_t)(i0 + r) * N + n)
+                  : u32x4_t{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int j = 0; j < kCbTiles; ++j)
+      bf[j][ks] = live && j < njt && jt0 + j <= it
+                      ? *reinterpret_cast<const u32x4_t*>(Bc + (int64_t)(16 * (jt0 + j) + r) * N + n)
+                      : u32x4_t{0u, 0u, 0u, 0u};
   }
-  for (int jt = 0; jt < Q / 16; ++jt) {
+#pragma unroll
+  for (int j = 0; j < kCbTiles; ++j) {
+    if (j >= njt) continue;
+    const int jt = jt0 + j;
     uint16_t* orow = out + (int64_t)(i0 + r) * Q + 16 * jt + 4 * gq;
-    if (jt > it) {
-      *reinterpret_cast<u32x2_t*>(orow) = u32x2_t{0u, 0u};
-      continue;
-    }
     f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    if (jt <= it) {
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      if (ks < nks) {
-        const int n = 32 * ks + 8 * gq;
-        const u32x4_t bf = n < N ? *reinterpret_cast<const u32x4_t*>(Bc + (int64_t)(16 * jt + r) * N + n)
-                                 : u32x4_t{0u, 0u, 0u, 0u};
-        acc = mfma16t<F16>(bf, cf[ks], acc);  // D[j][i] = sum_n B[j][n] C[i][n]
+      for (int ks = 0; ks < 4; ++ks)
+        if (ks < nks) acc = mfma16t<F16>(bf[j][ks], cf[ks], acc);  // D[j][i] = sum_n B[j][n] C[i][n]
+      // lane holds cb[i0 + r][16 jt + 4 gq + e]; the diagonal tile keeps j <= i
+      if (jt == it) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (4 * gq + e > r) acc[e] = 0.f;
       }
-    }
-    // lane holds cb[i0 + r][16 jt + 4 gq + e]
-    if (jt == it) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        if (4 * gq + e > r) acc[e] = 0.f;
     }
     *reinterpret_cast<u32x2_t*>(orow) =
         u32x2_t{pack2<F16>(acc[0], acc[1]), pack2<F16>(acc[2], acc[3])};
@@ -471,7 +480,9 @@ int bmm_chunk_impl(const void* B, const void* C, void* cb, int64_t batch, int64_
   if (!aligned16(B) || !aligned16(C) || (reinterpret_cast<uintptr_t>(cb) & 7u))
     return loom_fail(err, errlen, LOOM_EINVAL, "ssd_bmm_chunk: B, C 16-byte and cb 8-byte aligned");
   if (loom_validate_only()) return loom_ok(err, errlen);
-  hipLaunchKernelGGL(ssd_cb_kernel<F16>, dim3((unsigned)(batch * nchunks * ngroups), (unsigned)(chunk_size / 16)),
+  hipLaunchKernelGGL(ssd_cb_kernel<F16>,
+                     dim3((unsigned)(batch * nchunks * ngroups), (unsigned)(chunk_size / 16),
+                          (unsigned)((chunk_size / 16 + kCbTiles - 1) / kCbTiles)),
                      dim3(64), 0, static_cast<hipStream_t>(stream),
                      static_cast<const uint16_t*>(B), static_cast<const uint16_t*>(C),
                      static_cast<uint16_t*>(cb), (int)nchunks, (int)ngroups,
