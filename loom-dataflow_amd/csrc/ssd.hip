@@ -139,7 +139,7 @@ __global__ void __launch_bounds__(64) ssd_cb_kernel(const uint16_t* __restrict__
 // ---------------------------------------------------------------------------
 constexpr int kSsdQmax = 256, kSsdPmax = 256, kSsdNB = 64, kSsdWaves = 8;
 constexpr int kSsdStageMax = 36 * 1024;      // bytes per pipeline stage
-constexpr int kSsdRing = 4 * kSsdStageMax;   // LDS for the stage ring
+constexpr int kSsdRing = 136 * 1024;         // LDS for the stage ring (four 34 KB stages)
 constexpr int kSsdNSMax = 8;                 // stages at most
 constexpr int kSsdMaxLpw = 5;                // DMA copies per wave per unit at most
 
@@ -160,12 +160,19 @@ struct SsdStateParams {
   int ns;                    // stages in the ring (3 .. 8)
 };
 
-// SHARED_PT: P / 16 divides the wave count, so all tiles of a wave share
-// one p tile and the w-scaled x operand is built once per k step.
-template <int TPW, bool SHARED_PT, bool F16>
+// MODE 0: tile t of wave w is w + 8 t, each with its own p tile.
+// MODE 1: P / 16 divides the wave count, so all tiles of a wave share one p
+//         tile and the w-scaled x operand is built once per k step.
+// MODE 2: P / 16 is half the wave count: waves w and w + P/16 own the same
+//         tiles (p tile w % (P/16), every n tile) and split the k steps
+//         between them (even / odd), so each scaled x operand is built once
+//         per workgroup; at each chunk start the odd wave hands its partial
+//         sums to the even wave through LDS, which stores prev(c).
+template <int TPW, int MODE, bool F16>
 __global__ void __launch_bounds__(64 * kSsdWaves) ssd_state_kernel(SsdStateParams p) {
   __shared__ __attribute__((aligned(1024))) char smem[kSsdRing];
   __shared__ __attribute__((aligned(16))) float s_w[kSsdWaves][128];
+  __shared__ f32x4_t s_x[MODE == 2 ? (kSsdWaves / 2) * TPW * 64 : 1];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = lane & 15, gq = lane >> 4, a4 = r >> 2, c4 = r & 3;
@@ -265,7 +272,11 @@ __global__ void __launch_bounds__(64 * kSsdWaves) ssd_state_kernel(SsdStateParam
   f32x4_t R[TPW];
 #pragma unroll
   for (int t = 0; t < TPW; ++t) R[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  const int nst = min(TPW, max(0, (tiles - wave + kSsdWaves - 1) / kSsdWaves));  // tiles of this wave
+  // kq: this wave's k-step parity (MODE 2); ntw: tiles it accumulates; nst:
+  // prev stores it issues per chunk
+  const int kq = MODE == 2 ? wave / ptiles : 0;
+  const int ntw = MODE == 2 ? TPW : min(TPW, max(0, (tiles - wave + kSsdWaves - 1) / kSsdWaves));
+  const int nst = MODE == 2 ? (kq == 0 ? TPW : 0) : ntw;
   // w_c[k] = exp(dA[c, Q-1] - dA[c, k]) dt[c, k] of the current unit (zero
   // past its QS keys), one copy per wave in s_w[wave]: a wave writes and
   // reads only its own row, so no barrier is involved.  dAs: the stage's dA
@@ -310,7 +321,7 @@ __global__ void __launch_bounds__(64 * kSsdWaves) ssd_state_kernel(SsdStateParam
     o.w1 = *reinterpret_cast<const f32x4_t*>(sw + k0 + 16);
 #pragma unroll
     for (int t = 0; t < TPW; ++t) {
-      const int nt = min(wave + kSsdWaves * t, tiles - 1) / ptiles;
+      const int nt = MODE == 2 ? t : min(wave + kSsdWaves * t, tiles - 1) / ptiles;
       const lds_char_t* qb = bs + (k0 + a4) * BR + (2 * nt + (c4 >> 1)) * 16 + (c4 & 1) * 8;
       o.b0[t] = lds_read_tr16(qb);
       o.b1[t] = lds_read_tr16(qb + 16 * BR);
@@ -332,39 +343,63 @@ __global__ void __launch_bounds__(64 * kSsdWaves) ssd_state_kernel(SsdStateParam
       // prev(c) out, then R = exp(dA[c, Q-1]) R; states(c) accumulate below
       const float decay = fast_exp2(dAs[256 + 3] * 1.4426950408889634f);
       float* outc = p.prevT + (((int64_t)(b * nc + c) * H + h) * N + n0) * P;
+      if constexpr (MODE == 2) {
+        const int pt = wave % ptiles;
+        f32x4_t* xch = s_x + pt * TPW * 64 + lane;
+        if (kq == 1) {
 #pragma unroll
-      for (int t = 0; t < TPW; ++t) {
-        const int tt = wave + kSsdWaves * t;
-        if (tt < tiles) {
-          const int pt = tt % ptiles, nt = tt / ptiles;
-          *reinterpret_cast<f32x4_t*>(outc + (int64_t)(16 * nt + r) * P + 16 * pt + 4 * gq) = R[t];
-          R[t] *= decay;
+          for (int t = 0; t < TPW; ++t) xch[t * 64] = R[t];
+        }
+        LOOM_WAIT_LGKM0();
+        barrier_nofence();
+        if (kq == 0) {
+#pragma unroll
+          for (int t = 0; t < TPW; ++t)
+            *reinterpret_cast<f32x4_t*>(outc + (int64_t)(16 * t + r) * P + 16 * pt + 4 * gq) =
+                R[t] + xch[t * 64];
+        }
+#pragma unroll
+        for (int t = 0; t < TPW; ++t) R[t] *= decay;
+      } else {
+#pragma unroll
+        for (int t = 0; t < TPW; ++t) {
+          const int tt = wave + kSsdWaves * t;
+          if (tt < tiles) {
+            const int pt = tt % ptiles, nt = tt / ptiles;
+            *reinterpret_cast<f32x4_t*>(outc + (int64_t)(16 * nt + r) * P + 16 * pt + 4 * gq) = R[t];
+            R[t] *= decay;
+          }
         }
       }
     }
     const int nks = QSP / 32;
-    if constexpr (SHARED_PT) {
+    if constexpr (MODE >= 1) {
       // all tiles of the wave share p tile wave % ptiles: one scaled x
-      // operand per step; the next step's operands are read while this
-      // step's MFMAs run
+      // operand per step (MODE 2: every other step); the next step's
+      // operands are read while this step's MFMAs run
+      constexpr int KSTEP = MODE == 2 ? 2 : 1;
       const int ptw = wave % ptiles;
-      Ops cur;
-      load_ops(xs, bs, 0, ptw, cur);
-      for (int ks = 0; ks < nks; ++ks) {
-        Ops nxt;
-        load_ops(xs, bs, min(ks + 1, nks - 1), ptw, nxt);
-        u32x4_t xh, xl;
-        scale_x(cur.x0, cur.x1, cur.w0, cur.w1, xh, xl);
+      if (kq < nks) {
+        Ops cur;
+        load_ops(xs, bs, kq, ptw, cur);
+        for (int ks = kq; ks < nks; ks += KSTEP) {
+          Ops nxt;
+          load_ops(xs, bs, ks + KSTEP < nks ? ks + KSTEP : ks, ptw, nxt);
+          u32x4_t xh, xl;
+          scale_x(cur.x0, cur.x1, cur.w0, cur.w1, xh, xl);
 #pragma unroll
-        for (int t = 0; t < TPW; ++t) {
-          if (t < nst) {
-            const u32x4_t bf = u32x4_t{cur.b0[t][0], cur.b0[t][1], cur.b1[t][0], cur.b1[t][1]};
-            R[t] = mfma16t<F16>(xh, bf, R[t]);
-            R[t] = mfma16t<F16>(xl, bf, R[t]);
+          for (int t = 0; t < TPW; ++t) {
+            if (t < ntw) {
+              const u32x4_t bf = u32x4_t{cur.b0[t][0], cur.b0[t][1], cur.b1[t][0], cur.b1[t][1]};
+              R[t] = mfma16t<F16>(xh, bf, R[t]);
+              R[t] = mfma16t<F16>(xl, bf, R[t]);
+            }
           }
+          if (ks == kq && pre) issue(sn, un, 0, half);
+          cur = nxt;
         }
-        if (ks == 0 && pre) issue(sn, un, 0, half);
-        cur = nxt;
+      } else if (pre) {
+        issue(sn, un, 0, half);
       }
       if (pre) issue(sn, un, half, nlw);
     } else {
@@ -410,14 +445,14 @@ __global__ void __launch_bounds__(64 * kSsdWaves) ssd_state_kernel(SsdStateParam
 }
 
 template <int TPW, bool F16>
-void launch_state(const SsdStateParams& p, int grid_x, int grid_y, hipStream_t st) {
-  const int ptiles = p.P / 16;
-  if (kSsdWaves % ptiles == 0)
-    hipLaunchKernelGGL((ssd_state_kernel<TPW, true, F16>), dim3((unsigned)grid_x, (unsigned)grid_y),
-                       dim3(64 * kSsdWaves), 0, st, p);
+void launch_state(const SsdStateParams& p, int mode, int grid_x, int grid_y, hipStream_t st) {
+  const dim3 grid((unsigned)grid_x, (unsigned)grid_y), block(64 * kSsdWaves);
+  if (mode == 2)
+    hipLaunchKernelGGL((ssd_state_kernel<TPW, 2, F16>), grid, block, 0, st, p);
+  else if (mode == 1)
+    hipLaunchKernelGGL((ssd_state_kernel<TPW, 1, F16>), grid, block, 0, st, p);
   else
-    hipLaunchKernelGGL((ssd_state_kernel<TPW, false, F16>), dim3((unsigned)grid_x, (unsigned)grid_y),
-                       dim3(64 * kSsdWaves), 0, st, p);
+    hipLaunchKernelGGL((ssd_state_kernel<TPW, 0, F16>), grid, block, 0, st, p);
 }
 
 int check_ssd(const char* fn, int64_t batch, int64_t nchunks, int64_t nheads, int64_t ngroups,
@@ -505,8 +540,10 @@ int state_passing_impl(const void* x, const void* dt, const void* dA_cumsum,
     return loom_fail(err, errlen, LOOM_EINVAL, "ssd_chunk_state_passing: tensors must be 16-byte aligned");
   // n block: 64 wide while the P x 64 block fits four tiles per wave, else 32
   const int nb = (int)std::min<int64_t>(dstate, headdim <= 128 ? kSsdNB : 32);
-  const int tiles = (int)(headdim / 16) * (nb / 16);
-  const int tpw = (tiles + kSsdWaves - 1) / kSsdWaves;
+  const int ptiles = (int)(headdim / 16), tiles = ptiles * (nb / 16);
+  // kernel mode (see ssd_state_kernel) and tiles per wave
+  const int mode = kSsdWaves % ptiles ? 0 : (2 * ptiles == kSsdWaves ? 2 : 1);
+  const int tpw = mode == 2 ? nb / 16 : (tiles + kSsdWaves - 1) / kSsdWaves;
   if (dstate % nb != 0 || tpw > 4)
     return loom_fail(err, errlen, LOOM_EUNSUP,
                      "ssd_chunk_state_passing: dstate %lld with headdim %lld not built",
@@ -555,9 +592,9 @@ int state_passing_impl(const void* x, const void* dt, const void* dA_cumsum,
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int gx = (int)(batch * nheads), gy = (int)(dstate / nb);
   if (loom_validate_only()) return loom_ok(err, errlen);
-  if (tpw <= 1) launch_state<1, F16>(p, gx, gy, st);
-  else if (tpw <= 2) launch_state<2, F16>(p, gx, gy, st);
-  else launch_state<4, F16>(p, gx, gy, st);
+  if (tpw <= 1) launch_state<1, F16>(p, mode, gx, gy, st);
+  else if (tpw <= 2) launch_state<2, F16>(p, mode, gx, gy, st);
+  else launch_state<4, F16>(p, mode, gx, gy, st);
   return loom_check_launch(err, errlen, "ssd_chunk_state_passing");
 }
 
