@@ -267,7 +267,9 @@ __global__ void __launch_bounds__(64 * kSsdWaves) ssd_state_kernel(SsdStateParam
     }
   };
 
-  // running prev_states^T tiles: tile t = wave + 8 u -> (pt, nt); lane holds
+  // running prev_states^T tiles: R[t] is tile (pt, nt) = ((w + 8 t) % ptiles,
+  // (w + 8 t) / ptiles) in MODES 0 and 1, (w % ptiles, t) in MODE 2 (there a
+  // partial sum over half the k steps); lane holds
   // prev[n0 + 16 nt + r][16 pt + 4 gq + e]
   f32x4_t R[TPW];
 #pragma unroll
