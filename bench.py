@@ -51,7 +51,8 @@ def parse():
     ap.add_argument("--iters", type=int, default=20, help="timed calls per kernel in the table")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only run the workload profiled for roofline.traffic: a 256 MiB "
-                         "device copy (the calibration kernel) and three headline bmm launches")
+                         "device copy (the calibration kernel), three headline bmm launches "
+                         "and three split-K launches (cache flushed before each)")
     return ap.parse_args()
 
 
@@ -332,6 +333,15 @@ def main():
         out = torch.empty(16, 2048, 2048, dtype=torch.bfloat16, device="cuda")
         for _ in range(3):
             lh.batch_matmul(a0, a1, out, tile_m=256, tile_n=256)
+        del a0, a1, out
+        sa = (torch.randn(512, 16384, device="cuda") * 0.02).to(torch.bfloat16)
+        sb = (torch.randn(16384, 512, device="cuda") * 0.02).to(torch.bfloat16)
+        so = torch.empty(512, 512, dtype=torch.bfloat16, device="cuda")
+        sg = torch.empty(16, 512, 512, dtype=torch.float32, device="cuda")
+        flush = torch.empty(512 << 20, dtype=torch.uint8, device="cuda")
+        for _ in range(3):
+            flush.zero_()  # larger than the Infinity Cache: operands come from HBM
+            lh.split_k_matmul_gather(sa, sb, so, sg, tile_m=128, tile_n=128, tile_k=1024)
         torch.cuda.synchronize()
         print("traffic probe done", file=sys.stderr, flush=True)
         return
