@@ -100,6 +100,16 @@ def test_ragged_chunk_and_narrow_state(lh):
     _check_prologue(lh, x, dt, A, Bm, C, 48, "ragged")
 
 
+@pytest.mark.parametrize("Q,N", [(48, 32), (32, 64), (128, 128)])
+def test_paired_k_split_shapes(lh, Q, N):
+    """P = 64: two waves per p tile split the k steps.  Q = 48 is one ragged
+    unit of two steps, Q = 32 leaves the odd waves without a step (their
+    partial sums stay zero), Q = 128 is one full unit per chunk."""
+    rng = np.random.default_rng(45 + Q)
+    x, dt, A, Bm, C = _raw_inputs(rng, 1, 4, 2, 3 * Q, 64, N)
+    _check_prologue(lh, x, dt, A, Bm, C, Q, f"paired Q{Q} N{N}")
+
+
 def test_zero_B_gives_zero_states(lh):
     rng = np.random.default_rng(44)
     x, dt, A, Bm, C = _raw_inputs(rng, 1, 2, 1, 4 * 64, 32, 64)
