@@ -1003,27 +1003,23 @@ __global__ void __launch_bounds__(256) splitk_reduce_vec4(const float* __restric
   for (int64_t q = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; q < n4;
        q += (int64_t)gridDim.x * blockDim.x) {
     f32x4_t s = *reinterpret_cast<const f32x4_t*>(G + q * 4);
-    // eight slabs' loads in flight at a time; the adds stay in ascending s
-    int k = 1;
-    for (; k + 8 <= S; k += 8) {
-      f32x4_t v[8];
+    // sixteen slabs' loads in flight at a time (a short last group re-reads
+    // slab S-1 in the unused slots), so 17 slabs cost one memory latency;
+    // the adds stay in ascending s
+    for (int k = 1; k < S; k += 16) {
+      f32x4_t v[16];
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
-        v[j] = *reinterpret_cast<const f32x4_t*>(G + (int64_t)(k + j) * MN + q * 4);
+      for (int j = 0; j < 16; ++j)
+        v[j] = *reinterpret_cast<const f32x4_t*>(G + (int64_t)min(k + j, S - 1) * MN + q * 4);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        s[0] += v[j][0];
-        s[1] += v[j][1];
-        s[2] += v[j][2];
-        s[3] += v[j][3];
+      for (int j = 0; j < 16; ++j) {
+        if (k + j < S) {
+          s[0] += v[j][0];
+          s[1] += v[j][1];
+          s[2] += v[j][2];
+          s[3] += v[j][3];
+        }
       }
-    }
-    for (; k < S; ++k) {
-      const f32x4_t v = *reinterpret_cast<const f32x4_t*>(G + (int64_t)k * MN + q * 4);
-      s[0] += v[0];
-      s[1] += v[1];
-      s[2] += v[2];
-      s[3] += v[3];
     }
     u32x2_t o{pack2<H>(s[0], s[1]), pack2<H>(s[2], s[3])};
     *reinterpret_cast<u32x2_t*>(out + q * 4) = o;
