@@ -8,7 +8,13 @@
  * tensors hold raw bf16 bits, fp32 tensors IEEE floats.  Extents are explicit.
  * The tile_* arguments are the loom.sym block sizes the staged-ETG solver
  * binds (the `__tile_*` suffix of a materialized variant); each entry point
- * validates them and documents how it maps them onto the GPU.
+ * validates them and documents how it maps them onto the GPU.  As in the
+ * reference, every tile is bounded by the extent of the loop it tiles (the
+ * symbol's upper_bound, exported as natural_ub by
+ * lib/passes/lcs/src/staged_etg_builder.cpp:1420-1430): a larger value is
+ * rejected with LOOM_HIP_EINVAL.  Where a kernel builds a fixed set of
+ * workgroup tiles, a value equal to a whole extent below those tiles is also
+ * accepted and runs as the smallest built tile covering the extent.
  *
  * Conventions shared by every entry point:
  *   - `stream` is a hipStream_t (NULL = the default stream); work is only
@@ -62,17 +68,19 @@ const char* loom_hip_version(void);
  *   (x: memref<MxK>, y: memref<KxN>, out: memref<MxN>)
  * out = x . y, bf16 in, fp32 accumulate, bf16 out.
  * (tile_m, tile_n) is the workgroup output tile: (64,64), (128,128) or
- * (256,256).  tile_k is the K step of the reference loop; any value >= 1 is
- * accepted and the kernel stages K in 64-deep LDS tiles (the result does not
- * depend on it). */
+ * (256,256), tile_m <= M and tile_n <= N (tile_m = M or tile_n = N below the
+ * tile names it on that axis).  tile_k (1 <= tile_k <= K) is the K step of
+ * the reference loop; the kernel stages K in its own LDS steps (the result
+ * does not depend on it). */
 int loom_hip_matmul(const void* x, const void* y, void* out, int64_t M, int64_t N, int64_t K,
                     int64_t tile_m, int64_t tile_n, int64_t tile_k, void* stream, char* err,
                     size_t errlen);
 
 /* @batch_matmul -- examples/bmm_2Dmesh/IR/00_from_helion_frontend.mlir:4
  *   (arg0: memref<BxMxK>, arg1: memref<BxKxN>, arg2: memref<BxMxN>)
- * arg2[b] = arg0[b] . arg1[b].  Tiles as for loom_hip_matmul; tile_b >= 1
- * groups batches in the reference grid and does not change the result. */
+ * arg2[b] = arg0[b] . arg1[b].  Tiles as for loom_hip_matmul; tile_b
+ * (1 <= tile_b <= B) groups batches in the reference grid and does not
+ * change the result. */
 int loom_hip_batch_matmul(const void* arg0, const void* arg1, void* arg2, int64_t B, int64_t M,
                           int64_t N, int64_t K, int64_t tile_b, int64_t tile_m, int64_t tile_n,
                           int64_t tile_k, void* stream, char* err, size_t errlen);
@@ -98,9 +106,10 @@ int loom_hip_split_k_matmul_gather(const void* a, const void* b, void* out, void
  * Flash-attention forward with online softmax; `scale` multiplies q.k (the
  * reference hard-codes the f16 constant 0.08837890625 at :10); `causal`
  * (not in the reference; needs Sq == Skv) hides key j from query i < j.
- * tile_m (64, 128, 192 or 256) is the workgroup's query tile; tile_b (<= BH)
- * and tile_n (<= Skv, the online-softmax step) are validated, the kernel
- * streams KV in 64-key LDS blocks.  D = 64 or 128, Skv a multiple of 8. */
+ * tile_m (64, 128, 192 or 256, at most Sq; or Sq itself below 256) is the
+ * workgroup's query tile; tile_b (<= BH) and tile_n (<= Skv, the
+ * online-softmax step) are validated, the kernel streams KV in 64-key LDS
+ * blocks.  D = 64 or 128, Skv a multiple of 8. */
 int loom_hip_attention(const void* k, const void* v, const void* q, void* out, int64_t BH,
                        int64_t Sq, int64_t Skv, int64_t D, float scale, int causal,
                        int64_t tile_b, int64_t tile_m, int64_t tile_n, void* stream, char* err,
@@ -119,7 +128,8 @@ size_t loom_hip_flash_decode_workspace_bytes(int64_t B, int64_t H, int64_t D, in
  * [s*tile_s, (s+1)*tile_s); its (lse_s, o_s) land in the workspace, then a
  * second kernel performs the split-0 combine into out.  tile_b (<= B) and
  * tile_n (<= S) are validated and do not change the result.  D = 64 or 128,
- * H <= 32. */
+ * H <= 32.  scale must be finite and positive (the running max is taken
+ * over raw scores before scaling). */
 int loom_hip_flash_decode(const void* k, const void* v, const void* q, void* out,
                           void* workspace, size_t workspace_bytes, int64_t B, int64_t H,
                           int64_t D, int64_t S, float scale, int64_t tile_b, int64_t tile_s,
@@ -131,9 +141,10 @@ int loom_hip_flash_decode(const void* k, const void* v, const void* q, void* out
  *    prev_states_T: [b,c,H,N,P] fp32, out: [b,H,L,P] bf16), L = c*Q.
  * Mamba-2 SSD chunk scan with the intra-chunk causal mask k <= m.
  * tile_b = tile_h = tile_c = 1 (the reference's size-1 subviews skip work
- * otherwise); tile_m in {64,128,192,256} rows and tile_n in {16,32,64}
- * columns form the workgroup tile; tile_k >= 1 is the reference's k step and
- * does not change the result.  Q <= 256, N <= 128, Q, N, P multiples of 8. */
+ * otherwise); tile_m in {64,128,192,256} rows (<= Q, or Q itself) and
+ * tile_n in {16,32,64} columns (<= P, or P itself) form the workgroup tile;
+ * tile_k (1 <= tile_k <= Q) is the reference's k step and does not change
+ * the result.  Q <= 256, N <= 128, Q, N, P multiples of 8. */
 int loom_hip_helion_mamba2_chunk_scan_kernel(
     const void* cb, const void* x, const void* dt, const void* dA_cumsum, const void* C,
     const void* D, const void* prev_states_T, void* out, int64_t batch, int64_t nchunks,
@@ -147,8 +158,11 @@ int loom_hip_helion_mamba2_chunk_scan_kernel(
  * 16-bit tensor (inputs and outputs alike) in IEEE binary16 instead: same
  * arguments, tiles, workspaces, validation and return codes; MFMAs run on
  * f16 operands (v_mfma_f32_16x16x32_f16) with fp32 accumulation, and every
- * rounding to f16 is to nearest even.  fp32 tensors (dt, dA_cumsum, D,
- * prev_states_T, partials) stay fp32. */
+ * rounding to f16 is to nearest even.  The split-K partials and the decode
+ * workspace stay fp32.  loom_hip_helion_mamba2_chunk_scan_kernel_f16 takes
+ * the reference's exact signature: every tensor f16, dt, dA_cumsum, D and
+ * prev_states_T included (examples/mamba_chunk_scan/IR/
+ * 00_from_helion_frontend.mlir:4; widened to fp32 exactly on load). */
 int loom_hip_matmul_f16(const void* x, const void* y, void* out, int64_t M, int64_t N, int64_t K,
                         int64_t tile_m, int64_t tile_n, int64_t tile_k, void* stream, char* err,
                         size_t errlen);
@@ -184,9 +198,10 @@ int loom_hip_helion_mamba2_chunk_scan_kernel_f16(
  * softplus; the same memory as chunk_scan's dt [b,H,c,Q]), A [H] fp32,
  * B and C [b,G,L,N] bf16, L = nchunks * chunk_size, head h reads group
  * h / (H / G).  chunk_size, headdim and dstate are multiples of 16,
- * chunk_size <= 256, headdim <= 256, dstate <= 128 (a multiple of 32 above
- * 32; of 64 above 64 when headdim <= 128), and
- * ceil32(chunk_size) * headdim * 2 <= 64 KiB. */
+ * chunk_size <= 256 (a multiple of 32 from 128 up), headdim <= 256,
+ * dstate <= 128 (a multiple of 32 above 32; of 64 above 64 when
+ * headdim <= 128), and ceil32(chunk_size) * headdim * 2 <= 64 KiB.  The
+ * dt, dA_cumsum and prev_states_T of these stages are fp32 in both forms. */
 
 /* dA_cumsum[b,h,c,q] = sum_{q' <= q} dt[b,h,c*Q+q'] * A[h] (fp32; a wave
  * prefix scan, so the summation order differs from a serial loop). */
@@ -208,7 +223,9 @@ int loom_hip_ssd_chunk_state_passing(const void* x, const void* dt, const void* 
                                      int64_t chunk_size, int64_t headdim, int64_t dstate,
                                      void* stream, char* err, size_t errlen);
 
-/* All three stages in stream order: dA_cumsum, cb, prev_states_T. */
+/* All three stages in stream order: dA_cumsum, cb, prev_states_T.  Every
+ * stage's checks run before the first launch: a rejected call enqueues
+ * nothing. */
 int loom_hip_ssd_prologue(const void* x, const void* dt, const void* A, const void* B,
                           const void* C, void* dA_cumsum, void* cb, void* prev_states_T,
                           int64_t batch, int64_t nchunks, int64_t nheads, int64_t ngroups,

@@ -489,11 +489,6 @@ std::string jlist(const char* op, const std::vector<std::string>& xs) {
 std::string jrange(const char* sym, long long lo, long long hi) {
   return std::string("{\"InRange\":{\"x\":") + js(sym) + ",\"lo\":" + jc(lo) + ",\"hi\":" + jc(hi) + "}}";
 }
-std::string jin(const char* sym, std::initializer_list<long long> vals) {
-  std::vector<std::string> alts;
-  for (long long v : vals) alts.push_back(jop("Eq", js(sym), jc(v)));
-  return jlist("Or", alts);
-}
 std::string jsym(const char* name, long long ub, long long align) {
   return std::string("\"") + name + "\":{\"type\":\"int\",\"natural_ub\":" + std::to_string(ub) +
          ",\"alignment\":" + std::to_string(align) + "}";
@@ -519,13 +514,48 @@ int build_scope(const std::string& f, const int64_t* d, int nd, Scope& sc, std::
       }
     return true;
   };
-  // the GEMM tile pairs; both LDS-staged kernels hold 256 (tile_m + tile_n) bytes
+  // Every symbol lies in [1, natural_ub] (the extent of the loop it tiles,
+  // staged_etg_builder.cpp:1420-1430).  A tiled axis takes one of the built
+  // workgroup tiles up to its extent, or the extent itself when it is below a
+  // built tile (it then runs as the smallest built tile covering it; see
+  // loom_fit_tile in csrc/common.h).
+  auto ub = [&](const char* sym, long long extent) { sc.hard.push_back(jrange(sym, 1, extent)); };
+  auto cover = [](long long extent, std::initializer_list<long long> built) {
+    for (long long t : built)
+      if (t >= extent) return t;
+    return -1LL;
+  };
+  // the values of `sym` that run as workgroup tile T along an axis of `extent`
+  auto runs_as = [&](const char* sym, long long extent, long long T,
+                     std::initializer_list<long long> built) {
+    std::vector<std::string> alts;
+    if (T <= extent) alts.push_back(jop("Eq", js(sym), jc(T)));
+    else if (cover(extent, built) == T) alts.push_back(jop("Eq", js(sym), jc(extent)));
+    return alts;
+  };
+  auto tile_choice = [&](const char* sym, long long extent, std::initializer_list<long long> built) {
+    std::vector<std::string> alts;
+    for (long long T : built) {
+      auto a = runs_as(sym, extent, T, built);
+      alts.insert(alts.end(), a.begin(), a.end());
+    }
+    sc.hard.push_back(jlist("Or", alts));
+  };
+  // the GEMM tile pairs (square workgroup tiles); both LDS-staged kernels
+  // hold 256 (tile_m + tile_n) bytes
   auto gemm_tiles = [&](long long M, long long N) {
     sc.symbols.push_back(jsym("tile_m", M, 64));
     sc.symbols.push_back(jsym("tile_n", N, 64));
-    sc.hard.push_back(jlist("Or", {jlist("And", {jop("Eq", js("tile_m"), jc(64)), jop("Eq", js("tile_n"), jc(64))}),
-                                   jlist("And", {jop("Eq", js("tile_m"), jc(128)), jop("Eq", js("tile_n"), jc(128))}),
-                                   jlist("And", {jop("Eq", js("tile_m"), jc(256)), jop("Eq", js("tile_n"), jc(256))})}));
+    ub("tile_m", M);
+    ub("tile_n", N);
+    std::vector<std::string> pairs;
+    for (long long T : {64LL, 128LL, 256LL}) {
+      auto am = runs_as("tile_m", M, T, {64, 128, 256});
+      auto an = runs_as("tile_n", N, T, {64, 128, 256});
+      if (am.empty() || an.empty()) continue;
+      pairs.push_back(jlist("And", {jlist("Or", am), jlist("Or", an)}));
+    }
+    sc.hard.push_back(jlist("Or", pairs));
     sc.footprint.push_back(jop("Mul", jc(256), js("tile_m")));
     sc.footprint.push_back(jop("Mul", jc(256), js("tile_n")));
     sc.hard.push_back(jop("Le", jop("Add", sc.footprint[0], sc.footprint[1]), jc(kLdsBytes)));
@@ -536,22 +566,22 @@ int build_scope(const std::string& f, const int64_t* d, int nd, Scope& sc, std::
     if (!need(3)) return LOOM_HIP_EINVAL;
     gemm_tiles(d[0], d[1]);
     sc.symbols.push_back(jsym("tile_k", d[2], 1));
-    sc.hard.push_back(jop("Ge", js("tile_k"), jc(1)));
+    ub("tile_k", d[2]);
     sc.seq_iter = jop("Div", jc(d[2]), js("tile_k"));
   } else if (f == "batch_matmul") {
     if (!need(4)) return LOOM_HIP_EINVAL;
     sc.symbols.push_back(jsym("tile_b", d[0], 1));
-    sc.hard.push_back(jop("Ge", js("tile_b"), jc(1)));
+    ub("tile_b", d[0]);
     gemm_tiles(d[1], d[2]);
     sc.symbols.push_back(jsym("tile_k", d[3], 1));
-    sc.hard.push_back(jop("Ge", js("tile_k"), jc(1)));
+    ub("tile_k", d[3]);
     sc.temp_iter.insert(sc.temp_iter.begin(), jop("Div", jc(d[0]), js("tile_b")));
     sc.seq_iter = jop("Div", jc(d[3]), js("tile_k"));
   } else if (f == "split_k_matmul_gather") {
     if (!need(3)) return LOOM_HIP_EINVAL;
     gemm_tiles(d[0], d[1]);
     sc.symbols.push_back(jsym("tile_k", d[2], 1));
-    sc.hard.push_back(jrange("tile_k", 1, d[2]));
+    ub("tile_k", d[2]);
     sc.temp_iter.push_back(jop("Div", jc(d[2]), js("tile_k")));
   } else if (f == "attention") {
     if (!need(4)) return LOOM_HIP_EINVAL;
@@ -562,9 +592,10 @@ int build_scope(const std::string& f, const int64_t* d, int nd, Scope& sc, std::
     sc.symbols.push_back(jsym("tile_b", d[0], 1));
     sc.symbols.push_back(jsym("tile_m", d[1], 64));
     sc.symbols.push_back(jsym("tile_n", d[2], 1));
-    sc.hard.push_back(jrange("tile_b", 1, d[0]));
-    sc.hard.push_back(jin("tile_m", {64, 128, 192, 256}));
-    sc.hard.push_back(jrange("tile_n", 1, d[2]));
+    ub("tile_b", d[0]);
+    ub("tile_m", d[1]);
+    tile_choice("tile_m", d[1], {64, 128, 192, 256});
+    ub("tile_n", d[2]);
     // four stages of 64-key K and V blocks
     sc.footprint.push_back(jc(4 * 64 * d[3] * 2));
     sc.footprint.push_back(jc(4 * 64 * d[3] * 2));
@@ -600,12 +631,19 @@ int build_scope(const std::string& f, const int64_t* d, int nd, Scope& sc, std::
     sc.symbols.push_back(jsym("tile_c", d[1], 1));
     sc.symbols.push_back(jsym("tile_b", d[0], 1));
     sc.symbols.push_back(jsym("tile_h", d[2], 1));
+    ub("tile_b", d[0]);
+    ub("tile_h", d[2]);
+    ub("tile_c", d[1]);
     sc.hard.push_back(jop("Eq", js("tile_b"), jc(1)));
     sc.hard.push_back(jop("Eq", js("tile_h"), jc(1)));
     sc.hard.push_back(jop("Eq", js("tile_c"), jc(1)));
-    sc.hard.push_back(jin("tile_m", {64, 128, 192, 256}));
-    sc.hard.push_back(jin("tile_n", {16, 32, 64}));
-    sc.hard.push_back(jop("Ge", js("tile_k"), jc(1)));
+    ub("tile_m", d[4]);
+    tile_choice("tile_m", d[4], {64, 128, 192, 256});
+    ub("tile_n", d[5]);
+    tile_choice("tile_n", d[5], {16, 32, 64});
+    // tile_k tiles the keys of one chunk (the example's loom.sym bound, 8192
+    // at :1, is looser than the chunk it indexes)
+    ub("tile_k", d[4]);
     sc.temp_iter.push_back(jop("Div", jc(d[4]), js("tile_m")));
     sc.temp_iter.push_back(jop("Div", jc(d[5]), js("tile_n")));
     sc.seq_iter = jop("Div", jc(d[4]), js("tile_k"));
@@ -767,33 +805,50 @@ int loom_hip_preferred_block_sizes(const char* func, const int64_t* dims, int nd
   const int64_t* d = dims;
   constexpr long long kCUs = 256;
   std::map<std::string, long long> b;
-  // largest GEMM tile that still gives every CU a workgroup
-  auto gemm_tile = [&](long long M, long long N, long long z) {
+  // a workgroup tile T bound within natural_ub: T itself, or the whole
+  // extent when that is below T (it runs as T)
+  auto bound = [](long long T, long long extent) { return std::min(T, extent); };
+  // largest square GEMM tile that still gives every CU a workgroup, among
+  // those a binding can name for these extents
+  auto gemm_pick = [&](long long M, long long N, long long z) {
+    auto nameable = [&](long long T, long long E) {
+      return T <= E || (T == 64 && E < 64) || (T == 128 && E > 64 && E < 128) ||
+             (T == 256 && E > 128 && E < 256);
+    };
     for (long long t : {256LL, 128LL})
-      if (ceil_div(M, t) * ceil_div(N, t) * z >= kCUs) return t;
-    return 64LL;
+      if (nameable(t, M) && nameable(t, N) && ceil_div(M, t) * ceil_div(N, t) * z >= kCUs) {
+        b["tile_m"] = bound(t, M);
+        b["tile_n"] = bound(t, N);
+        return;
+      }
+    // 64 is nameable on every axis (64 itself, or an extent below it)
+    b["tile_m"] = bound(64, M);
+    b["tile_n"] = bound(64, N);
   };
   if (f == "matmul") {
-    b["tile_m"] = b["tile_n"] = gemm_tile(d[0], d[1], 1);
-    b["tile_k"] = 64;
+    gemm_pick(d[0], d[1], 1);
+    b["tile_k"] = std::min<long long>(64, d[2]);
   } else if (f == "batch_matmul") {
     b["tile_b"] = 1;
-    b["tile_m"] = b["tile_n"] = gemm_tile(d[1], d[2], d[0]);
-    b["tile_k"] = 64;
+    gemm_pick(d[1], d[2], d[0]);
+    b["tile_k"] = std::min<long long>(64, d[3]);
   } else if (f == "split_k_matmul_gather") {
     // 128x128 tiles (64x64 when M or N is small), enough K slabs to cover
     // the CUs, slabs a whole number of the pipelined kernel's rounds (256
     // deep for 128 tiles, 512 for 64) when K allows
     const long long t = (d[0] >= 128 && d[1] >= 128) ? 128 : 64;
     const long long round = t == 128 ? 256 : 512;
-    b["tile_m"] = b["tile_n"] = t;
+    b["tile_m"] = bound(t, d[0]);
+    b["tile_n"] = bound(t, d[1]);
     const long long tiles = ceil_div(d[0], t) * ceil_div(d[1], t);
     const long long step = d[2] >= round ? round : 64;
     const long long S = std::max(1LL, std::min(ceil_div(kCUs, tiles), ceil_div(d[2], step)));
     b["tile_k"] = std::min<long long>(d[2], ceil_div(ceil_div(d[2], S), step) * step);
   } else if (f == "attention") {
     b["tile_b"] = 1;
-    b["tile_m"] = 256;
+    // 256 query rows, or the largest built tile within a shorter Sq (Sq
+    // itself below 64)
+    b["tile_m"] = d[1] >= 256 ? 256 : d[1] >= 192 ? 192 : d[1] >= 128 ? 128 : d[1] >= 64 ? 64 : d[1];
     b["tile_n"] = std::min<long long>(64, d[2]);
   } else if (f == "flash_decode") {
     b["tile_b"] = 1;
@@ -803,9 +858,10 @@ int loom_hip_preferred_block_sizes(const char* func, const int64_t* dims, int nd
     b["tile_n"] = std::min<long long>(128, b["tile_s"]);
   } else {  // helion_mamba2_chunk_scan_kernel
     b["tile_b"] = b["tile_h"] = b["tile_c"] = 1;
-    b["tile_m"] = std::min<long long>(256, ceil_div(d[4], 64) * 64);
-    b["tile_n"] = d[5] >= 64 ? 64 : d[5] >= 32 ? 32 : 16;
-    b["tile_k"] = 64;
+    // one m tile per chunk: the chunk itself (it runs as the covering tile)
+    b["tile_m"] = d[4];
+    b["tile_n"] = d[5] >= 64 ? 64 : d[5] >= 32 ? 32 : d[5] >= 16 ? 16 : d[5];
+    b["tile_k"] = std::min<long long>(64, d[4]);
   }
   std::string j = "{";
   bool first = true;

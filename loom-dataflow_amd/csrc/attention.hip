@@ -324,10 +324,20 @@ int attention_impl(const void* k, const void* v, const void* q, void* out, int64
                      (long long)tile_b, (long long)tile_m, (long long)tile_n);
   if (causal && Sq != Skv)
     return loom_fail(err, errlen, LOOM_EINVAL, "attention: causal needs Sq == Skv");
-  if (!(tile_m == 64 || tile_m == 128 || tile_m == 192 || tile_m == 256))
+  // tile_m is bounded by Sq (natural_ub); a tile_m equal to a short Sq runs
+  // as the smallest built query tile covering it
+  static const int64_t kQTiles[4] = {64, 128, 192, 256};
+  const int64_t wm = loom_fit_tile(tile_m, Sq, kQTiles, 4);
+  if (wm == 0)
+    return loom_fail(err, errlen, LOOM_EINVAL,
+                     "attention: tile_m=%lld exceeds its extent Sq=%lld (natural_ub)",
+                     (long long)tile_m, (long long)Sq);
+  if (wm < 0)
     return loom_fail(err, errlen, LOOM_EUNSUP,
-                     "attention: tile_m %lld not built for gfx950 (64, 128, 192, 256)",
+                     "attention: tile_m %lld not built for gfx950 (64, 128, 192, 256, or Sq "
+                     "itself below 256)",
                      (long long)tile_m);
+  tile_m = wm;
   if (!(D == 64 || D == 128))
     return loom_fail(err, errlen, LOOM_EUNSUP, "attention: head_dim %lld not built (64, 128)",
                      (long long)D);

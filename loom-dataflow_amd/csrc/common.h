@@ -179,6 +179,25 @@ static inline int loom_check_launch(char* err, size_t errlen, const char* what) 
 static inline int64_t cdiv64(int64_t a, int64_t b) { return (a + b - 1) / b; }
 static inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// The reference bounds every loom.sym by the extent of the loop it tiles
+// (its upper_bound, exported as natural_ub:
+// lib/passes/lcs/src/staged_etg_builder.cpp:1420-1430).  Returns the
+// workgroup tile a bound value runs as along an axis of `extent`, given the
+// tiles built for that axis (`built`, ascending):
+//   > 0  the value itself when it is built, or -- when the value is the whole
+//        extent -- the smallest built tile covering it (one block on the axis);
+//     0  the value exceeds the extent (callers return LOOM_EINVAL);
+//    -1  the value is legal in the reference but nothing is built for it.
+static inline int64_t loom_fit_tile(int64_t t, int64_t extent, const int64_t* built, int nbuilt) {
+  if (t > extent) return 0;
+  for (int i = 0; i < nbuilt; ++i)
+    if (built[i] == t) return t;
+  if (t == extent)
+    for (int i = 0; i < nbuilt; ++i)
+      if (built[i] >= t) return built[i];
+  return -1;
+}
+
 // ---------------------------------------------------------------------------
 // raw buffer loads: range-checked by the hardware against `bytes` (reads past
 // the end return zeros and issue no memory request), so guarded loads need

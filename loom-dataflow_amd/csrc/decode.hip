@@ -27,6 +27,8 @@
 // gathered tensors; a second kernel performs the split-0 combine.
 #include "common.h"
 
+#include <cmath>
+
 namespace {
 
 constexpr int kWaves = 4;
@@ -371,6 +373,11 @@ int flash_decode_impl(const void* k, const void* v, const void* q, void* out,
                      "flash_decode: tiles must satisfy 1 <= tile_b <= B, 1 <= tile_s, tile_n <= S "
                      "(tile_b=%lld tile_s=%lld tile_n=%lld)",
                      (long long)tile_b, (long long)tile_s, (long long)tile_n);
+  // the running max is taken over raw scores and scaled afterwards, which
+  // equals the max of the scaled scores only for a positive scale
+  if (!(scale > 0.f) || !std::isfinite(scale))
+    return loom_fail(err, errlen, LOOM_EINVAL,
+                     "flash_decode: scale must be finite and positive (got %g)", (double)scale);
   if (!(D == 64 || D == 128))
     return loom_fail(err, errlen, LOOM_EUNSUP, "flash_decode: head_dim %lld not built (64, 128)",
                      (long long)D);

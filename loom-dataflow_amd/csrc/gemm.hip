@@ -29,10 +29,6 @@
 #include <atomic>
 #include <type_traits>
 
-#ifndef LOOM_GEMM_PERSIST
-#define LOOM_GEMM_PERSIST 1
-#endif
-
 namespace {
 
 constexpr int kBK = 64;  // K depth of one LDS stage (8 chunks of 8 bf16)
@@ -960,15 +956,19 @@ __global__ void __launch_bounds__(256) gemm_persist_kernel(GemmParams p, int nr)
   }
 }
 
-// Launches the persistent kernel when every tile is whole, the tiles divide
-// evenly over one workgroup per CU (at least two each) and the pipelined
-// kernel's conditions hold; the caller falls back otherwise.
-// CU count of the current device, cached per device (0 when unknown: the
-// persistent kernel is then not used).
-int device_cus() {
+// CU count of the device `st` belongs to (the null stream: the current
+// device), cached per device; 0 when unknown (the persistent kernel is then
+// not used).
+int device_cus(hipStream_t st) {
   static std::atomic<int> cache[64];   // count + 1; 0 = not queried yet
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  if (st != nullptr) {
+    hipDevice_t d = 0;
+    if (hipStreamGetDevice(st, &d) != hipSuccess) return 0;
+    dev = (int)d;
+  } else if (hipGetDevice(&dev) != hipSuccess) {
+    return 0;
+  }
   if (dev < 0 || dev >= 64) return 0;
   int c = cache[dev].load(std::memory_order_relaxed);
   if (c == 0) {
@@ -980,11 +980,14 @@ int device_cus() {
   return c - 1;
 }
 
+// Launches the persistent kernel when every tile is whole, the tiles divide
+// evenly over one workgroup per CU (at least two each) and the pipelined
+// kernel's conditions hold; the caller falls back otherwise.
 template <bool H>
 bool launch_persist(const GemmParams& p, bool aligned, bool out_f32, hipStream_t st) {
-  const int cus = device_cus();
+  const int cus = device_cus(st);
   const int64_t ntiles = (int64_t)p.tiles_m * p.tiles_n * p.nz;
-  const bool ok = LOOM_GEMM_PERSIST && aligned && !out_f32 && !p.split && cus >= 8 && cus % 8 == 0 &&
+  const bool ok = aligned && !out_f32 && !p.split && cus >= 8 && cus % 8 == 0 &&
                   p.M % 256 == 0 && p.N % 256 == 0 && p.k_total % 128 == 0 && ntiles % cus == 0 &&
                   ntiles / cus >= 2 && p.lda < (1 << 22) && p.ldb < (1 << 22) && p.ldc < (1 << 22);
   if (!ok) return false;
@@ -1055,18 +1058,12 @@ hipError_t launch_tile(const GemmParams& p, bool aligned, bool out_f32, hipStrea
   return hipGetLastError();
 }
 
-// Workgroup tiles built for gfx950: (tile_m, tile_n) -> waves (WM x WN).
-bool tile_supported(int64_t tm, int64_t tn) {
-  return (tm == 64 && tn == 64) || (tm == 128 && tn == 128) || (tm == 256 && tn == 256);
-}
+// Square workgroup tiles built for gfx950 (tile_m = tile_n).
+constexpr int64_t kGemmTiles[3] = {64, 128, 256};
 
-// Depth of the DMA pipeline of the 256x256 kernel: BK-deep stages, NS of them.
-#ifndef LOOM_GEMM_DMA_BK
-#define LOOM_GEMM_DMA_BK 32
-#endif
-#ifndef LOOM_GEMM_DMA_NS
-#define LOOM_GEMM_DMA_NS 4
-#endif
+// Depth of the DMA pipeline of the 256x256 fallback kernel: BK-deep stages,
+// NS of them (32 x 4 measured fastest of 32/64 deep, 2-4 stages).
+constexpr int kDmaBK = 32, kDmaNS = 4;
 
 template <bool H>
 hipError_t launch_gemm(GemmParams p, int64_t tile_m, int64_t tile_n, bool aligned, bool out_f32,
@@ -1085,7 +1082,7 @@ hipError_t launch_gemm(GemmParams p, int64_t tile_m, int64_t tile_n, bool aligne
   if (launch_pipe<256, H>(p, aligned, out_f32, st)) return hipGetLastError();
   const dim3 grid((unsigned)((int64_t)p.tiles_m * p.tiles_n * p.nz)), block(256);
   // otherwise the LDS-DMA kernel needs whole BK steps in every K range
-  constexpr int BK = LOOM_GEMM_DMA_BK, NS = LOOM_GEMM_DMA_NS;
+  constexpr int BK = kDmaBK, NS = kDmaNS;
   const bool dma = aligned && p.k_total % BK == 0 && (!p.split || p.k_slab % BK == 0);
   if (dma) {
     if (out_f32)
@@ -1097,9 +1094,13 @@ hipError_t launch_gemm(GemmParams p, int64_t tile_m, int64_t tile_n, bool aligne
   return launch_tile<256, 256, 2, 4, H>(p, aligned, out_f32, st);
 }
 
+// Checks what every GEMM entry point shares.  On success *wg is the square
+// workgroup tile the (tile_m, tile_n) binding runs as: a built tile, or --
+// for a tile equal to a whole extent below it -- the smallest one covering
+// that extent.  Every tile is bounded by its loop extent (natural_ub).
 int check_gemm_common(const void* a, const void* b, const void* c, int64_t M, int64_t N,
-                      int64_t K, int64_t tile_m, int64_t tile_n, int64_t tile_k, const char* fn,
-                      char* err, size_t errlen) {
+                      int64_t K, int64_t tile_m, int64_t tile_n, int64_t tile_k, int64_t* wg,
+                      const char* fn, char* err, size_t errlen) {
   if (!a || !b || !c) return loom_fail(err, errlen, LOOM_EINVAL, "%s: null tensor pointer", fn);
   if (M <= 0 || N <= 0 || K <= 0)
     return loom_fail(err, errlen, LOOM_EINVAL, "%s: extents must be positive (M=%lld N=%lld K=%lld)",
@@ -1108,21 +1109,30 @@ int check_gemm_common(const void* a, const void* b, const void* c, int64_t M, in
     return loom_fail(err, errlen, LOOM_EINVAL, "%s: M and N must be below 2^30", fn);
   if (tile_m <= 0 || tile_n <= 0 || tile_k <= 0)
     return loom_fail(err, errlen, LOOM_EINVAL, "%s: tile sizes must be positive", fn);
-  if (!tile_supported(tile_m, tile_n))
+  const int64_t em = loom_fit_tile(tile_m, M, kGemmTiles, 3);
+  const int64_t en = loom_fit_tile(tile_n, N, kGemmTiles, 3);
+  if (em == 0 || en == 0 || tile_k > K)
+    return loom_fail(err, errlen, LOOM_EINVAL,
+                     "%s: tiles exceed their extents (natural_ub): tile_m=%lld (M=%lld), "
+                     "tile_n=%lld (N=%lld), tile_k=%lld (K=%lld)",
+                     fn, (long long)tile_m, (long long)M, (long long)tile_n, (long long)N,
+                     (long long)tile_k, (long long)K);
+  if (em < 0 || en < 0 || em != en)
     return loom_fail(err, errlen, LOOM_EUNSUP,
                      "%s: workgroup tile %lldx%lld not built for gfx950 (built: 64x64, 128x128, "
-                     "256x256)",
+                     "256x256; a tile equal to a whole extent runs as the smallest covering it)",
                      fn, (long long)tile_m, (long long)tile_n);
+  *wg = em;
   return LOOM_OK;
 }
-
-
 
 template <bool H>
 int matmul_impl(const void* x, const void* y, void* out, int64_t M, int64_t N, int64_t K,
                     int64_t tile_m, int64_t tile_n, int64_t tile_k, void* stream, char* err,
                     size_t errlen) {
-  int rc = check_gemm_common(x, y, out, M, N, K, tile_m, tile_n, tile_k, "matmul", err, errlen);
+  int64_t wg = 0;
+  int rc = check_gemm_common(x, y, out, M, N, K, tile_m, tile_n, tile_k, &wg, "matmul", err,
+                             errlen);
   if (rc) return rc;
   GemmParams p{};
   p.A = static_cast<const uint16_t*>(x);
@@ -1139,7 +1149,7 @@ int matmul_impl(const void* x, const void* y, void* out, int64_t M, int64_t N, i
   p.nz = 1;
   const bool al = K % 8 == 0 && N % 8 == 0 && aligned16(x) && aligned16(y);
   if (loom_validate_only()) return loom_ok(err, errlen);
-  (void)launch_gemm<H>(p, tile_m, tile_n, al, false, static_cast<hipStream_t>(stream));
+  (void)launch_gemm<H>(p, wg, wg, al, false, static_cast<hipStream_t>(stream));
   return loom_check_launch(err, errlen, "matmul");
 }
 
@@ -1147,12 +1157,17 @@ template <bool H>
 int batch_matmul_impl(const void* arg0, const void* arg1, void* arg2, int64_t Bt, int64_t M,
                           int64_t N, int64_t K, int64_t tile_b, int64_t tile_m, int64_t tile_n,
                           int64_t tile_k, void* stream, char* err, size_t errlen) {
-  int rc = check_gemm_common(arg0, arg1, arg2, M, N, K, tile_m, tile_n, tile_k, "batch_matmul",
-                             err, errlen);
+  int64_t wg = 0;
+  int rc = check_gemm_common(arg0, arg1, arg2, M, N, K, tile_m, tile_n, tile_k, &wg,
+                             "batch_matmul", err, errlen);
   if (rc) return rc;
   if (Bt <= 0 || tile_b <= 0)
     return loom_fail(err, errlen, LOOM_EINVAL, "batch_matmul: batch and tile_b must be positive");
-  const int64_t tiles = cdiv64(M, tile_m) * cdiv64(N, tile_n) * Bt;
+  if (tile_b > Bt)
+    return loom_fail(err, errlen, LOOM_EINVAL,
+                     "batch_matmul: tile_b=%lld exceeds its extent B=%lld (natural_ub)",
+                     (long long)tile_b, (long long)Bt);
+  const int64_t tiles = cdiv64(M, wg) * cdiv64(N, wg) * Bt;
   if (tiles > 0x7fffffff)
     return loom_fail(err, errlen, LOOM_EINVAL, "batch_matmul: grid too large");
   GemmParams p{};
@@ -1173,7 +1188,7 @@ int batch_matmul_impl(const void* arg0, const void* arg1, void* arg2, int64_t Bt
   p.nz = (int)Bt;
   const bool al = K % 8 == 0 && N % 8 == 0 && aligned16(arg0) && aligned16(arg1);
   if (loom_validate_only()) return loom_ok(err, errlen);
-  (void)launch_gemm<H>(p, tile_m, tile_n, al, false, static_cast<hipStream_t>(stream));
+  (void)launch_gemm<H>(p, wg, wg, al, false, static_cast<hipStream_t>(stream));
   return loom_check_launch(err, errlen, "batch_matmul");
 }
 
@@ -1183,20 +1198,17 @@ int split_k_matmul_gather_impl(const void* a, const void* b, void* out, void* pa
                                    size_t partials_bytes, int64_t M, int64_t N, int64_t K,
                                    int64_t tile_m, int64_t tile_n, int64_t tile_k, void* stream,
                                    char* err, size_t errlen) {
-  int rc = check_gemm_common(a, b, out, M, N, K, tile_m, tile_n, tile_k, "split_k_matmul_gather",
-                             err, errlen);
+  int64_t wg = 0;
+  int rc = check_gemm_common(a, b, out, M, N, K, tile_m, tile_n, tile_k, &wg,
+                             "split_k_matmul_gather", err, errlen);
   if (rc) return rc;
-  if (tile_k > K)
-    return loom_fail(err, errlen, LOOM_EINVAL,
-                     "split_k_matmul_gather: tile_k=%lld exceeds K=%lld", (long long)tile_k,
-                     (long long)K);
   const int64_t S = cdiv64(K, tile_k);
   const size_t need = loom_hip_split_k_workspace_bytes(M, N, K, tile_k);
   if (!partials || partials_bytes < need)
     return loom_fail(err, errlen, LOOM_EINVAL,
                      "split_k_matmul_gather: partials workspace needs %zu bytes, got %zu", need,
                      partials_bytes);
-  if (S * cdiv64(M, tile_m) * cdiv64(N, tile_n) > 0x7fffffff)
+  if (S * cdiv64(M, wg) * cdiv64(N, wg) > 0x7fffffff)
     return loom_fail(err, errlen, LOOM_EINVAL, "split_k_matmul_gather: grid too large");
   hipStream_t st = static_cast<hipStream_t>(stream);
   GemmParams p{};
@@ -1215,7 +1227,7 @@ int split_k_matmul_gather_impl(const void* a, const void* b, void* out, void* pa
   p.nz = (int)S;
   const bool al = K % 8 == 0 && N % 8 == 0 && tile_k % 8 == 0 && aligned16(a) && aligned16(b);
   if (loom_validate_only()) return loom_ok(err, errlen);
-  (void)launch_gemm<H>(p, tile_m, tile_n, al, true, st);
+  (void)launch_gemm<H>(p, wg, wg, al, true, st);
   rc = loom_check_launch(err, errlen, "split_k_matmul_gather (slab GEMM)");
   if (rc) return rc;
   const int64_t MN = M * N;

@@ -43,15 +43,27 @@ constexpr int kWaves = 4;
 struct MambaParams {
   const uint16_t* cb;
   const uint16_t* x;
-  const float* dt;
-  const float* dA;
+  const void* dt;      // fp32, or f16 in the f16 variant
+  const void* dA;      // fp32 / f16
   const uint16_t* C;
-  const float* Dh;
-  const float* prevT;
+  const void* Dh;      // fp32 / f16
+  const void* prevT;   // fp32 / f16
   uint16_t* out;
   int Bb, nc, H, G, Q, P, N;
   int tile_m, tile_n, nmt, npt;
 };
+
+// Element i of a side tensor (dt, dA_cumsum, D, prev_states_T) as fp32: fp32
+// in the bf16 variant, f16 -- the reference's own type
+// (examples/mamba_chunk_scan/IR/00_from_helion_frontend.mlir:4) -- in the f16
+// variant.  The widening is exact.
+template <bool F16>
+LOOM_DEV float side_at(const void* __restrict__ t, int64_t i) {
+  if constexpr (F16)
+    return (float)reinterpret_cast<const _Float16* __restrict__>(t)[i];
+  else
+    return reinterpret_cast<const float* __restrict__>(t)[i];
+}
 
 template <int PT, bool F16>  // p tiles of 16 per workgroup (tile_n = 16 PT); F16: f16 elements
 __global__ void __launch_bounds__(64 * kWaves) mamba_chunk_scan_kernel(MambaParams p) {
@@ -87,7 +99,9 @@ __global__ void __launch_bounds__(64 * kWaves) mamba_chunk_scan_kernel(MambaPara
   const uint16_t* __restrict__ xg = p.x + ((int64_t)(b * H + h) * L + (int64_t)c * Q) * P;
   const uint16_t* __restrict__ Cg = p.C + ((int64_t)(b * p.G + grp) * L + (int64_t)c * Q) * N;
   const uint16_t* __restrict__ cbg = p.cb + ((int64_t)(b * p.nc + c) * p.G + grp) * Q * Q;
-  const float* __restrict__ pvg = p.prevT + ((int64_t)(b * p.nc + c) * H + h) * N * P;
+  const int64_t pv0 = ((int64_t)(b * p.nc + c) * H + h) * N * P;   // prevT element offset
+  const float* __restrict__ pvg = reinterpret_cast<const float*>(p.prevT) + pv0;        // bf16 form
+  const uint16_t* __restrict__ pvh = reinterpret_cast<const uint16_t*>(p.prevT) + pv0;  // f16 form
   const int64_t sidx = ((int64_t)(b * H + h) * p.nc + c) * Q;
 
   // ---- staging: every global load first, then conversions and LDS stores.
@@ -103,9 +117,9 @@ __global__ void __launch_bounds__(64 * kWaves) mamba_chunk_scan_kernel(MambaPara
   f32x4_t pr[8][2];
   float dA_v = 0.f, dt_v = 0.f, dA_e = 0.f;
   if (tid < Q) {
-    dA_v = p.dA[sidx + tid];
-    dt_v = p.dt[sidx + tid];
-    dA_e = p.dA[sidx + min(tid | 31, Q - 1)];  // last key of tid's 32-key block
+    dA_v = side_at<F16>(p.dA, sidx + tid);
+    dt_v = side_at<F16>(p.dt, sidx + tid);
+    dA_e = side_at<F16>(p.dA, sidx + min(tid | 31, Q - 1));  // last key of tid's 32-key block
   }
   if (do_x) {
     const int pg = p0 + x_pc * 8;
@@ -122,8 +136,14 @@ __global__ void __launch_bounds__(64 * kWaves) mamba_chunk_scan_kernel(MambaPara
     for (int e = 0; e < 8; ++e) {
       const int n = p_nc * 8 + e;
       if (n < N && pg < P) {
-        pr[e][0] = *reinterpret_cast<const f32x4_t*>(pvg + (int64_t)n * P + pg);
-        pr[e][1] = *reinterpret_cast<const f32x4_t*>(pvg + (int64_t)n * P + pg + 4);
+        if constexpr (F16) {
+          const u32x4_t w = *reinterpret_cast<const u32x4_t*>(pvh + (int64_t)n * P + pg);
+          pr[e][0] = f32x4_t{lo16<true>(w[0]), hi16<true>(w[0]), lo16<true>(w[1]), hi16<true>(w[1])};
+          pr[e][1] = f32x4_t{lo16<true>(w[2]), hi16<true>(w[2]), lo16<true>(w[3]), hi16<true>(w[3])};
+        } else {
+          pr[e][0] = *reinterpret_cast<const f32x4_t*>(pvg + (int64_t)n * P + pg);
+          pr[e][1] = *reinterpret_cast<const f32x4_t*>(pvg + (int64_t)n * P + pg + 4);
+        }
       } else {
         pr[e][0] = pr[e][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
       }
@@ -144,7 +164,8 @@ __global__ void __launch_bounds__(64 * kWaves) mamba_chunk_scan_kernel(MambaPara
     for (int u = 0; u < 8; ++u) xT[(x_pc * 8 + u) * XROW + (x_kc ^ u)] = tr[u];  // row & 7 == u
   }
   if (do_p) {
-    // prevT split into bf16 hi + lo (the state term keeps ~16 mantissa bits)
+    // prevT split into bf16 hi + lo (the state term keeps ~16 mantissa bits);
+    // an f16 prevT is exact in f16, so its lo half is zero and never used
     u32x4_t hi[8], lo[8], thi[8], tlo[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -158,17 +179,17 @@ __global__ void __launch_bounds__(64 * kWaves) mamba_chunk_scan_kernel(MambaPara
       }
     }
     transpose8x8(hi, thi);
-    transpose8x8(lo, tlo);
+    if constexpr (!F16) transpose8x8(lo, tlo);
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const int pp = p_pc * 8 + u;
       pT[0][pp * PROW + (p_nc ^ u)] = thi[u];
-      pT[1][pp * PROW + (p_nc ^ u)] = tlo[u];
+      if constexpr (!F16) pT[1][pp * PROW + (p_nc ^ u)] = tlo[u];
     }
   }
   __syncthreads();
 
-  const float Dh = p.Dh[h];
+  const float Dh = side_at<F16>(p.Dh, h);
   const int nmt16 = (mend - m0 + 15) / 16;  // 16-row tiles of this workgroup
   constexpr int MAXT = kQmax / 16 / kWaves;  // tiles per wave at most
   constexpr int NSN = kNmax / 32;            // state-term steps at most
@@ -234,7 +255,7 @@ __global__ void __launch_bounds__(64 * kWaves) mamba_chunk_scan_kernel(MambaPara
         const int pp = pt * 16 + rr;
         const int ch = (ns * 4 + g4) ^ (pp & 7);
         acc_s[pt] = mfma16t<F16>(pT[0][pp * PROW + ch], rw.c[ns], acc_s[pt]);
-        acc_s[pt] = mfma16t<F16>(pT[1][pp * PROW + ch], rw.c[ns], acc_s[pt]);
+        if constexpr (!F16) acc_s[pt] = mfma16t<F16>(pT[1][pp * PROW + ch], rw.c[ns], acc_s[pt]);
       }
     }
     const float dAm = am < Q ? s_dA[am] : 0.f;
@@ -337,12 +358,30 @@ int chunk_scan_impl(
     return loom_fail(err, errlen, LOOM_EINVAL, "%s: tile_b, tile_h and tile_c must be 1", fn);
   if (tile_m <= 0 || tile_n <= 0 || tile_k <= 0)
     return loom_fail(err, errlen, LOOM_EINVAL, "%s: tile sizes must be positive", fn);
-  if (tile_m % 64 != 0 || tile_m > kQmax)
-    return loom_fail(err, errlen, LOOM_EUNSUP, "%s: tile_m must be 64, 128, 192 or 256 (got %lld)",
-                     fn, (long long)tile_m);
-  if (!(tile_n == 16 || tile_n == 32 || tile_n == 64))
-    return loom_fail(err, errlen, LOOM_EUNSUP, "%s: tile_n must be 16, 32 or 64 (got %lld)", fn,
+  // every tile is bounded by the extent of its loop (natural_ub): tile_m and
+  // tile_k by chunk_size (the m rows and k keys of one chunk), tile_n by
+  // headdim; a tile equal to a short extent runs as the smallest built tile
+  // covering it
+  static const int64_t kMTiles[4] = {64, 128, 192, 256};
+  static const int64_t kNTiles[3] = {16, 32, 64};
+  const int64_t wm = loom_fit_tile(tile_m, chunk_size, kMTiles, 4);
+  const int64_t wn = loom_fit_tile(tile_n, headdim, kNTiles, 3);
+  if (wm == 0 || wn == 0 || tile_k > chunk_size)
+    return loom_fail(err, errlen, LOOM_EINVAL,
+                     "%s: tiles exceed their extents (natural_ub): tile_m=%lld and tile_k=%lld "
+                     "(chunk_size=%lld), tile_n=%lld (headdim=%lld)",
+                     fn, (long long)tile_m, (long long)tile_k, (long long)chunk_size,
+                     (long long)tile_n, (long long)headdim);
+  if (wm < 0)
+    return loom_fail(err, errlen, LOOM_EUNSUP,
+                     "%s: tile_m must be 64, 128, 192 or 256, or chunk_size itself (got %lld)", fn,
+                     (long long)tile_m);
+  if (wn < 0)
+    return loom_fail(err, errlen, LOOM_EUNSUP,
+                     "%s: tile_n must be 16, 32 or 64, or headdim itself (got %lld)", fn,
                      (long long)tile_n);
+  tile_m = wm;
+  tile_n = wn;
   if (chunk_size > kQmax || dstate > kNmax || chunk_size % 8 || dstate % 8 || headdim % 8)
     return loom_fail(err, errlen, LOOM_EUNSUP,
                      "%s: built for chunk_size <= %d, dstate <= %d, both and headdim multiples "
@@ -358,11 +397,11 @@ int chunk_scan_impl(
   MambaParams p{};
   p.cb = static_cast<const uint16_t*>(cb);
   p.x = static_cast<const uint16_t*>(x);
-  p.dt = static_cast<const float*>(dt);
-  p.dA = static_cast<const float*>(dA_cumsum);
+  p.dt = dt;
+  p.dA = dA_cumsum;
   p.C = static_cast<const uint16_t*>(C);
-  p.Dh = static_cast<const float*>(D);
-  p.prevT = static_cast<const float*>(prev_states_T);
+  p.Dh = D;
+  p.prevT = prev_states_T;
   p.out = static_cast<uint16_t*>(out);
   p.Bb = (int)batch;
   p.nc = (int)nchunks;

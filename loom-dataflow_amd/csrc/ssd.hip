@@ -609,15 +609,25 @@ int prologue_impl(const void* x, const void* dt, const void* A, const void* B,
   int rc = check_ssd("ssd_prologue", batch, nchunks, nheads, ngroups, chunk_size, headdim, dstate,
                      err, errlen);
   if (rc) return rc;
-  rc = loom_hip_ssd_chunk_cumsum(dt, A, dA_cumsum, batch, nchunks, nheads, chunk_size, stream,
-                                 err, errlen);
-  if (rc) return rc;
-  rc = bmm_chunk_impl<F16>(B, C, cb, batch, nchunks, ngroups, chunk_size, dstate, stream, err,
-                              errlen);
-  if (rc) return rc;
-  return state_passing_impl<F16>(x, dt, dA_cumsum, B, prev_states_T, batch, nchunks,
-                                          nheads, ngroups, chunk_size, headdim, dstate, stream,
-                                          err, errlen);
+  // the three stages' own checks run first, validate-only, so a shape the
+  // last stage rejects (e.g. an LDS plan that does not fit) launches nothing
+  auto stages = [&]() {
+    int r = loom_hip_ssd_chunk_cumsum(dt, A, dA_cumsum, batch, nchunks, nheads, chunk_size,
+                                      stream, err, errlen);
+    if (r) return r;
+    r = bmm_chunk_impl<F16>(B, C, cb, batch, nchunks, ngroups, chunk_size, dstate, stream, err,
+                            errlen);
+    if (r) return r;
+    return state_passing_impl<F16>(x, dt, dA_cumsum, B, prev_states_T, batch, nchunks, nheads,
+                                   ngroups, chunk_size, headdim, dstate, stream, err, errlen);
+  };
+  bool& vo = loom_validate_only_flag();
+  const bool outer = vo;
+  vo = true;
+  rc = stages();
+  vo = outer;
+  if (rc || outer) return rc;
+  return stages();
 }
 
 }  // namespace

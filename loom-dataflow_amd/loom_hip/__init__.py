@@ -16,6 +16,7 @@ raises.
 from __future__ import annotations
 
 import ctypes
+import functools
 import math
 import os
 
@@ -115,20 +116,6 @@ def _stream(t: torch.Tensor) -> int:
     return torch.cuda.current_stream(t.device).cuda_stream
 
 
-def _need(t: torch.Tensor, name: str, dtype: torch.dtype, ndim: int) -> int:
-    if not isinstance(t, torch.Tensor):
-        raise TypeError(f"{name}: expected a torch.Tensor")
-    if t.device.type != "cuda":
-        raise ValueError(f"{name}: must be on a ROCm device, got {t.device}")
-    if t.dtype != dtype:
-        raise TypeError(f"{name}: expected {dtype}, got {t.dtype}")
-    if t.dim() != ndim:
-        raise ValueError(f"{name}: expected {ndim} dims, got shape {tuple(t.shape)}")
-    if not t.is_contiguous():
-        raise ValueError(f"{name}: must be contiguous")
-    return t.data_ptr()
-
-
 _bf16, _f16, _fp32 = torch.bfloat16, torch.float16, torch.float32
 
 
@@ -141,40 +128,148 @@ def _elt(t):
     return _bf16, ""
 
 
+# Tensor arguments of every function, in IR order: (name, kind, shape from
+# the extents).  kind "e" is the 16-bit element type of the call; "s" a side
+# tensor -- fp32 in the bf16 variant, f16 (the reference's own type,
+# examples/mamba_chunk_scan/IR/00_from_helion_frontend.mlir:4) in the f16
+# variant.  Extents are in loom_hip_dispatch's order.
+_SPECS = {
+    "matmul": lambda M, N, K: (("x", "e", (M, K)), ("y", "e", (K, N)), ("out", "e", (M, N))),
+    "batch_matmul": lambda B, M, N, K: (("arg0", "e", (B, M, K)), ("arg1", "e", (B, K, N)),
+                                        ("arg2", "e", (B, M, N))),
+    "split_k_matmul_gather": lambda M, N, K: (("a", "e", (M, K)), ("b", "e", (K, N)),
+                                              ("out", "e", (M, N))),
+    "attention": lambda BH, Sq, Skv, D: (("k", "e", (BH, D, Skv)), ("v", "e", (BH, Skv, D)),
+                                         ("q", "e", (BH, Sq, D)), ("out", "e", (BH, Sq, D))),
+    "flash_decode": lambda B, H, D, S: (("k", "e", (B, D, S)), ("v", "e", (B, S, D)),
+                                        ("q", "e", (B, H, D)), ("out", "e", (B, H, D))),
+    "helion_mamba2_chunk_scan_kernel": lambda b, nc, H, G, Q, P, N: (
+        ("cb", "e", (b, nc, G, Q, Q)), ("x", "e", (b, H, nc * Q, P)),
+        ("dt", "s", (b, H, nc, Q)), ("dA_cumsum", "s", (b, H, nc, Q)),
+        ("C", "e", (b, G, nc * Q, N)), ("D", "s", (H,)), ("prev_states_T", "s", (b, nc, H, N, P)),
+        ("out", "e", (b, H, nc * Q, P))),
+}
+
+
+def _check_form(t, name: str, dtype: torch.dtype, shape) -> None:
+    """Type, dtype, exact shape and contiguity of one argument.  Nothing
+    reaches the C ABI unchecked: it takes raw pointers and cannot see a short
+    buffer or a wrong element type."""
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name}: expected a torch.Tensor, got {type(t).__name__}")
+    if t.dtype != dtype:
+        raise TypeError(f"{name}: expected {dtype}, got {t.dtype}")
+    if tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name}: expected shape {tuple(shape)}, got {tuple(t.shape)}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name}: must be contiguous")
+
+
+def _check_device(t, name: str, device=None) -> int:
+    """One argument is on the call's ROCm device; its device pointer."""
+    if t.device.type != "cuda":
+        raise ValueError(f"{name}: must be on a ROCm device, got {t.device}")
+    if device is not None and t.device != device:
+        raise ValueError(f"{name}: on {t.device}, the call's tensors are on {device}")
+    return t.data_ptr()
+
+
+def _check_tensor(t, name: str, dtype: torch.dtype, shape, device=None) -> int:
+    _check_form(t, name, dtype, shape)
+    return _check_device(t, name, device)
+
+
+def _check_call(func: str, tensors, dims, e: torch.dtype):
+    """Validates every tensor argument of `func` against its extents (the form
+    of all of them first, then their devices); returns the device pointers in
+    IR order."""
+    spec = _SPECS[func](*dims)
+    if len(tensors) != len(spec):
+        raise ValueError(f"{func}: takes {len(spec)} tensors ({', '.join(n for n, _, _ in spec)}), "
+                         f"got {len(tensors)}")
+    side = _fp32 if e == _bf16 else _f16
+    for t, (name, kind, shape) in zip(tensors, spec):
+        _check_form(t, name, e if kind == "e" else side, shape)
+    dev0 = tensors[0].device
+    return [_check_device(t, name, dev0) for t, (name, _, _) in zip(tensors, spec)]
+
+
+def _shape2(t, name):
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name}: expected a torch.Tensor, got {type(t).__name__}")
+    return tuple(t.shape)
+
+
+def _dims_of(func: str, tensors):
+    """Extents of a call (loom_hip_dispatch's order), read from its inputs;
+    _check_call then holds every tensor to them."""
+    sh = [_shape2(t, f"tensor {i}") for i, t in enumerate(tensors)]
+    need = {"matmul": 2, "split_k_matmul_gather": 2, "batch_matmul": 2, "attention": 3,
+            "flash_decode": 3, "helion_mamba2_chunk_scan_kernel": 5}[func]
+    if len(sh) < need:
+        raise ValueError(f"{func}: expected at least {need} tensors, got {len(sh)}")
+    rank = lambda i, r: len(sh[i]) == r or (_ for _ in ()).throw(  # noqa: E731
+        ValueError(f"{func}: tensor {i} must have {r} dims, got shape {sh[i]}"))
+    if func in ("matmul", "split_k_matmul_gather"):
+        rank(0, 2), rank(1, 2)
+        return [sh[0][0], sh[1][1], sh[0][1]]
+    if func == "batch_matmul":
+        rank(0, 3), rank(1, 3)
+        return [sh[0][0], sh[0][1], sh[1][2], sh[0][2]]
+    if func == "attention":
+        rank(0, 3), rank(2, 3)
+        return [sh[0][0], sh[2][1], sh[0][2], sh[0][1]]
+    if func == "flash_decode":
+        rank(0, 3), rank(2, 3)
+        return [sh[0][0], sh[2][1], sh[0][1], sh[0][2]]
+    rank(0, 5), rank(1, 4), rank(4, 4)
+    b, nc, G, Q, _ = sh[0]
+    return [b, nc, sh[1][1], G, Q, sh[1][3], sh[4][3]]
+
+
+@functools.lru_cache(maxsize=256)
+def _preferred(func: str, dims: tuple) -> dict:
+    return preferred_block_sizes(func, list(dims))
+
+
+def _tiles(func: str, dims, **given):
+    """Tile arguments of a call: the values given, and for each left as None
+    the library's preferred binding for these extents (always within every
+    symbol's natural_ub)."""
+    if any(v is None for v in given.values()):
+        pref = _preferred(func, tuple(int(d) for d in dims))
+        given = {k: pref[k] if v is None else v for k, v in given.items()}
+    return [int(given[k]) for k in given]
+
+
+def _out_like(out, shape, e, dev):
+    return torch.empty(shape, dtype=e, device=dev) if out is None else out
+
+
 # ---------------------------------------------------------------------------
 # kernels (examples/<k>/IR/00_from_helion_frontend.mlir)
 # ---------------------------------------------------------------------------
 
-def matmul(x, y, out=None, *, tile_m=128, tile_n=128, tile_k=64):
-    """@matmul (examples/mm/IR/00_from_helion_frontend.mlir:2): out = x . y."""
-    _e, _sfx = _elt(x)
-    M, K = x.shape
-    N = y.shape[1]
-    if y.shape[0] != K:
-        raise ValueError(f"matmul: inner dims differ: {tuple(x.shape)} . {tuple(y.shape)}")
-    if out is None:
-        out = torch.empty((M, N), dtype=_e, device=x.device)
-    if tuple(out.shape) != (M, N):
-        raise ValueError("matmul: out shape mismatch")
-    _call("loom_hip_matmul" + _sfx, _need(x, "x", _e, 2), _need(y, "y", _e, 2),
-          _need(out, "out", _e, 2), M, N, K, tile_m, tile_n, tile_k, _stream(x))
+def matmul(x, y, out=None, *, tile_m=None, tile_n=None, tile_k=None):
+    """@matmul (examples/mm/IR/00_from_helion_frontend.mlir:2): out = x . y.
+    Tiles left as None take the preferred binding for the extents."""
+    e, sfx = _elt(x)
+    M, N, K = _dims_of("matmul", (x, y))
+    out = _out_like(out, (M, N), e, x.device)
+    ptrs = _check_call("matmul", (x, y, out), (M, N, K), e)
+    t = _tiles("matmul", (M, N, K), tile_m=tile_m, tile_n=tile_n, tile_k=tile_k)
+    _call("loom_hip_matmul" + sfx, *ptrs, M, N, K, *t, _stream(x))
     return out
 
 
-def batch_matmul(arg0, arg1, arg2=None, *, tile_b=1, tile_m=256, tile_n=256, tile_k=64):
+def batch_matmul(arg0, arg1, arg2=None, *, tile_b=None, tile_m=None, tile_n=None, tile_k=None):
     """@batch_matmul (examples/bmm_2Dmesh/IR/00_from_helion_frontend.mlir:4)."""
-    _e, _sfx = _elt(arg0)
-    B, M, K = arg0.shape
-    N = arg1.shape[2]
-    if tuple(arg1.shape[:2]) != (B, K):
-        raise ValueError("batch_matmul: arg1 shape mismatch")
-    if arg2 is None:
-        arg2 = torch.empty((B, M, N), dtype=_e, device=arg0.device)
-    if tuple(arg2.shape) != (B, M, N):
-        raise ValueError("batch_matmul: arg2 shape mismatch")
-    _call("loom_hip_batch_matmul" + _sfx, _need(arg0, "arg0", _e, 3), _need(arg1, "arg1", _e, 3),
-          _need(arg2, "arg2", _e, 3), B, M, N, K, tile_b, tile_m, tile_n, tile_k,
-          _stream(arg0))
+    e, sfx = _elt(arg0)
+    dims = _dims_of("batch_matmul", (arg0, arg1))
+    arg2 = _out_like(arg2, (dims[0], dims[1], dims[2]), e, arg0.device)
+    ptrs = _check_call("batch_matmul", (arg0, arg1, arg2), dims, e)
+    t = _tiles("batch_matmul", dims, tile_b=tile_b, tile_m=tile_m, tile_n=tile_n, tile_k=tile_k)
+    _call("loom_hip_batch_matmul" + sfx, *ptrs, *dims, *t, _stream(arg0))
     return arg2
 
 
@@ -182,45 +277,44 @@ def split_k_workspace_bytes(M, N, K, tile_k) -> int:
     return int(_lib.loom_hip_split_k_workspace_bytes(M, N, K, tile_k))
 
 
-def split_k_matmul_gather(a, b, out=None, partials=None, *, tile_m=64, tile_n=64, tile_k=1024):
+def split_k_matmul_gather(a, b, out=None, partials=None, *, tile_m=None, tile_n=None,
+                          tile_k=None):
     """@split_k_matmul_gather (examples/split_k_mm_gather/IR/00_from_helion_frontend.mlir:2).
 
     Returns (out [M,N] bf16, partials [S,M,N] fp32 -- the gathered K-slab
     products, S = ceil(K / tile_k))."""
-    _e, _sfx = _elt(a)
-    M, K = a.shape
-    N = b.shape[1]
-    if b.shape[0] != K:
-        raise ValueError("split_k_matmul_gather: inner dims differ")
-    S = -(-K // tile_k) if tile_k > 0 else 0
-    if out is None:
-        out = torch.empty((M, N), dtype=_e, device=a.device)
+    e, sfx = _elt(a)
+    M, N, K = _dims_of("split_k_matmul_gather", (a, b))
+    tile_m, tile_n, tile_k = _tiles("split_k_matmul_gather", (M, N, K), tile_m=tile_m,
+                                    tile_n=tile_n, tile_k=tile_k)
+    S = -(-K // tile_k) if tile_k > 0 else 1
+    out = _out_like(out, (M, N), e, a.device)
     if partials is None:
         partials = torch.empty((max(S, 1), M, N), dtype=_fp32, device=a.device)
-    _call("loom_hip_split_k_matmul_gather" + _sfx, _need(a, "a", _e, 2), _need(b, "b", _e, 2),
-          _need(out, "out", _e, 2), _need(partials, "partials", _fp32, 3),
-          partials.numel() * 4, M, N, K, tile_m, tile_n, tile_k, _stream(a))
+    _check_form(partials, "partials", _fp32, (max(S, 1), M, N))
+    ptrs = _check_call("split_k_matmul_gather", (a, b, out), (M, N, K), e)
+    pp = _check_device(partials, "partials", a.device)
+    _call("loom_hip_split_k_matmul_gather" + sfx, *ptrs, pp, partials.numel() * 4, M, N, K,
+          tile_m, tile_n, tile_k, _stream(a))
     return out, partials
 
 
-def attention(k, v, q, out=None, *, scale=None, causal=False, tile_b=1, tile_m=256,
-              tile_n=64):
+def attention(k, v, q, out=None, *, scale=None, causal=False, tile_b=None, tile_m=None,
+              tile_n=None):
     """@attention (examples/flashattn/IR/00_from_helion_frontend.mlir:4).
 
     k [BH,D,Skv] (keys transposed), v [BH,Skv,D], q [BH,Sq,D] -> out [BH,Sq,D].
     ``scale`` defaults to 1/sqrt(D)."""
-    _e, _sfx = _elt(k)
-    BH, D, Skv = k.shape
-    Sq = q.shape[1]
-    if tuple(v.shape) != (BH, Skv, D) or tuple(q.shape) != (BH, Sq, D):
-        raise ValueError("attention: k/v/q shapes disagree")
+    e, sfx = _elt(k)
+    dims = _dims_of("attention", (k, v, q))
+    BH, Sq, Skv, D = dims
     if scale is None:
         scale = 1.0 / math.sqrt(D)
-    if out is None:
-        out = torch.empty((BH, Sq, D), dtype=_e, device=q.device)
-    _call("loom_hip_attention" + _sfx, _need(k, "k", _e, 3), _need(v, "v", _e, 3),
-          _need(q, "q", _e, 3), _need(out, "out", _e, 3), BH, Sq, Skv, D,
-          float(scale), int(bool(causal)), tile_b, tile_m, tile_n, _stream(q))
+    out = _out_like(out, (BH, Sq, D), e, q.device)
+    ptrs = _check_call("attention", (k, v, q, out), dims, e)
+    t = _tiles("attention", dims, tile_b=tile_b, tile_m=tile_m, tile_n=tile_n)
+    _call("loom_hip_attention" + sfx, *ptrs, BH, Sq, Skv, D, float(scale), int(bool(causal)), *t,
+          _stream(q))
     return out
 
 
@@ -234,29 +328,36 @@ def flash_decode_workspace(B, H, D, S, tile_s, device):
                        dtype=torch.uint8, device=device)
 
 
-def flash_decode(k, v, q, out=None, workspace=None, *, scale=None, tile_b=1, tile_s=1024,
-                 tile_n=128, return_partials=False):
+def _check_workspace(ws, need, device, fn):
+    if not isinstance(ws, torch.Tensor) or ws.device != device or ws.dtype != torch.uint8 or \
+            not ws.is_contiguous() or ws.dim() != 1:
+        raise ValueError(f"{fn}: workspace must be a contiguous 1-D uint8 tensor on {device}")
+    if ws.numel() < need:
+        raise ValueError(f"{fn}: workspace needs {need} bytes, got {ws.numel()}")
+    return ws.data_ptr()
+
+
+def flash_decode(k, v, q, out=None, workspace=None, *, scale=None, tile_b=None, tile_s=None,
+                 tile_n=None, return_partials=False):
     """@flash_decode (examples/mqa_decode/IR/00_from_helion_frontend.mlir:6).
 
     k [B,D,S] (transposed), v [B,S,D], q [B,H,D] -> out [B,H,D].  With
     ``return_partials`` also returns the gathered (lse [ns,B,H], o [ns,B,H,D])."""
-    _e, _sfx = _elt(k)
-    B, D, S = k.shape
-    H = q.shape[1]
-    if tuple(v.shape) != (B, S, D) or tuple(q.shape) != (B, H, D):
-        raise ValueError("flash_decode: k/v/q shapes disagree")
+    e, sfx = _elt(k)
+    dims = _dims_of("flash_decode", (k, v, q))
+    B, H, D, S = dims
+    tile_b, tile_s, tile_n = _tiles("flash_decode", dims, tile_b=tile_b, tile_s=tile_s,
+                                    tile_n=tile_n)
     if scale is None:
         scale = 1.0 / math.sqrt(D)
-    if out is None:
-        out = torch.empty((B, H, D), dtype=_e, device=q.device)
+    out = _out_like(out, (B, H, D), e, q.device)
+    ptrs = _check_call("flash_decode", (k, v, q, out), dims, e)
     if workspace is None:
         workspace = flash_decode_workspace(B, H, D, S, tile_s, q.device)
-    if workspace.device != q.device or workspace.dtype != torch.uint8 or \
-            not workspace.is_contiguous():
-        raise ValueError("flash_decode: workspace must be a contiguous uint8 tensor")
-    _call("loom_hip_flash_decode" + _sfx, _need(k, "k", _e, 3), _need(v, "v", _e, 3),
-          _need(q, "q", _e, 3), _need(out, "out", _e, 3), workspace.data_ptr(),
-          workspace.numel(), B, H, D, S, float(scale), tile_b, tile_s, tile_n, _stream(q))
+    wp = _check_workspace(workspace, flash_decode_workspace_bytes(B, H, D, S, tile_s), q.device,
+                          "flash_decode")
+    _call("loom_hip_flash_decode" + sfx, *ptrs, wp, workspace.numel(), B, H, D, S, float(scale),
+          tile_b, tile_s, tile_n, _stream(q))
     if not return_partials:
         return out
     ns = -(-S // tile_s)
@@ -268,26 +369,22 @@ def flash_decode(k, v, q, out=None, workspace=None, *, scale=None, tile_b=1, til
 
 
 def helion_mamba2_chunk_scan_kernel(cb, x, dt, dA_cumsum, C, D, prev_states_T, out=None, *,
-                                    tile_b=1, tile_h=1, tile_c=1, tile_m=256, tile_n=64,
-                                    tile_k=64):
+                                    tile_b=None, tile_h=None, tile_c=None, tile_m=None,
+                                    tile_n=None, tile_k=None):
     """@helion_mamba2_chunk_scan_kernel
-    (examples/mamba_chunk_scan/IR/00_from_helion_frontend.mlir:4)."""
-    _e, _sfx = _elt(x)
-    b, nc, G, Q, _ = cb.shape
-    _, H, L, P = x.shape
-    N = C.shape[-1]
-    if L != nc * Q or tuple(C.shape) != (b, G, L, N) or tuple(dt.shape) != (b, H, nc, Q) \
-            or tuple(dA_cumsum.shape) != (b, H, nc, Q) or tuple(D.shape) != (H,) \
-            or tuple(prev_states_T.shape) != (b, nc, H, N, P):
-        raise ValueError("helion_mamba2_chunk_scan_kernel: argument shapes disagree")
-    if out is None:
-        out = torch.empty((b, H, L, P), dtype=_e, device=x.device)
-    _call("loom_hip_helion_mamba2_chunk_scan_kernel" + _sfx, _need(cb, "cb", _e, 5),
-          _need(x, "x", _e, 4), _need(dt, "dt", _fp32, 4),
-          _need(dA_cumsum, "dA_cumsum", _fp32, 4), _need(C, "C", _e, 4),
-          _need(D, "D", _fp32, 1), _need(prev_states_T, "prev_states_T", _fp32, 5),
-          _need(out, "out", _e, 4), b, nc, H, G, Q, P, N, tile_b, tile_h, tile_c,
-          tile_m, tile_n, tile_k, _stream(x))
+    (examples/mamba_chunk_scan/IR/00_from_helion_frontend.mlir:4).
+
+    bf16 call: cb, x, C, out bf16; dt, dA_cumsum, D, prev_states_T fp32.
+    f16 call (x in f16): every tensor f16, the reference's own signature."""
+    e, sfx = _elt(x)
+    f = "helion_mamba2_chunk_scan_kernel"
+    dims = _dims_of(f, (cb, x, dt, dA_cumsum, C))
+    b, nc, H, G, Q, P, N = dims
+    out = _out_like(out, (b, H, nc * Q, P), e, x.device)
+    ptrs = _check_call(f, (cb, x, dt, dA_cumsum, C, D, prev_states_T, out), dims, e)
+    t = _tiles(f, dims, tile_b=tile_b, tile_h=tile_h, tile_c=tile_c, tile_m=tile_m, tile_n=tile_n,
+               tile_k=tile_k)
+    _call("loom_hip_" + f + sfx, *ptrs, *dims, *t, _stream(x))
     return out
 
 
@@ -298,28 +395,33 @@ def helion_mamba2_chunk_scan_kernel(cb, x, dt, dA_cumsum, C, D, prev_states_T, o
 def ssd_prologue(x, dt, A, B, C, chunk_size, *, dA_cumsum=None, cb=None, prev_states_T=None):
     """x [b,H,L,P] bf16, dt [b,H,L] fp32 (post-softplus), A [H] fp32,
     B, C [b,G,L,N] bf16 -> (dt [b,H,c,Q] (a view of dt), dA_cumsum [b,H,c,Q],
-    cb [b,c,G,Q,Q] bf16, prev_states_T [b,c,H,N,P] fp32)."""
-    _e, _sfx = _elt(x)
+    cb [b,c,G,Q,Q] bf16, prev_states_T [b,c,H,N,P] fp32).  With f16 x, B, C
+    the cb output is f16; dA_cumsum and prev_states_T stay fp32."""
+    e, sfx = _elt(x)
+    if not isinstance(x, torch.Tensor) or x.dim() != 4 or not isinstance(B, torch.Tensor) \
+            or B.dim() != 4:
+        raise ValueError("ssd_prologue: x and B must be 4-D tensors")
     b, H, L, P = x.shape
     G, N = B.shape[1], B.shape[3]
     Q = int(chunk_size)
-    if L % Q:
-        raise ValueError("ssd_prologue: L must be a multiple of chunk_size")
+    if Q <= 0 or L % Q:
+        raise ValueError("ssd_prologue: L must be a positive multiple of chunk_size")
     nc = L // Q
-    if tuple(dt.shape) != (b, H, L) or tuple(A.shape) != (H,) or tuple(B.shape) != (b, G, L, N) \
-            or tuple(C.shape) != (b, G, L, N):
-        raise ValueError("ssd_prologue: argument shapes disagree")
     dev = x.device
     if dA_cumsum is None:
         dA_cumsum = torch.empty((b, H, nc, Q), dtype=_fp32, device=dev)
     if cb is None:
-        cb = torch.empty((b, nc, G, Q, Q), dtype=_e, device=dev)
+        cb = torch.empty((b, nc, G, Q, Q), dtype=e, device=dev)
     if prev_states_T is None:
         prev_states_T = torch.empty((b, nc, H, N, P), dtype=_fp32, device=dev)
-    _call("loom_hip_ssd_prologue" + _sfx, _need(x, "x", _e, 4), _need(dt, "dt", _fp32, 3),
-          _need(A, "A", _fp32, 1), _need(B, "B", _e, 4), _need(C, "C", _e, 4),
-          _need(dA_cumsum, "dA_cumsum", _fp32, 4), _need(cb, "cb", _e, 5),
-          _need(prev_states_T, "prev_states_T", _fp32, 5), b, nc, H, G, Q, P, N, _stream(x))
+    spec = [(x, "x", e, (b, H, L, P)), (dt, "dt", _fp32, (b, H, L)), (A, "A", _fp32, (H,)),
+            (B, "B", e, (b, G, L, N)), (C, "C", e, (b, G, L, N)),
+            (dA_cumsum, "dA_cumsum", _fp32, (b, H, nc, Q)), (cb, "cb", e, (b, nc, G, Q, Q)),
+            (prev_states_T, "prev_states_T", _fp32, (b, nc, H, N, P))]
+    for a in spec:
+        _check_form(*a)
+    args = [_check_device(a[0], a[1], dev) for a in spec]
+    _call("loom_hip_ssd_prologue" + sfx, *args, b, nc, H, G, Q, P, N, _stream(x))
     return dt.view(b, H, nc, Q), dA_cumsum, cb, prev_states_T
 
 # ---------------------------------------------------------------------------
@@ -365,55 +467,40 @@ def parse_variant(name: str):
     return func.value.decode(), {s: int(t) for s, t in zip(TILE_SYMBOLS, tiles) if t >= 0}
 
 
-def _dims_of(func: str, tensors):
-    if func in ("matmul", "split_k_matmul_gather"):
-        (M, K), N = tensors[0].shape, tensors[1].shape[1]
-        return [M, N, K]
-    if func == "batch_matmul":
-        (B, M, K), N = tensors[0].shape, tensors[1].shape[2]
-        return [B, M, N, K]
-    if func == "attention":
-        BH, D, Skv = tensors[0].shape
-        return [BH, tensors[2].shape[1], Skv, D]
-    if func == "flash_decode":
-        B, D, S = tensors[0].shape
-        return [B, tensors[2].shape[1], D, S]
-    if func == "helion_mamba2_chunk_scan_kernel":
-        b, nc, G, Q, _ = tensors[0].shape
-        _, H, _, P = tensors[1].shape
-        return [b, nc, H, G, Q, P, tensors[4].shape[-1]]
-    raise LoomHipError("loom_hip_dispatch", 2, f"no gfx950 kernel for function '{func}'")
-
-
 def dispatch(variant: str, *tensors, workspace=None, scale=None, causal=False):
     """Runs the kernel a materialized variant name selects on ``tensors``
     (the function's memref arguments in IR order, outputs included) through
-    ``loom_hip_dispatch``.  split_k_matmul_gather and flash_decode allocate
-    their workspace when none is given; it is returned with the output."""
+    ``loom_hip_dispatch``.  Every tensor is checked against the function's
+    signature (dtype, shape, device, contiguity) before anything launches.
+    split_k_matmul_gather and flash_decode allocate their workspace when none
+    is given; it is returned with the output."""
     func, tiles = parse_variant(variant)
+    if func not in _SPECS:
+        raise LoomHipError("loom_hip_dispatch", 2, f"no gfx950 kernel for function '{func}'")
     dims = _dims_of(func, tensors)
-    ptrs = []
-    for i, t in enumerate(tensors):
-        if not isinstance(t, torch.Tensor) or t.device.type != "cuda" or not t.is_contiguous():
-            raise ValueError(f"dispatch: tensor {i} must be a contiguous ROCm tensor")
-        ptrs.append(t.data_ptr())
+    e = _elt(tensors[1] if func == "helion_mamba2_chunk_scan_kernel" else tensors[0])[0]
+    ptrs = _check_call(func, tensors, dims, e)
     dev = tensors[0].device
-    if workspace is None and func == "split_k_matmul_gather" and "tile_k" in tiles:
+    need = 0
+    if func == "split_k_matmul_gather" and "tile_k" in tiles:
         M, N, K = dims
-        workspace = torch.empty(max(split_k_workspace_bytes(M, N, K, tiles["tile_k"]), 4),
-                                dtype=torch.uint8, device=dev)
-    if workspace is None and func == "flash_decode" and "tile_s" in tiles:
+        need = split_k_workspace_bytes(M, N, K, tiles["tile_k"])
+    if func == "flash_decode" and "tile_s" in tiles:
         B, H, D, S = dims
-        workspace = flash_decode_workspace(B, H, D, S, tiles["tile_s"], dev)
+        need = flash_decode_workspace_bytes(B, H, D, S, tiles["tile_s"])
+    if workspace is None and need:
+        workspace = torch.empty(max(need, 4), dtype=torch.uint8, device=dev)
+    ws_ptr, ws_bytes = None, 0
+    if workspace is not None:
+        ws_ptr = _check_workspace(workspace, need, dev, "dispatch")
+        ws_bytes = workspace.numel()
     if scale is None:
-        d = dims[3] if func in ("attention",) else dims[2] if func == "flash_decode" else 1
+        d = dims[3] if func == "attention" else dims[2] if func == "flash_decode" else 1
         scale = 1.0 / math.sqrt(d)
     tarr = (_vp * max(len(ptrs), 1))(*ptrs)
     darr = (_i64 * max(len(dims), 1))(*dims)
-    ws_ptr = workspace.data_ptr() if workspace is not None else None
-    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
     err = ctypes.create_string_buffer(512)
-    disp = _lib.loom_hip_dispatch_f16 if _elt(tensors[0])[0] == _f16 else _lib.loom_hip_dispatch
+    disp = _lib.loom_hip_dispatch_f16 if e == _f16 else _lib.loom_hip_dispatch
     rc = disp(variant.encode(), tarr, len(ptrs), darr, len(dims), float(scale),
               int(bool(causal)), ws_ptr, ws_bytes, _stream(tensors[0]), err, len(err))
     if rc != 0:

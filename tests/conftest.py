@@ -40,3 +40,20 @@ def assert_close(actual, expected, atol, rtol, what=""):
         raise AssertionError(
             f"{what}: {int(bad.sum())}/{a.size} elements outside atol={atol} rtol={rtol}; "
             f"worst at {idx}: got {a[idx]!r} expected {e[idx]!r}; max abs err {err.max():.3e}")
+
+
+GEMM_TILES = (64, 128, 256)
+ATTN_TILES = (64, 128, 192, 256)
+MAMBA_M_TILES = (64, 128, 192, 256)
+MAMBA_N_TILES = (16, 32, 64)
+
+
+def tile_for(T, extent, built):
+    """The tile_* value that makes a kernel run workgroup tile T along an axis
+    of `extent`: T itself within the extent (every symbol is bounded by its
+    loop extent, natural_ub), the whole extent when T is the smallest built
+    tile covering it, else None (T cannot be bound for this extent)."""
+    if T <= extent:
+        return T
+    cover = [t for t in built if t >= extent]
+    return extent if cover and min(cover) == T else None

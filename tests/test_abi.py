@@ -52,7 +52,7 @@ def _call(lh, name, *args):
 
 
 def test_matmul_rejections(lh):
-    rc, msg = _call(lh, "loom_hip_matmul", FAKE, FAKE, FAKE, 64, 64, 64, 96, 96, 64, None)
+    rc, msg = _call(lh, "loom_hip_matmul", FAKE, FAKE, FAKE, 256, 256, 256, 96, 96, 64, None)
     assert rc == 2 and "not built" in msg
     rc, msg = _call(lh, "loom_hip_matmul", None, FAKE, FAKE, 64, 64, 64, 64, 64, 64, None)
     assert rc == 1 and "null" in msg
@@ -61,6 +61,62 @@ def test_matmul_rejections(lh):
     rc, msg = _call(lh, "loom_hip_batch_matmul", FAKE, FAKE, FAKE, 2, 64, 64, 64, 0, 64, 64, 64,
                     None)
     assert rc == 1 and "tile_b" in msg
+
+
+# Every loom.sym is bounded by the extent of the loop it tiles (natural_ub,
+# lib/passes/lcs/src/staged_etg_builder.cpp:1420-1430; e.g. upper_bound = 2048
+# for tile_m of a 2048-row matmul, examples/mm/IR/00_from_helion_frontend.mlir:8).
+NATURAL_UB_CASES = [
+    # (entry point, args before the stream, offending symbol)
+    ("loom_hip_matmul", [FAKE] * 3 + [48, 1024, 1024, 256, 256, 64], "tile_m"),
+    ("loom_hip_matmul", [FAKE] * 3 + [1024, 100, 1024, 128, 128, 64], "tile_n"),
+    ("loom_hip_matmul", [FAKE] * 3 + [1024, 1024, 64, 64, 64, 4096], "tile_k"),
+    ("loom_hip_batch_matmul", [FAKE] * 3 + [4, 256, 256, 256, 8, 64, 64, 64], "tile_b"),
+    ("loom_hip_batch_matmul", [FAKE] * 3 + [4, 100, 256, 256, 1, 128, 128, 64], "tile_m"),
+    ("loom_hip_batch_matmul", [FAKE] * 3 + [4, 256, 256, 32, 1, 64, 64, 64], "tile_k"),
+    ("loom_hip_split_k_matmul_gather", [FAKE] * 4 + [1 << 30, 48, 512, 1024, 64, 64, 128],
+     "tile_m"),
+    ("loom_hip_split_k_matmul_gather", [FAKE] * 4 + [1 << 30, 512, 512, 1024, 64, 64, 2048],
+     "tile_k"),
+    ("loom_hip_attention", [FAKE] * 4 + [4, 128, 128, 128, 0.1, 0, 1, 256, 64], "tile_m"),
+    ("loom_hip_attention", [FAKE] * 4 + [4, 128, 128, 128, 0.1, 0, 1, 128, 256], "tile_n"),
+    ("loom_hip_attention", [FAKE] * 4 + [4, 128, 128, 128, 0.1, 0, 8, 128, 64], "tile_b"),
+    ("loom_hip_flash_decode", [FAKE] * 5 + [1 << 30, 2, 32, 128, 1024, 0.1, 4, 256, 64], "tile_b"),
+    ("loom_hip_flash_decode", [FAKE] * 5 + [1 << 30, 2, 32, 128, 1024, 0.1, 1, 2048, 64],
+     "tile_s"),
+    ("loom_hip_flash_decode", [FAKE] * 5 + [1 << 30, 2, 32, 128, 1024, 0.1, 1, 256, 4096],
+     "tile_n"),
+    ("loom_hip_helion_mamba2_chunk_scan_kernel",
+     [FAKE] * 8 + [1, 2, 4, 1, 64, 64, 128, 1, 1, 1, 64, 64, 99999], "tile_k"),
+    ("loom_hip_helion_mamba2_chunk_scan_kernel",
+     [FAKE] * 8 + [1, 2, 4, 1, 64, 64, 128, 1, 1, 1, 128, 64, 64], "tile_m"),
+    ("loom_hip_helion_mamba2_chunk_scan_kernel",
+     [FAKE] * 8 + [1, 2, 4, 1, 64, 32, 128, 1, 1, 1, 64, 64, 64], "tile_n"),
+]
+
+
+@pytest.mark.parametrize("name,args,sym", NATURAL_UB_CASES,
+                         ids=[f"{c[0][9:]}-{c[2]}" for c in NATURAL_UB_CASES])
+def test_tile_above_natural_ub_rejected(lh, name, args, sym):
+    for suffix in ("", "_f16"):
+        rc, msg = _call(lh, name + suffix, *args, None)
+        assert rc == 1 and sym in msg, (name + suffix, rc, msg)
+
+
+def test_whole_extent_tile_accepted(lh):
+    """A tile equal to a short extent is legal (it runs as the smallest built
+    tile covering it); anything else below the built tiles is not."""
+    lh.check_variant("matmul__tile_k24__tile_m48__tile_n40", [48, 40, 24])
+    lh.check_variant("matmul__tile_k24__tile_m48__tile_n64", [48, 300, 24])
+    lh.check_variant("attention__tile_b1__tile_m40__tile_n40", [2, 40, 40, 64])
+    lh.check_variant("helion_mamba2_chunk_scan_kernel__tile_b1__tile_c1__tile_h1__tile_k48"
+                     "__tile_m48__tile_n32", [1, 2, 4, 1, 48, 32, 64])
+    with pytest.raises(RuntimeError) as ei:
+        lh.check_variant("matmul__tile_k24__tile_m48__tile_n40", [48, 300, 24])
+    assert ei.value.code == 2
+    with pytest.raises(RuntimeError) as ei:
+        lh.check_variant("matmul__tile_k24__tile_m64__tile_n64", [48, 40, 24])
+    assert ei.value.code == 1
 
 
 def test_split_k_rejections(lh):
@@ -103,6 +159,11 @@ def test_flash_decode_rejections(lh):
     rc, msg = _call(lh, "loom_hip_flash_decode", FAKE, FAKE, FAKE, FAKE, FAKE, need,
                     B, H, D, S, 0.1, 1, S + 8, 64, None)
     assert rc == 1
+    # the running max is taken before scaling: only a finite positive scale is valid
+    for bad in (0.0, -0.1, float("nan"), float("inf")):
+        rc, msg = _call(lh, "loom_hip_flash_decode", FAKE, FAKE, FAKE, FAKE, FAKE, need,
+                        B, H, D, S, bad, 1, ts, 64, None)
+        assert rc == 1 and "scale" in msg, bad
 
 
 def test_mamba_rejections(lh):
@@ -133,3 +194,8 @@ def test_ssd_rejections(lh):
     assert rc == 1 and "null" in msg
     rc, msg = _call(lh, "loom_hip_ssd_chunk_cumsum", FAKE, FAKE, FAKE, 1, 2, 4, 1024, None)
     assert rc == 2 and "512" in msg
+    # chunk_size 144 passes the shared checks but fits no LDS plan of the state
+    # kernel: the prologue rejects it before launching its first two stages
+    # (a launch here, without a GPU, would fail with code 3 instead)
+    rc, msg = _call(lh, "loom_hip_ssd_prologue", *([FAKE] * 8), 1, 2, 4, 1, 144, 64, 128, None)
+    assert rc == 2 and "LDS stage" in msg, (rc, msg)

@@ -144,7 +144,30 @@ def test_unsupported_shapes_and_functions():
     with pytest.raises(RuntimeError) as ei:
         loom_hip.constraint_scope("matmul", (1, 2))
     assert ei.value.code == 1
-    # TT-style alignment is gone: tile 64 is legal for a 48x40 GEMM, 32 is not
+    # TT-style 32-alignment is gone; every symbol is bounded by its extent
+    # (natural_ub): on a 48x40 GEMM the whole extents are legal (they run as
+    # one 64x64 tile), 64 exceeds them and 32 is not a gfx950 tile
     hard = loom_hip.constraint_scope("matmul", (48, 40, 24))["constraint_scope"]["hard_constraints"]
-    assert all(evaluate(c, {"tile_m": 64, "tile_n": 64, "tile_k": 24}) for c in hard)
+    assert all(evaluate(c, {"tile_m": 48, "tile_n": 40, "tile_k": 24}) for c in hard)
+    assert not all(evaluate(c, {"tile_m": 64, "tile_n": 64, "tile_k": 24}) for c in hard)
     assert not all(evaluate(c, {"tile_m": 32, "tile_n": 32, "tile_k": 24}) for c in hard)
+    assert not all(evaluate(c, {"tile_m": 48, "tile_n": 40, "tile_k": 25}) for c in hard)
+
+
+@pytest.mark.parametrize("func", sorted(CASES))
+def test_every_symbol_bounded_by_natural_ub(func):
+    """Each symbol's natural_ub is an InRange bound of the scope: its value
+    passes, natural_ub + 1 fails (the other symbols at a legal binding)."""
+    syms, shapes = CASES[func]
+    for dims in shapes:
+        scope = loom_hip.constraint_scope(func, dims)["constraint_scope"]
+        hard, meta = scope["hard_constraints"], scope["metadata"]["symbols"]
+        pref = loom_hip.preferred_block_sizes(func, dims)
+        for s in syms:
+            ub = meta[s]["natural_ub"]
+            assert {"InRange": {"x": {"Sym": s}, "lo": {"Const": 1}, "hi": {"Const": ub}}} in hard
+            over = dict(pref, **{s: ub + 1})
+            assert not all(evaluate(c, over) for c in hard), (func, dims, s)
+            with pytest.raises(RuntimeError) as ei:
+                loom_hip.check_variant(_variant(func, over), dims)
+            assert ei.value.code == 1, (func, s, str(ei.value))

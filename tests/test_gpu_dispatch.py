@@ -128,5 +128,5 @@ def test_dispatch_rejects_unbuilt_tiles(lh):
     x = dev(rng_bf16(rng, (64, 64)))
     out = torch.empty((64, 64), dtype=torch.bfloat16, device="cuda")
     with pytest.raises(RuntimeError) as ei:
-        lh.dispatch("matmul__tile_k512__tile_m64__tile_n32", x, x, out)
+        lh.dispatch("matmul__tile_k64__tile_m64__tile_n32", x, x, out)
     assert ei.value.code == 2

@@ -55,7 +55,8 @@ def rnd(rng, shape, scale=1.0):
 def test_matmul_f16(lh, tile):
     rng = np.random.default_rng(51)
     x, y = rnd(rng, (320, 256)), rnd(rng, (256, 192))
-    out = lh.matmul(dev(x), dev(y), tile_m=tile, tile_n=tile)
+    # tile_n bounded by N = 192 (natural_ub): 192 runs as the 256 tile
+    out = lh.matmul(dev(x), dev(y), tile_m=tile, tile_n=min(tile, 192))
     assert out.dtype == torch.float16
     ref = oracle.matmul(x, y, 64, 64, 64)
     assert_close(from_f16(host(out)), from_f16(ref), **GEMM_TOL, what=f"matmul f16 {tile}")
@@ -127,11 +128,22 @@ def test_ssd_prologue_and_chunk_scan_f16(lh):
     pg = prev.cpu().numpy()
     scale = 1e-2 * float(np.abs(prev_o).max())
     assert np.all(np.abs(pg - prev_o) <= 1e-3 * (np.abs(prev_o) + scale)), "prev_states f16"
-    out = lh.helion_mamba2_chunk_scan_kernel(cb, dev(x), dt4.contiguous(), dA, dev(C), devf(Dh),
-                                             prev, tile_m=192, tile_n=64)
+    # the chunk scan's f16 signature is the reference's own: every tensor f16,
+    # dt, dA_cumsum, D and prev_states_T included
+    # (examples/mamba_chunk_scan/IR/00_from_helion_frontend.mlir:4)
+    h16 = lambda a: np.asarray(a, np.float32).astype(np.float16).astype(np.float32)  # noqa: E731
+    dt_h, dA_h, D_h, prev_h = h16(dt.reshape(b, H, nc, Q)), h16(dA_o), h16(Dh), h16(prev_o)
+    f16 = lambda a: torch.from_numpy(a).to(torch.float16).cuda()  # noqa: E731
+    out = lh.helion_mamba2_chunk_scan_kernel(dev(cb_o), dev(x), f16(dt_h), f16(dA_h), dev(C),
+                                             f16(D_h), f16(prev_h), tile_m=192, tile_n=64)
     assert out.dtype == torch.float16
-    ref = oracle.mamba_chunk_scan(cb_o, x, dt.reshape(b, H, nc, Q), dA_o, C, Dh, prev_o, 64, 64, 64)
+    with oracle.element_type("f16"):
+        ref = oracle.mamba_chunk_scan(cb_o, x, dt_h, dA_h, C, D_h, prev_h, 64, 64, 64)
     assert_close(from_f16(host(out)), from_f16(ref), **ATTN_TOL, what="chunk scan f16")
+    # the fp32 side tensors are refused by the f16 signature before any launch
+    with pytest.raises(TypeError):
+        lh.helion_mamba2_chunk_scan_kernel(cb, dev(x), dt4.contiguous(), dA, dev(C), devf(Dh),
+                                           prev, tile_m=192, tile_n=64)
 
 
 def test_dispatch_f16(lh):

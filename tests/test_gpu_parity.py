@@ -18,7 +18,7 @@ import torch
 
 import oracle
 from oracle import from_bf16, to_bf16
-from tests.conftest import assert_close
+from tests.conftest import ATTN_TILES, GEMM_TILES, MAMBA_M_TILES, assert_close, tile_for
 
 pytestmark = pytest.mark.gpu
 
@@ -56,12 +56,35 @@ def rng_bf16(rng, shape, kind="normal", scale=1.0):
 
 # ------------------------------------------------------------------- matmul
 
-@pytest.mark.parametrize("tiles", [(64, 64), (128, 128), (256, 256)])
+def gemm_bindings(M, N):
+    """(T, tile_m, tile_n) for every square workgroup tile T a binding can
+    name on an M x N output (tiles within their extents)."""
+    out = []
+    for T in GEMM_TILES:
+        tm, tn = tile_for(T, M, GEMM_TILES), tile_for(T, N, GEMM_TILES)
+        if tm is not None and tn is not None:
+            out.append((T, tm, tn))
+    assert out, (M, N)
+    return out
+
+
 @pytest.mark.parametrize("name", ["mm_tiles", "mm_ragged"])
-def test_matmul_golden(lh, golden, name, tiles):
+def test_matmul_golden(lh, golden, name):
     g = golden(name)
-    out = host(lh.matmul(dev(g["x"]), dev(g["y"]), tile_m=tiles[0], tile_n=tiles[1], tile_k=32))
-    assert_close(from_bf16(out), g["expected"], **GEMM_TOL, what=f"{name} {tiles}")
+    M, N = g["expected"].shape
+    for T, tm, tn in gemm_bindings(M, N):
+        out = host(lh.matmul(dev(g["x"]), dev(g["y"]), tile_m=tm, tile_n=tn, tile_k=32))
+        assert_close(from_bf16(out), g["expected"], **GEMM_TOL, what=f"{name} T{T}")
+
+
+def test_matmul_whole_extent_tiles(lh):
+    """Tiles equal to short extents (below the smallest built tile) run as one
+    covering tile: 48 x 40 output with tile_m = 48, tile_n = 40, tile_k = K."""
+    rng = np.random.default_rng(14)
+    x = to_bf16(rng.integers(-8, 9, (48, 24)).astype(np.float32))
+    y = to_bf16(rng.integers(-8, 9, (24, 40)).astype(np.float32))
+    got = host(lh.matmul(dev(x), dev(y), tile_m=48, tile_n=40, tile_k=24))
+    assert np.array_equal(got, oracle.matmul(x, y))
 
 
 def test_matmul_integer_bit_exact(lh):
@@ -69,8 +92,9 @@ def test_matmul_integer_bit_exact(lh):
     x = to_bf16(rng.integers(-8, 9, (200, 328)).astype(np.float32))
     y = to_bf16(rng.integers(-8, 9, (328, 136)).astype(np.float32))
     ref = oracle.matmul(x, y)
-    for t in [(64, 64), (128, 128), (256, 256)]:
-        assert np.array_equal(host(lh.matmul(dev(x), dev(y), tile_m=t[0], tile_n=t[1])), ref), t
+    assert len(gemm_bindings(200, 136)) == 3
+    for T, tm, tn in gemm_bindings(200, 136):
+        assert np.array_equal(host(lh.matmul(dev(x), dev(y), tile_m=tm, tile_n=tn)), ref), T
 
 
 def test_matmul_pipelined_edge_tiles_bit_exact(lh):
@@ -81,9 +105,10 @@ def test_matmul_pipelined_edge_tiles_bit_exact(lh):
         x = to_bf16(rng.integers(-8, 9, (M, K)).astype(np.float32))
         y = to_bf16(rng.integers(-8, 9, (K, N)).astype(np.float32))
         ref = oracle.matmul(x, y)
-        for t in [(64, 64), (128, 128), (256, 256)]:
-            got = host(lh.matmul(dev(x), dev(y), tile_m=t[0], tile_n=t[1]))
-            assert np.array_equal(got, ref), (M, N, K, t)
+        assert len(gemm_bindings(M, N)) == 3
+        for T, tm, tn in gemm_bindings(M, N):
+            got = host(lh.matmul(dev(x), dev(y), tile_m=tm, tile_n=tn))
+            assert np.array_equal(got, ref), (M, N, K, T)
 
 
 def test_matmul_tile64_whole_tiles_bit_exact(lh):
@@ -116,9 +141,10 @@ def test_matmul_baseline_1024(lh):
 
 def test_batch_matmul_golden(lh, golden):
     g = golden("bmm_small")
-    for t in [(64, 64), (128, 128)]:
-        out = host(lh.batch_matmul(dev(g["arg0"]), dev(g["arg1"]), tile_m=t[0], tile_n=t[1]))
-        assert_close(from_bf16(out), g["expected"], **GEMM_TOL, what=f"bmm golden {t}")
+    _, M, N = g["expected"].shape
+    for T, tm, tn in gemm_bindings(M, N):
+        out = host(lh.batch_matmul(dev(g["arg0"]), dev(g["arg1"]), tile_m=tm, tile_n=tn))
+        assert_close(from_bf16(out), g["expected"], **GEMM_TOL, what=f"bmm golden T{T}")
 
 
 def test_batch_matmul_baseline(lh):
@@ -172,8 +198,9 @@ def test_split_k_integer_partials_bit_exact(lh, golden):
 def test_split_k_float(lh, golden):
     g = golden("splitk_float")
     o_ref, p_ref = oracle.split_k_matmul_gather(g["a"], g["b"], 16, 32, int(g["tile_k"]))
-    out, parts = lh.split_k_matmul_gather(dev(g["a"]), dev(g["b"]), tile_m=64, tile_n=64,
-                                          tile_k=int(g["tile_k"]))
+    M, N = g["expected"].shape
+    out, parts = lh.split_k_matmul_gather(dev(g["a"]), dev(g["b"]), tile_m=tile_for(64, M, GEMM_TILES),
+                                          tile_n=tile_for(64, N, GEMM_TILES), tile_k=int(g["tile_k"]))
     assert_close(parts.cpu().numpy(), p_ref, atol=1e-4, rtol=1e-4, what="partials")
     assert_close(from_bf16(host(out)), g["expected"], **GEMM_TOL, what="split-K out")
 
@@ -182,8 +209,9 @@ def test_split_k_ragged_slab(lh, golden):
     """tile_k = 500 does not divide K = 768 and is not a multiple of 8."""
     g = golden("splitk_float")
     o_ref, p_ref = oracle.split_k_matmul_gather(g["a"], g["b"], 16, 32, 500)
-    out, parts = lh.split_k_matmul_gather(dev(g["a"]), dev(g["b"]), tile_m=64, tile_n=64,
-                                          tile_k=500)
+    M, N = g["expected"].shape
+    out, parts = lh.split_k_matmul_gather(dev(g["a"]), dev(g["b"]), tile_m=tile_for(64, M, GEMM_TILES),
+                                          tile_n=tile_for(64, N, GEMM_TILES), tile_k=500)
     assert parts.shape[0] == 2
     assert_close(parts.cpu().numpy(), p_ref, atol=1e-4, rtol=1e-4, what="ragged partials")
     assert_close(from_bf16(host(out)), from_bf16(o_ref), **GEMM_TOL, what="ragged out")
@@ -232,13 +260,20 @@ def test_split_k_baseline_float(lh):
 
 # ---------------------------------------------------------------- attention
 
-@pytest.mark.parametrize("tile_m", [64, 128, 192, 256])
 @pytest.mark.parametrize("name", ["attention_noncausal", "attention_causal"])
-def test_attention_golden(lh, golden, name, tile_m):
+def test_attention_golden(lh, golden, name):
     g = golden(name)
-    out = lh.attention(dev(g["k"]), dev(g["v"]), dev(g["q"]), scale=float(g["scale"]),
-                       causal=bool(g["causal"]), tile_m=tile_m, tile_n=32)
-    assert_close(from_bf16(host(out)), g["expected"], **ATTN_TOL, what=f"{name} {tile_m}")
+    Sq = g["q"].shape[1]
+    ran = 0
+    for T in ATTN_TILES:   # every query tile a binding can name for this Sq
+        tm = tile_for(T, Sq, ATTN_TILES)
+        if tm is None:
+            continue
+        out = lh.attention(dev(g["k"]), dev(g["v"]), dev(g["q"]), scale=float(g["scale"]),
+                           causal=bool(g["causal"]), tile_m=tm, tile_n=32)
+        assert_close(from_bf16(host(out)), g["expected"], **ATTN_TOL, what=f"{name} T{T}")
+        ran += 1
+    assert ran == 2
 
 
 @pytest.mark.parametrize("causal", [False, True])
@@ -369,7 +404,8 @@ def test_mamba_chain_matches_recurrence(lh, golden):
     g = golden("mamba_small")
     Q = int(g["chunk_size"])
     dt, dA, cb, prev = oracle.mamba_prologue(g["x"], g["dt"], g["A"], g["B"], g["C"], Q)
-    out = _mamba_gpu(lh, cb, g["x"], dt, dA, g["C"], g["D"], prev, tile_m=64, tile_n=16)
+    out = _mamba_gpu(lh, cb, g["x"], dt, dA, g["C"], g["D"], prev,
+                     tile_m=tile_for(64, Q, MAMBA_M_TILES), tile_n=16, tile_k=Q)
     assert_close(from_bf16(out), g["expected"], atol=3e-2, rtol=1e-2, what="mamba vs recurrence")
     ref = oracle.mamba_chunk_scan(cb, g["x"], dt, dA, g["C"], g["D"], prev, 16, 16, 16)
     assert_close(from_bf16(out), from_bf16(ref), **ATTN_TOL, what="mamba vs oracle")

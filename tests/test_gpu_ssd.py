@@ -67,7 +67,7 @@ def test_golden_chain_against_recurrence(lh, golden):
     Q = int(g["chunk_size"])
     dt_v, dA, cb, prev = _check_prologue(lh, g["x"], g["dt"], g["A"], g["B"], g["C"], Q, "golden")
     out = lh.helion_mamba2_chunk_scan_kernel(cb, dev(g["x"]), dt_v.contiguous(), dA, dev(g["C"]),
-                                             devf(g["D"]), prev, tile_m=64, tile_n=16)
+                                             devf(g["D"]), prev, tile_m=Q, tile_n=16, tile_k=Q)
     assert_close(from_bf16(host(out)), g["expected"], atol=3e-2, rtol=1e-2,
                  what="GPU prologue + chunk scan vs recurrence")
 
@@ -117,3 +117,47 @@ def test_zero_B_gives_zero_states(lh):
     _, _, cb, prev = lh.ssd_prologue(dev(x), devf(dt), devf(A), dev(Bm), dev(C), 64)
     assert not torch.any(cb.view(torch.int16) != 0)
     assert not torch.any(prev != 0)
+
+
+def _bf16_bits(t):
+    """torch fp32 (CPU) -> numpy bf16 bits, round to nearest even."""
+    return t.to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+
+
+def test_mamba_baseline_full_config(lh):
+    """The BASELINE Mamba-2 config end to end: b4 L4096 h32 P64 N128 g1 Q256
+    (16 chunks, 2048 chunk-scan programs, the full XCD remap and the 16-chunk
+    state carry of the state-passing kernel).  GPU prologue from seeded raw
+    inputs against the oracle's prologue on every (b, c, h); then the GPU
+    chunk scan twice: on the GPU prologue's outputs against the oracle's
+    chain, and on the oracle's prologue outputs against the oracle's scan
+    (isolating the scan).  Every element of every output is compared."""
+    b, H, G, Q, nc, P, N = 4, 32, 1, 256, 16, 64, 128
+    L = nc * Q
+    g = torch.Generator().manual_seed(20240)
+    x = _bf16_bits(torch.randn((b, H, L, P), generator=g))
+    Bm = _bf16_bits(torch.randn((b, G, L, N), generator=g))
+    C = _bf16_bits(torch.randn((b, G, L, N), generator=g))
+    dt = torch.nn.functional.softplus(torch.randn((b, H, L), generator=g)).numpy()
+    A = (-torch.exp(torch.rand(H, generator=g))).numpy()
+    D = torch.randn(H, generator=g).numpy()
+    print("mamba full config: inputs ready", flush=True)
+    dt_v, dA, cb, prev = _check_prologue(lh, x, dt, A, Bm, C, Q, "full config")
+    print("mamba full config: prologue ok", flush=True)
+    D_d = devf(D)
+    out = lh.helion_mamba2_chunk_scan_kernel(cb, dev(x), dt_v.contiguous(), dA, dev(C), D_d, prev,
+                                             tile_m=256, tile_n=64)
+    dt_o, dA_o, cb_o, prev_o = oracle.mamba_prologue(x, dt, A, Bm, C, Q)
+    ref = oracle.mamba_chunk_scan(cb_o, x, dt_o, dA_o, C, D, prev_o, 64, 64, 64)
+    assert_close(from_bf16(host(out)), from_bf16(ref), **ATTN_TOL, what="full config chain")
+    out2 = lh.helion_mamba2_chunk_scan_kernel(dev(cb_o), dev(x), devf(dt_o), devf(dA_o), dev(C),
+                                              D_d, devf(prev_o), tile_m=256, tile_n=64)
+    got2 = host(out2)
+    assert_close(from_bf16(got2), from_bf16(ref), **ATTN_TOL, what="full config scan")
+    # run to run: the same inputs give the same bits
+    out3 = lh.helion_mamba2_chunk_scan_kernel(dev(cb_o), dev(x), devf(dt_o), devf(dA_o), dev(C),
+                                              D_d, devf(prev_o), tile_m=256, tile_n=64)
+    assert np.array_equal(host(out3), got2), "chunk scan not deterministic"
+    _, dA2, cb2, prev2 = lh.ssd_prologue(dev(x), devf(dt), devf(A), dev(Bm), dev(C), Q)
+    assert torch.equal(dA2, dA) and torch.equal(cb2.view(torch.int16), cb.view(torch.int16)) \
+        and torch.equal(prev2, prev), "SSD prologue not deterministic"
