@@ -135,6 +135,23 @@ int loom_hip_flash_decode(const void* k, const void* v, const void* q, void* out
                           int64_t D, int64_t S, float scale, int64_t tile_b, int64_t tile_s,
                           int64_t tile_n, void* stream, char* err, size_t errlen);
 
+/* loom_hip_flash_decode without a workspace argument, for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  It has no counterpart in the
+ * reference.  The split partials go to a static device array of 16 MiB
+ * (16777216 bytes; each device holds its own copy until the process ends),
+ * so loom_hip_flash_decode_workspace_bytes(B, H, D, S, tile_s) must not
+ * exceed it -- larger calls return LOOM_HIP_EINVAL (use a larger tile_s, or
+ * loom_hip_flash_decode).  Nothing is allocated and no allocating routine is
+ * called.  Every call on a device shares that device's array: calls that
+ * overlap in time on one device (different streams, concurrent threads)
+ * race and must be ordered by the caller.  bf16 only; arguments, validation
+ * and results otherwise as loom_hip_flash_decode. */
+int loom_hip_flash_decode_noalloc(const void* k, const void* v, const void* q, void* out,
+                                  int64_t B, int64_t H, int64_t D, int64_t S, float scale,
+                                  int64_t tile_b, int64_t tile_s, int64_t tile_n, void* stream,
+                                  char* err, size_t errlen);
+
 /* @helion_mamba2_chunk_scan_kernel -- examples/mamba_chunk_scan/IR/00_from_helion_frontend.mlir:4
  *   (cb: [b,c,G,Q,Q] bf16, x: [b,H,L,P] bf16, dt: [b,H,c,Q] fp32,
  *    dA_cumsum: [b,H,c,Q] fp32, C: [b,G,L,N] bf16, D: [H] fp32,

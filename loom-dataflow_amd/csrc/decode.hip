@@ -28,6 +28,7 @@
 #include "common.h"
 
 #include <cmath>
+#include <mutex>
 
 namespace {
 
@@ -426,9 +427,92 @@ int flash_decode_impl(const void* k, const void* v, const void* q, void* out,
   return loom_check_launch(err, errlen, "flash_decode (combine)");
 }
 
+// ---------------------------------------------------------------------------
+// Allocation-free form (loom_hip_flash_decode_noalloc): the split partials go
+// to `scratch`, a file-scope device array, instead of a caller workspace.
+// Every device the library runs on holds its own copy until the process
+// ends.  In host code `scratch` names a host-side stand-in, never device
+// memory: its address on a device comes from hipGetSymbolAddress, taken once
+// per device with that device current and kept in g_scratch.
+// ---------------------------------------------------------------------------
+constexpr size_t kScratchBytes = (size_t)16 << 20;   // 16 MiB of split partials
+
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::once_flag g_scratch_once[kMaxDevices];
+void* g_scratch[kMaxDevices];
+hipError_t g_scratch_rc[kMaxDevices];
+
+// Device address of `scratch` on the device `stream` belongs to (the current
+// device for the null stream).
+int scratch_on(void* stream, void** ptr, char* err, size_t errlen) {
+  int dev = 0;
+  hipError_t e = hipSuccess;
+  if (stream != nullptr) {
+    hipDevice_t d = 0;
+    e = hipStreamGetDevice(static_cast<hipStream_t>(stream), &d);
+    dev = (int)d;
+  } else {
+    e = hipGetDevice(&dev);
+  }
+  if (e != hipSuccess)
+    return loom_fail(err, errlen, LOOM_EHIP, "flash_decode_noalloc: no device for the stream: %s",
+                     hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices)
+    return loom_fail(err, errlen, LOOM_EUNSUP, "flash_decode_noalloc: device %d above %d", dev,
+                     kMaxDevices - 1);
+  std::call_once(g_scratch_once[dev], [dev] {
+    int cur = 0;
+    hipError_t r = hipGetDevice(&cur);
+    if (r == hipSuccess && cur != dev) r = hipSetDevice(dev);
+    void* ptr = nullptr;
+    if (r == hipSuccess) r = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (cur != dev) (void)hipSetDevice(cur);
+    g_scratch[dev] = ptr;
+    g_scratch_rc[dev] = r;
+  });
+  if (g_scratch_rc[dev] != hipSuccess || g_scratch[dev] == nullptr)
+    return loom_fail(err, errlen, LOOM_EHIP,
+                     "flash_decode_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s",
+                     dev, hipGetErrorString(g_scratch_rc[dev]));
+  *ptr = g_scratch[dev];
+  return LOOM_OK;
+}
+
 }  // namespace
 
 extern "C" {
+
+int loom_hip_flash_decode_noalloc(const void* k, const void* v, const void* q, void* out,
+                                  int64_t B, int64_t H, int64_t D, int64_t S, float scale,
+                                  int64_t tile_b, int64_t tile_s, int64_t tile_n, void* stream,
+                                  char* err, size_t errlen) {
+  // every check of the workspace form first (validate-only, with a stand-in
+  // workspace of the scratch's size), so a rejected call touches no device
+  const size_t need = loom_hip_flash_decode_workspace_bytes(B, H, D, S, tile_s);
+  if (need > kScratchBytes)
+    return loom_fail(err, errlen, LOOM_EINVAL,
+                     "flash_decode_noalloc: the split partials need %zu bytes, the static scratch "
+                     "holds %zu (fewer splits: a larger tile_s)",
+                     need, kScratchBytes);
+  bool& vo = loom_validate_only_flag();
+  const bool outer = vo;
+  vo = true;
+  int rc = flash_decode_impl<false>(k, v, q, out, reinterpret_cast<void*>(uintptr_t(1) << 20),
+                                    kScratchBytes, B, H, D, S, scale, tile_b, tile_s, tile_n,
+                                    stream, err, errlen);
+  vo = outer;
+  if (rc || outer) return rc;
+  void* ptr = nullptr;
+  if ((rc = scratch_on(stream, &ptr, err, errlen))) return rc;
+  return flash_decode_impl<false>(k, v, q, out, ptr, kScratchBytes, B, H, D, S, scale, tile_b,
+                                  tile_s, tile_n, stream, err, errlen);
+}
 
 size_t loom_hip_flash_decode_workspace_bytes(int64_t B, int64_t H, int64_t D, int64_t S,
                                              int64_t tile_s) {

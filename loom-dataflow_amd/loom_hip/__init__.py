@@ -44,6 +44,7 @@ _SIGS = {
     + [_vp, *_ERR],
     "loom_hip_flash_decode": [_vp] * 5 + [_sz] + [_i64] * 4 + [_f32] + [_i64] * 3
     + [_vp, *_ERR],
+    "loom_hip_flash_decode_noalloc": [_vp] * 4 + [_i64] * 4 + [_f32] + [_i64] * 3 + [_vp, *_ERR],
     "loom_hip_helion_mamba2_chunk_scan_kernel": [_vp] * 8 + [_i64] * 13 + [_vp, *_ERR],
     "loom_hip_ssd_chunk_cumsum": [_vp] * 3 + [_i64] * 4 + [_vp, *_ERR],
     "loom_hip_ssd_bmm_chunk": [_vp] * 3 + [_i64] * 5 + [_vp, *_ERR],
@@ -366,6 +367,28 @@ def flash_decode(k, v, q, out=None, workspace=None, *, scale=None, tile_b=None, 
     lse = workspace[:n_lse * 4].view(torch.float32).view(ns, B, H)
     o = workspace[off:off + n_lse * D * 4].view(torch.float32).view(ns, B, H, D)
     return out, lse, o
+
+
+#: bytes of the static device scratch loom_hip_flash_decode_noalloc keeps its
+#: split partials in (one copy per device)
+NOALLOC_SCRATCH_BYTES = 16 << 20
+
+
+def flash_decode_noalloc(k, v, q, out, *, scale=None, tile_b=None, tile_s=None, tile_n=None):
+    """flash_decode without a workspace: the split partials live in the
+    library's static per-device scratch (``NOALLOC_SCRATCH_BYTES``), nothing is
+    allocated (``out`` must be given).  Calls that overlap in time on one
+    device share that scratch and race.  bf16 only."""
+    dims = _dims_of("flash_decode", (k, v, q))
+    B, H, D, S = dims
+    tile_b, tile_s, tile_n = _tiles("flash_decode", dims, tile_b=tile_b, tile_s=tile_s,
+                                    tile_n=tile_n)
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    ptrs = _check_call("flash_decode", (k, v, q, out), dims, _bf16)
+    _call("loom_hip_flash_decode_noalloc", *ptrs, B, H, D, S, float(scale), tile_b, tile_s, tile_n,
+          _stream(q))
+    return out
 
 
 def helion_mamba2_chunk_scan_kernel(cb, x, dt, dA_cumsum, C, D, prev_states_T, out=None, *,

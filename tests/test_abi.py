@@ -166,6 +166,25 @@ def test_flash_decode_rejections(lh):
         assert rc == 1 and "scale" in msg, bad
 
 
+def test_flash_decode_noalloc_rejections(lh):
+    """The allocation-free decode keeps its partials in a 16 MiB static
+    scratch: a call needing more is refused before anything touches a device
+    (the scratch lookup itself would fail here, without a GPU, with code 3)."""
+    B, H, D, S = 32, 32, 128, 8192
+    assert lh.flash_decode_workspace_bytes(B, H, D, S, 1024) <= lh.NOALLOC_SCRATCH_BYTES
+    assert lh.flash_decode_workspace_bytes(B, H, D, S, 256) > lh.NOALLOC_SCRATCH_BYTES
+    rc, msg = _call(lh, "loom_hip_flash_decode_noalloc", FAKE, FAKE, FAKE, FAKE, B, H, D, S, 0.1,
+                    1, 256, 64, None)
+    assert rc == 1 and "scratch" in msg, (rc, msg)
+    # the workspace form's own checks run first too
+    rc, msg = _call(lh, "loom_hip_flash_decode_noalloc", FAKE, FAKE, FAKE, FAKE, B, 64, D, S, 0.1,
+                    1, 1024, 64, None)
+    assert rc == 2 and "heads" in msg, (rc, msg)
+    rc, msg = _call(lh, "loom_hip_flash_decode_noalloc", FAKE, FAKE, FAKE, FAKE, B, H, D, S, -1.0,
+                    1, 1024, 64, None)
+    assert rc == 1 and "scale" in msg, (rc, msg)
+
+
 def test_mamba_rejections(lh):
     dims = [1, 2, 4, 1, 64, 64, 128]
     rc, msg = _call(lh, "loom_hip_helion_mamba2_chunk_scan_kernel", *([FAKE] * 8), *dims,
