@@ -264,6 +264,107 @@ int loom_hip_ssd_prologue_f16(const void* x, const void* dt, const void* A, cons
                               int64_t chunk_size, int64_t headdim, int64_t dstate, void* stream,
                               char* err, size_t errlen);
 
+/* ---- MLIR memref descriptors ---------------------------------------------
+ * A materialized variant is an MLIR function over memrefs; a caller lowered
+ * through MLIR's C interface (`_mlir_ciface_<func>`, whose arguments are
+ * pointers to ranked descriptors -- StridedMemRefType<T, R> of MLIR's C
+ * runner utilities) holds exactly these structs: the allocated and aligned
+ * base pointers, the element offset, and sizes and strides in elements.
+ * The loom_hip_ciface_* entry points take them in the MLIR function's
+ * argument order (extents come from the sizes; the data pointer is
+ * aligned + offset elements) and launch the same kernels as the pointer
+ * entry points above.  Every argument must be row-major contiguous:
+ * innermost stride 1 and each outer stride the product of the sizes inside
+ * it (a dimension of size 1 is never stepped over, so its stride is free);
+ * other layouts, sizes that disagree between arguments, a null aligned
+ * pointer or a negative offset return LOOM_HIP_EINVAL with a message naming
+ * the argument.  Element types: 16-bit tensors bf16 (f16 in the _f16 forms);
+ * mamba's dt, dA_cumsum, D and prev_states_T fp32 (f16 in the _f16 form). */
+typedef struct loom_memref1 { void* allocated; void* aligned; int64_t offset; int64_t sizes[1]; int64_t strides[1]; } loom_memref1_t;
+typedef struct loom_memref2 { void* allocated; void* aligned; int64_t offset; int64_t sizes[2]; int64_t strides[2]; } loom_memref2_t;
+typedef struct loom_memref3 { void* allocated; void* aligned; int64_t offset; int64_t sizes[3]; int64_t strides[3]; } loom_memref3_t;
+typedef struct loom_memref4 { void* allocated; void* aligned; int64_t offset; int64_t sizes[4]; int64_t strides[4]; } loom_memref4_t;
+typedef struct loom_memref5 { void* allocated; void* aligned; int64_t offset; int64_t sizes[5]; int64_t strides[5]; } loom_memref5_t;
+
+/* @matmul (x, y, out) -- examples/mm/IR/00_from_helion_frontend.mlir:2 */
+int loom_hip_ciface_matmul(const loom_memref2_t* x, const loom_memref2_t* y,
+                           const loom_memref2_t* out, int64_t tile_m, int64_t tile_n,
+                           int64_t tile_k, void* stream, char* err, size_t errlen);
+int loom_hip_ciface_matmul_f16(const loom_memref2_t* x, const loom_memref2_t* y,
+                               const loom_memref2_t* out, int64_t tile_m, int64_t tile_n,
+                               int64_t tile_k, void* stream, char* err, size_t errlen);
+/* @batch_matmul (arg0, arg1, arg2) -- examples/bmm_2Dmesh/IR/00_from_helion_frontend.mlir:4 */
+int loom_hip_ciface_batch_matmul(const loom_memref3_t* arg0, const loom_memref3_t* arg1,
+                                 const loom_memref3_t* arg2, int64_t tile_b, int64_t tile_m,
+                                 int64_t tile_n, int64_t tile_k, void* stream, char* err,
+                                 size_t errlen);
+int loom_hip_ciface_batch_matmul_f16(const loom_memref3_t* arg0, const loom_memref3_t* arg1,
+                                     const loom_memref3_t* arg2, int64_t tile_b, int64_t tile_m,
+                                     int64_t tile_n, int64_t tile_k, void* stream, char* err,
+                                     size_t errlen);
+/* @split_k_matmul_gather (a, b, out) -- examples/split_k_mm_gather/IR/00_from_helion_frontend.mlir:2;
+ * the gathered partial stack stays a workspace as for the pointer form. */
+int loom_hip_ciface_split_k_matmul_gather(const loom_memref2_t* a, const loom_memref2_t* b,
+                                          const loom_memref2_t* out, void* partials,
+                                          size_t partials_bytes, int64_t tile_m, int64_t tile_n,
+                                          int64_t tile_k, void* stream, char* err, size_t errlen);
+int loom_hip_ciface_split_k_matmul_gather_f16(const loom_memref2_t* a, const loom_memref2_t* b,
+                                              const loom_memref2_t* out, void* partials,
+                                              size_t partials_bytes, int64_t tile_m,
+                                              int64_t tile_n, int64_t tile_k, void* stream,
+                                              char* err, size_t errlen);
+/* @attention (k, v, q, out) -- examples/flashattn/IR/00_from_helion_frontend.mlir:4 */
+int loom_hip_ciface_attention(const loom_memref3_t* k, const loom_memref3_t* v,
+                              const loom_memref3_t* q, const loom_memref3_t* out, float scale,
+                              int causal, int64_t tile_b, int64_t tile_m, int64_t tile_n,
+                              void* stream, char* err, size_t errlen);
+int loom_hip_ciface_attention_f16(const loom_memref3_t* k, const loom_memref3_t* v,
+                                  const loom_memref3_t* q, const loom_memref3_t* out, float scale,
+                                  int causal, int64_t tile_b, int64_t tile_m, int64_t tile_n,
+                                  void* stream, char* err, size_t errlen);
+/* @flash_decode (k, v, q, out) -- examples/mqa_decode/IR/00_from_helion_frontend.mlir:6 */
+int loom_hip_ciface_flash_decode(const loom_memref3_t* k, const loom_memref3_t* v,
+                                 const loom_memref3_t* q, const loom_memref3_t* out,
+                                 void* workspace, size_t workspace_bytes, float scale,
+                                 int64_t tile_b, int64_t tile_s, int64_t tile_n, void* stream,
+                                 char* err, size_t errlen);
+int loom_hip_ciface_flash_decode_f16(const loom_memref3_t* k, const loom_memref3_t* v,
+                                     const loom_memref3_t* q, const loom_memref3_t* out,
+                                     void* workspace, size_t workspace_bytes, float scale,
+                                     int64_t tile_b, int64_t tile_s, int64_t tile_n, void* stream,
+                                     char* err, size_t errlen);
+/* @helion_mamba2_chunk_scan_kernel (cb, x, dt, dA_cumsum, C, D, prev_states_T, out) --
+ * examples/mamba_chunk_scan/IR/00_from_helion_frontend.mlir:4 */
+int loom_hip_ciface_helion_mamba2_chunk_scan_kernel(
+    const loom_memref5_t* cb, const loom_memref4_t* x, const loom_memref4_t* dt,
+    const loom_memref4_t* dA_cumsum, const loom_memref4_t* C, const loom_memref1_t* D,
+    const loom_memref5_t* prev_states_T, const loom_memref4_t* out, int64_t tile_b,
+    int64_t tile_h, int64_t tile_c, int64_t tile_m, int64_t tile_n, int64_t tile_k, void* stream,
+    char* err, size_t errlen);
+int loom_hip_ciface_helion_mamba2_chunk_scan_kernel_f16(
+    const loom_memref5_t* cb, const loom_memref4_t* x, const loom_memref4_t* dt,
+    const loom_memref4_t* dA_cumsum, const loom_memref4_t* C, const loom_memref1_t* D,
+    const loom_memref5_t* prev_states_T, const loom_memref4_t* out, int64_t tile_b,
+    int64_t tile_h, int64_t tile_c, int64_t tile_m, int64_t tile_n, int64_t tile_k, void* stream,
+    char* err, size_t errlen);
+
+/* loom_hip_dispatch over descriptors: `descs` points to the function's
+ * memref descriptors in IR order, each of the rank its argument has
+ * (loom_memref<R>_t); extents come from them.  Otherwise as
+ * loom_hip_dispatch (the workspace carries split-K's partials or decode's
+ * gathered splits). */
+int loom_hip_dispatch_memref(const char* variant, const void* const* descs, int ndescs,
+                             float scale, int causal, void* workspace, size_t workspace_bytes,
+                             void* stream, char* err, size_t errlen);
+int loom_hip_dispatch_memref_f16(const char* variant, const void* const* descs, int ndescs,
+                                 float scale, int causal, void* workspace, size_t workspace_bytes,
+                                 void* stream, char* err, size_t errlen);
+/* Validates a descriptor call of loom_hip_dispatch_memref (f16 != 0: the
+ * _f16 form) exactly as it would run -- descriptors, layouts, shapes, tiles,
+ * scale -- and launches nothing (no device is needed). */
+int loom_hip_check_memref(const char* variant, const void* const* descs, int ndescs, int f16,
+                          float scale, char* err, size_t errlen);
+
 /* ---- materialization contract and by-name dispatch ---------------------- */
 
 /* Variant names the materialization pipeline emits for `funcs` under the

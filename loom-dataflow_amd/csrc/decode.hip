@@ -387,7 +387,7 @@ int flash_decode_impl(const void* k, const void* v, const void* q, void* out,
                      (long long)H);
   if (S * D * 2 > 0x7fffffffll || B > 65535)
     return loom_fail(err, errlen, LOOM_EINVAL, "flash_decode: S*D or B too large");
-  if (!aligned16(k) || !aligned16(v) || !aligned16(q))
+  if (!aligned16(k) || !aligned16(v) || !aligned16(q) || !aligned16(out))
     return loom_fail(err, errlen, LOOM_EINVAL, "flash_decode: tensors must be 16-byte aligned");
   const int64_t ns = cdiv64(S, tile_s);
   const size_t need = loom_hip_flash_decode_workspace_bytes(B, H, D, S, tile_s);

@@ -1147,7 +1147,9 @@ int matmul_impl(const void* x, const void* y, void* out, int64_t M, int64_t N, i
   p.k_slab = K;
   p.split = 0;
   p.nz = 1;
-  const bool al = K % 8 == 0 && N % 8 == 0 && aligned16(x) && aligned16(y);
+  // the vector-store kernels also need a 16-byte-aligned C; others take the
+  // register-staged kernel (element stores)
+  const bool al = K % 8 == 0 && N % 8 == 0 && aligned16(x) && aligned16(y) && aligned16(out);
   if (loom_validate_only()) return loom_ok(err, errlen);
   (void)launch_gemm<H>(p, wg, wg, al, false, static_cast<hipStream_t>(stream));
   return loom_check_launch(err, errlen, "matmul");
@@ -1186,7 +1188,8 @@ int batch_matmul_impl(const void* arg0, const void* arg1, void* arg2, int64_t Bt
   p.k_slab = K;
   p.split = 0;
   p.nz = (int)Bt;
-  const bool al = K % 8 == 0 && N % 8 == 0 && aligned16(arg0) && aligned16(arg1);
+  const bool al =
+      K % 8 == 0 && N % 8 == 0 && aligned16(arg0) && aligned16(arg1) && aligned16(arg2);
   if (loom_validate_only()) return loom_ok(err, errlen);
   (void)launch_gemm<H>(p, wg, wg, al, false, static_cast<hipStream_t>(stream));
   return loom_check_launch(err, errlen, "batch_matmul");
@@ -1225,7 +1228,8 @@ int split_k_matmul_gather_impl(const void* a, const void* b, void* out, void* pa
   p.k_slab = tile_k;
   p.split = 1;
   p.nz = (int)S;
-  const bool al = K % 8 == 0 && N % 8 == 0 && tile_k % 8 == 0 && aligned16(a) && aligned16(b);
+  const bool al = K % 8 == 0 && N % 8 == 0 && tile_k % 8 == 0 && aligned16(a) && aligned16(b) &&
+                  aligned16(partials);
   if (loom_validate_only()) return loom_ok(err, errlen);
   (void)launch_gemm<H>(p, wg, wg, al, true, st);
   rc = loom_check_launch(err, errlen, "split_k_matmul_gather (slab GEMM)");

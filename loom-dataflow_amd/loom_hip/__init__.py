@@ -85,7 +85,41 @@ for _fn in ("loom_hip_constraint_scope", "loom_hip_preferred_block_sizes"):
                                    ctypes.c_char_p, _sz, *_ERR]
     getattr(_lib, _fn).restype = ctypes.c_int
 
-EXPORTED = tuple(_SIGS) + ("loom_hip_split_k_workspace_bytes",
+# MLIR ranked memref descriptors {allocated, aligned, offset, sizes[R], strides[R]}
+# (loom_memref<R>_t in include/loom_hip.h)
+MEMREF = {}
+for _r in range(1, 6):
+    MEMREF[_r] = type(f"loom_memref{_r}_t", (ctypes.Structure,), {"_fields_": [
+        ("allocated", _vp), ("aligned", _vp), ("offset", _i64), ("sizes", _i64 * _r),
+        ("strides", _i64 * _r)]})
+_MP = {r: ctypes.POINTER(MEMREF[r]) for r in MEMREF}
+# descriptor ranks of each function's arguments, in IR order
+_RANKS = {"matmul": (2, 2, 2), "batch_matmul": (3, 3, 3), "split_k_matmul_gather": (2, 2, 2),
+          "attention": (3, 3, 3, 3), "flash_decode": (3, 3, 3, 3),
+          "helion_mamba2_chunk_scan_kernel": (5, 4, 4, 4, 4, 1, 5, 4)}
+_CIFACE_TAIL = {"matmul": [_i64] * 3, "batch_matmul": [_i64] * 4,
+                "split_k_matmul_gather": [_vp, _sz] + [_i64] * 3,
+                "attention": [_f32, ctypes.c_int] + [_i64] * 3,
+                "flash_decode": [_vp, _sz, _f32] + [_i64] * 3,
+                "helion_mamba2_chunk_scan_kernel": [_i64] * 6}
+_CIFACE = []
+for _f, _ranks in _RANKS.items():
+    for _sfx in ("", "_f16"):
+        _n = "loom_hip_ciface_" + _f + _sfx
+        getattr(_lib, _n).argtypes = [_MP[r] for r in _ranks] + _CIFACE_TAIL[_f] + [_vp, *_ERR]
+        getattr(_lib, _n).restype = ctypes.c_int
+        _CIFACE.append(_n)
+for _n in ("loom_hip_dispatch_memref", "loom_hip_dispatch_memref_f16"):
+    getattr(_lib, _n).argtypes = [ctypes.c_char_p, ctypes.POINTER(_vp), ctypes.c_int, _f32,
+                                  ctypes.c_int, _vp, _sz, _vp, *_ERR]
+    getattr(_lib, _n).restype = ctypes.c_int
+_lib.loom_hip_check_memref.argtypes = [ctypes.c_char_p, ctypes.POINTER(_vp), ctypes.c_int,
+                                       ctypes.c_int, _f32, *_ERR]
+_lib.loom_hip_check_memref.restype = ctypes.c_int
+
+EXPORTED = tuple(_SIGS) + tuple(_CIFACE) + ("loom_hip_dispatch_memref",
+                                            "loom_hip_dispatch_memref_f16",
+                                            "loom_hip_check_memref") + ("loom_hip_split_k_workspace_bytes",
                            "loom_hip_flash_decode_workspace_bytes", "loom_hip_version",
                            "loom_hip_materialize_variants", "loom_hip_parse_variant",
                            "loom_hip_dispatch", "loom_hip_dispatch_f16", "loom_hip_check_variant",
@@ -565,3 +599,91 @@ def constraint_scope(func: str, dims) -> dict:
 def preferred_block_sizes(func: str, dims) -> dict:
     """The binding this library runs fastest for these extents."""
     return _json_call("loom_hip_preferred_block_sizes", func, dims)
+
+
+# ---------------------------------------------------------------------------
+# MLIR memref descriptors: the _mlir_ciface_ form of every function
+# ---------------------------------------------------------------------------
+
+def memref(t: torch.Tensor, offset: int = 0, base: torch.Tensor = None, strides=None):
+    """A ranked memref descriptor (``MEMREF[t.dim()]``) for tensor ``t``.  With
+    ``base`` given, the descriptor's allocated/aligned pointer is ``base``'s
+    and ``offset`` is ``t``'s element offset from it (``t`` must lie inside
+    ``base``); ``strides`` overrides the strides (in elements)."""
+    r = t.dim()
+    d = MEMREF[r]()
+    if base is None:
+        ptr, off = t.data_ptr(), offset
+    else:
+        ptr = base.data_ptr()
+        off = (t.data_ptr() - ptr) // t.element_size()
+    d.allocated = d.aligned = ptr
+    d.offset = off
+    for i in range(r):
+        d.sizes[i] = t.shape[i]
+        d.strides[i] = (strides if strides is not None else t.stride())[i]
+    return d
+
+
+def _desc_array(descs):
+    keep = list(descs)
+    arr = (_vp * max(len(keep), 1))(*[ctypes.cast(ctypes.pointer(d), _vp) for d in keep])
+    return arr, keep
+
+
+def ciface(func: str, *descs, f16=False, workspace=None, workspace_bytes=0, scale=1.0,
+           causal=False, stream=None, **tiles):
+    """Calls ``loom_hip_ciface_<func>`` (``_f16`` with ``f16``) on memref
+    descriptors in IR order; tiles as keywords (``tile_m=...``)."""
+    name = "loom_hip_ciface_" + func + ("_f16" if f16 else "")
+    fn = getattr(_lib, name)
+    ptrs = [ctypes.pointer(d) for d in descs]
+    order = {"matmul": ("tile_m", "tile_n", "tile_k"),
+             "batch_matmul": ("tile_b", "tile_m", "tile_n", "tile_k"),
+             "split_k_matmul_gather": ("tile_m", "tile_n", "tile_k"),
+             "attention": ("tile_b", "tile_m", "tile_n"),
+             "flash_decode": ("tile_b", "tile_s", "tile_n"),
+             "helion_mamba2_chunk_scan_kernel": ("tile_b", "tile_h", "tile_c", "tile_m", "tile_n",
+                                                 "tile_k")}[func]
+    t = [int(tiles[k]) for k in order]
+    if stream is None:
+        stream = torch.cuda.current_stream().cuda_stream if torch.cuda.is_available() else None
+    ws = workspace.data_ptr() if isinstance(workspace, torch.Tensor) else workspace
+    wsb = workspace.numel() if isinstance(workspace, torch.Tensor) else workspace_bytes
+    if func == "split_k_matmul_gather":
+        args = [*ptrs, ws, wsb, *t]
+    elif func == "attention":
+        args = [*ptrs, float(scale), int(bool(causal)), *t]
+    elif func == "flash_decode":
+        args = [*ptrs, ws, wsb, float(scale), *t]
+    else:
+        args = [*ptrs, *t]
+    _call(name, *args, stream)
+
+
+def dispatch_memref(variant: str, *descs, f16=False, workspace=None, scale=1.0, causal=False,
+                    stream=None):
+    """Runs a materialized variant on memref descriptors through
+    ``loom_hip_dispatch_memref`` (``_f16`` with ``f16``)."""
+    arr, _keep = _desc_array(descs)
+    if stream is None:
+        stream = torch.cuda.current_stream().cuda_stream if torch.cuda.is_available() else None
+    ws = workspace.data_ptr() if workspace is not None else None
+    wsb = workspace.numel() if workspace is not None else 0
+    fn = _lib.loom_hip_dispatch_memref_f16 if f16 else _lib.loom_hip_dispatch_memref
+    err = ctypes.create_string_buffer(512)
+    rc = fn(variant.encode(), arr, len(descs), float(scale), int(bool(causal)), ws, wsb, stream,
+            err, len(err))
+    if rc != 0:
+        raise LoomHipError("loom_hip_dispatch_memref", rc, err.value.decode(errors="replace"))
+
+
+def check_memref(variant: str, *descs, f16=False, scale=1.0):
+    """Raises ``LoomHipError`` if ``loom_hip_dispatch_memref`` would reject the
+    call; launches nothing (no GPU needed)."""
+    arr, _keep = _desc_array(descs)
+    err = ctypes.create_string_buffer(512)
+    rc = _lib.loom_hip_check_memref(variant.encode(), arr, len(descs), int(bool(f16)),
+                                    float(scale), err, len(err))
+    if rc != 0:
+        raise LoomHipError("loom_hip_check_memref", rc, err.value.decode(errors="replace"))
