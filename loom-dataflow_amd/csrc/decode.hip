@@ -46,78 +46,329 @@ struct DecodeParams {
   float c2;    // scale * log2(e)
 };
 
-// Split-0 combine of the reference (:147-199), one wave per (b, head):
-// lane s < 64 holds lse_s, M = max_s lse_s and den = sum_s exp(lse_s - M)
-// are wave reductions, then every lane accumulates out[d] = sum_s w_s o_s[d]
-// (w_s = exp(lse_s - M) / den, ascending s) for its D/64 values of d with
-// eight splits' loads in flight at a time.  Splits beyond 64 are taken in
-// chunks of 64.
+// Split-0 combine of the reference (:147-199): M = max_s lse_s,
+// w_s = exp(lse_s - M) / sum_s exp(lse_s - M), out = sum_s w_s o_s (ascending
+// s).  One thread per two consecutive d of one (b, head): every split's lse
+// and o loads are independent and issued together (in chunks of 16 splits),
+// so the combine costs about one memory round trip.
 template <int D, bool F16>
 __global__ void __launch_bounds__(256) decode_combine_kernel(DecodeParams p) {
-  constexpr int DPL = D / 64;  // d values per lane
-  const int lane = threadIdx.x & 63;
+  constexpr int TPR = D / 2;   // threads per (b, head) row
   const int64_t BH = (int64_t)p.B * p.H;
-  const int64_t bh = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t bh = t / TPR;
   if (bh >= BH) return;
+  const int d = (int)(t % TPR) * 2;
   const int ns = p.ns;
-  float M = -INFINITY;
-  for (int s = lane; s < ns; s += 64) M = fmaxf(M, p.lse[s * BH + bh]);
-  M = wave_max(M);
-  float den = 0.f;
-  for (int s = lane; s < ns; s += 64) den += expf(p.lse[s * BH + bh] - M);
-  den = wave_sum(den);
-  float acc[DPL];
+  constexpr int CH = 16;
+  // every load of a chunk of CH splits is issued before any is used; across
+  // chunks the running max moves and the sums rescale (one chunk at BASELINE
+  // shapes, so one memory round trip)
+  float M = -INFINITY, den = 0.f, a0 = 0.f, a1 = 0.f;
+  for (int c0 = 0; c0 < ns; c0 += CH) {
+    float l[CH];
+    f32x2_t o[CH];
 #pragma unroll
-  for (int i = 0; i < DPL; ++i) acc[i] = 0.f;
-  for (int c0 = 0; c0 < ns; c0 += 64) {
-    const int sl = c0 + lane;
-    const float wl = sl < ns ? expf(p.lse[sl * BH + bh] - M) / den : 0.f;
-    const int cn = min(64, ns - c0);
-    for (int u0 = 0; u0 < cn; u0 += 8) {
-      float v[8][DPL];
+    for (int u = 0; u < CH; ++u) {
+      const int64_t s = min(c0 + u, ns - 1);   // clamped: weight 0 past the end
+      l[u] = p.lse[s * BH + bh];
+      o[u] = *reinterpret_cast<const f32x2_t*>(p.o + (s * BH + bh) * D + d);
+    }
+    float mc = M;
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int s = c0 + min(u0 + u, cn - 1);  // clamped: weight 0 past the end
-        const float* src = p.o + (s * BH + bh) * D + lane * DPL;
+    for (int u = 0; u < CH; ++u) mc = fmaxf(mc, l[u]);
+    const float r = expf(M - mc);   // 0 on the first chunk (M = -inf)
+    den *= r;
+    a0 *= r;
+    a1 *= r;
+    M = mc;
 #pragma unroll
-        for (int i = 0; i < DPL; ++i) v[u][i] = src[i];
+    for (int u = 0; u < CH; ++u) {
+      const float w = c0 + u < ns ? expf(l[u] - M) : 0.f;
+      den += w;
+      a0 += w * o[u][0];
+      a1 += w * o[u][1];
+    }
+  }
+  const float inv = 1.f / den;
+  *reinterpret_cast<uint32_t*>(p.out + bh * D + d) = pack2<F16>(a0 * inv, a1 * inv);
+}
+
+// ---------------------------------------------------------------------------
+// Split kernel, LDS-DMA form (the production path: S a multiple of 8,
+// H <= 32).  One workgroup of four waves per (batch, split).  K and V of the
+// split stream through LDS in 64-key stages copied by LDS DMA
+// (global_load_lds_dwordx4), four stages deep: up to 96 KB per workgroup in
+// flight with no registers held by loads, which is what streaming HBM at
+// full rate takes.  Ks is [d][key] and Vs [key][d], as the tensors lay them
+// out; the MFMA operands that need k-contiguous data come from
+// ds_read_b64_tr_b16:
+//   S^T[key, h]  = K^T . Q^T : row operand K^T from Ks (lane r: key, eight
+//                              consecutive d), column operand Q^T (16 heads);
+//   O^T[d, h]   += V^T . P^T : row operand V^T from Vs (lane r: d, keys
+//                              4 g + 0..3 and 16 + 4 g + 0..3 of a 32-key half),
+//                              the keys P^T holds in lane group g.
+// Wave w takes the 32-key half kh = w & 1 of every stage for the heads of
+// tile ht = w >> 1 (16 heads; 32 head slots in all, slots past H are zero
+// queries and never stored), with an online softmax of its own in the log2
+// domain whose base only moves when a score rises 8 above it (P <= 2^8; the
+// row sum is an MFMA of the same bf16 P against ones, so numerator and
+// denominator see identical weights).  At the end the two halves of each
+// head tile merge through the (then idle) stage LDS into (lse_s, o_s).
+// Blocks start at the split's first key rounded down to a multiple of 8;
+// keys outside [s0, s1) are masked to -inf, reads past S are clamped.
+// ---------------------------------------------------------------------------
+// 16-byte chunk swizzles of the Ks and Vs rows (as in attention.hip): each
+// 32-lane pass of a transposed read touches 32 distinct 16-byte slots of the
+// 512-byte LDS bank window.
+LOOM_DEV int dk_swz(int d) { return 2 * ((d >> 3) & 1); }
+LOOM_DEV int dv_swz(int k) { return 2 * ((k >> 1) & 3); }
+
+template <int D, bool F16>
+__global__ void __launch_bounds__(256) decode_dma_kernel(DecodeParams p) {
+  constexpr int KB = 64;                       // keys per stage
+  constexpr int NS = 4;                        // stages
+  constexpr int W = 4;
+  constexpr int K_BYTES = D * KB * 2, V_BYTES = KB * D * 2;
+  constexpr int K_INSTR = K_BYTES / 1024 / W, V_INSTR = V_BYTES / 1024 / W;
+  constexpr int LPW = K_INSTR + V_INSTR;       // DMA instructions per wave per stage
+  constexpr int VROW = D * 2, V_ROWS_PER_I = 1024 / VROW;
+  constexpr int DSTEPS = D / 32, DT = D / 16;
+  static_assert(LPW * (NS - 2) <= 63, "vmcnt range");
+  constexpr int STAGE = K_BYTES + V_BYTES;
+  constexpr int ROW = D + 4;                   // merge row: D o values, m, l (16-byte rows)
+  constexpr int MERGE = W * 16 * ROW * 4;      // per wave: 16 heads
+  static_assert(MERGE <= NS * STAGE, "merge area fits the stage ring");
+  constexpr int Q_BYTES = 32 * D * 2;          // 32 head slots of q
+  constexpr int Q_INSTR = Q_BYTES / 1024 / W;
+  __shared__ __attribute__((aligned(1024))) char smem[NS * STAGE + Q_BYTES];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = lane & 15, g = lane >> 4;
+  const int a4 = r >> 2, c4 = r & 3;           // transposed-read lane roles
+  const int kh = wave & 1, ht = wave >> 1;
+
+  const int split = blockIdx.x, b = blockIdx.y;
+  const int H = p.H, S = p.S;
+  const int s0 = split * p.tile_s;
+  const int s1 = min(S, s0 + p.tile_s);
+  const int kbeg = s0 & ~7;                    // 16-byte aligned first key
+  const int nblk = (s1 - kbeg + KB - 1) / KB;
+  const uint16_t* __restrict__ kg = p.k + (int64_t)b * D * S;
+  const uint16_t* __restrict__ vg = p.v + (int64_t)b * S * D;
+
+  auto stK = [&](int s) { return (lds_char_t*)(smem + s * STAGE); };
+  auto stV = [&](int s) { return (lds_char_t*)(smem + s * STAGE + K_BYTES); };
+  // ---- DMA of block `blk` into stage s (reads past S clamped; masked later)
+  auto issue = [&](int s, int blk) {
+    const int kv0 = kbeg + blk * KB;
+    const uint32_t lk = lds_addr(stK(s)), lv = lds_addr(stV(s));
+#pragma unroll
+    for (int i = 0; i < K_INSTR; ++i) {
+      const int j = wave * K_INSTR + i;
+      const int d = j * 8 + lane / 8;                   // Ks row
+      const int c = (lane % 8) ^ dk_swz(d);
+      const int key = min(kv0 + c * 8, S - 8);
+      dma_load16(kg + (int64_t)d * S + key, lk + j * 1024);
+    }
+#pragma unroll
+    for (int i = 0; i < V_INSTR; ++i) {
+      const int j = wave * V_INSTR + i;
+      const int kr = j * V_ROWS_PER_I + lane / (D / 8); // Vs row (key)
+      const int c = (lane % (D / 8)) ^ dv_swz(kr);
+      const int key = min(kv0 + kr, S - 1);
+      dma_load16(vg + (int64_t)key * D + c * 8, lv + j * 1024);
+    }
+  };
+  // q[b] (32 head slots, rows past H clamped to row H-1 and zeroed on read)
+  // arrives by LDS DMA ahead of the first stages: a plain load would make the
+  // compiler wait for every copy in flight before its first use
+  lds_char_t* sq = (lds_char_t*)(smem + NS * STAGE);
+#pragma unroll
+  for (int i = 0; i < Q_INSTR; ++i) {
+    const int j = wave * Q_INSTR + i;
+    const int e = j * 512 + lane * 8;                     // element of the [32][D] slots
+    const int hq = min(e / D, H - 1);
+    dma_load16(p.q + ((int64_t)b * H + hq) * D + e % D, lds_addr(sq) + j * 1024);
+  }
+#pragma unroll
+  for (int s = 0; s < NS - 1; ++s)
+    if (s < nblk) issue(s, s);
+
+  // Q^T operand of this wave's head tile, q[b][16 ht + r][32 ds + 8 g ..],
+  // read from LDS once the first stage has landed
+  const int h = 16 * ht + r;
+  u32x4_t qf[DSTEPS];
+
+  const float c2 = p.c2;
+  float m_run = 0.f;                           // base (log2 domain) of head h
+  f32x4_t ot[DT], lacc = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) ot[dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  const u32x4_t ones = u32x4_t{kOnePair<F16>, kOnePair<F16>, kOnePair<F16>, kOnePair<F16>};
+  bool first = true;
+
+  auto compute = [&](int s, int blk) {
+    const int kv0 = kbeg + blk * KB + 32 * kh;   // this wave's 32 keys
+    const lds_char_t* ks = stK(s);
+    const lds_char_t* vs = stV(s);
+    // ---- raw scores S^T = K^T Q^T; st[j][i] is key kv0 + 16 j + 4 g + i of head h
+    f32x4_t st[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) st[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ds = 0; ds < DSTEPS; ++ds) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int jt = 2 * kh + j;
+        const int d = ds * 32 + g * 8 + a4;
+        const int ch = (2 * jt + (c4 >> 1)) ^ dk_swz(d);
+        const lds_char_t* q = ks + d * (KB * 2) + ch * 16 + (c4 & 1) * 8;
+        const u32x2_t lo = lds_read_tr16(q);
+        const u32x2_t hi = lds_read_tr16(q + 4 * (KB * 2));
+        st[j] = mfma16t<F16>(u32x4_t{lo[0], lo[1], hi[0], hi[1]}, qf[ds], st[j]);
       }
+    }
+    // ---- log2-domain scores relative to the base; keys outside the split
+    // (or past S) are -inf
+    const bool edge = kv0 < s0 || kv0 + 32 > s1;
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const float w = u0 + u < cn ? __shfl(wl, u0 + u) : 0.f;
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int i = 0; i < DPL; ++i) acc[i] += v[u][i] * w;
+      for (int i = 0; i < 4; ++i) {
+        float v = __builtin_fmaf(st[j][i], c2, -m_run);
+        if (edge) {
+          const int key = kv0 + 16 * j + 4 * g + i;
+          if (key < s0 || key >= s1) v = -INFINITY;
+        }
+        st[j][i] = v;
+      }
+    // ---- lazy online softmax: the base moves (and O, l rescale) only on
+    // this wave's first block or when a score rises more than 8 above it
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) mx = fmaxf(mx, st[j][i]);
+    if (first || __builtin_amdgcn_ballot_w64(mx > 8.f) != 0) {
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      // masking is per key, so a block is masked for every head or for none:
+      // a wholly masked first block adds nothing and leaves the base unset
+      if (first && __builtin_amdgcn_ballot_w64(mx != -INFINITY) == 0) return;
+      const float shift = first ? mx : fmaxf(mx, 0.f);
+      if (!first) {
+        const float alpha = fast_exp2(-shift);
+        lacc *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) ot[dt] *= alpha;
+      }
+      m_run += shift;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) st[j] -= shift;
+      first = false;
+    }
+    f32x4_t e0, e1;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      e0[i] = fast_exp2(st[0][i]);
+      e1[i] = fast_exp2(st[1][i]);
+    }
+    const u32x4_t pf = u32x4_t{pack2<F16>(e0[0], e0[1]), pack2<F16>(e0[2], e0[3]),
+                               pack2<F16>(e1[0], e1[1]), pack2<F16>(e1[2], e1[3])};
+    lacc = mfma16t<F16>(ones, pf, lacc);
+    // ---- O^T += V^T P^T over the 32 keys
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      const int k0r = 32 * kh + 4 * g + a4;
+      const int ch = (2 * dt + (c4 >> 1)) ^ dv_swz(k0r);
+      const lds_char_t* q = vs + k0r * VROW + ch * 16 + (c4 & 1) * 8;
+      const u32x2_t lo = lds_read_tr16(q);                // keys 4 g + 0..3
+      const u32x2_t hi = lds_read_tr16(q + 16 * VROW);    // keys 16 + 4 g + 0..3
+      ot[dt] = mfma16t<F16>(u32x4_t{lo[0], lo[1], hi[0], hi[1]}, pf, ot[dt]);
+    }
+  };
+
+  // ---- pipeline: NS stages, the first NS-1 issued above; each wave waits
+  // for its own copies of the stage (copies complete in issue order, q's
+  // first), the barrier for everyone's (the waits are placed by hand, as in
+  // gemm.hip and attention.hip)
+  for (int it0 = 0; it0 < nblk; it0 += NS) {
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const int it = it0 + s;
+      if (it < nblk) {
+        const int younger = min(NS - 2, nblk - 1 - it);
+        if (younger >= 2) LOOM_WAIT_VMCNT(2 * LPW);
+        else if (younger == 1) LOOM_WAIT_VMCNT(LPW);
+        else LOOM_WAIT_VMCNT(0);
+        barrier_nofence();
+        if (it == 0) {
+          // q's copies were issued before stage 0's, so they have landed too
+#pragma unroll
+          for (int ds = 0; ds < DSTEPS; ++ds) {
+            const u32x4_t raw = *reinterpret_cast<const __attribute__((address_space(3))) u32x4_t*>(
+                sq + (h * D + ds * 32 + g * 8) * 2);
+            qf[ds] = h < H ? raw : u32x4_t{0u, 0u, 0u, 0u};
+          }
+        }
+        if (it + NS - 1 < nblk) issue((s + NS - 1) % NS, it + NS - 1);
+        compute(s, it);
       }
     }
   }
-  uint16_t* dst = p.out + bh * D + lane * DPL;
-  if constexpr (DPL == 2)
-    *reinterpret_cast<uint32_t*>(dst) = pack2<F16>(acc[0], acc[1]);
-  else
-    dst[0] = (uint16_t)cvt16<F16>(acc[0]);
+
+  // ---- merge the two key halves of each head tile through LDS: per wave
+  // [16 heads][ROW] (fp32)
+  LOOM_WAIT_VMCNT(0);
+  barrier_nofence();
+  float* mg = reinterpret_cast<float*>(smem);
+  float* my = mg + wave * 16 * ROW + r * ROW;
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) my[dt * 16 + 4 * g + i] = ot[dt][i];
+  if (g == 0) {
+    my[D] = m_run;
+    my[D + 1] = lacc[0];
+  }
+  __syncthreads();
+  // one head and D/8 consecutive d per thread: the weights once, then
+  // 16-byte LDS reads and stores
+  constexpr int DPT = D / 8;                   // d values per thread
+  const int hh = tid >> 3, d0 = (tid & 7) * DPT;
+  if (hh < H) {
+    const float* w0 = mg + (2 * (hh >> 4)) * 16 * ROW + (hh & 15) * ROW;
+    const float* w1 = w0 + 16 * ROW;
+    // a half that saw no key of the split (l = 0) takes no part
+    const float l0 = w0[D + 1], l1 = w1[D + 1];
+    const float M = l0 > 0.f ? (l1 > 0.f ? fmaxf(w0[D], w1[D]) : w0[D]) : w1[D];
+    const float f0 = l0 > 0.f ? fast_exp2(w0[D] - M) : 0.f;
+    const float f1 = l1 > 0.f ? fast_exp2(w1[D] - M) : 0.f;
+    const float L = l0 * f0 + l1 * f1;
+    const float g0 = f0 / L, g1 = f1 / L;
+    const int64_t row = ((int64_t)split * p.B + b) * H + hh;
+    f32x4_t* dst = reinterpret_cast<f32x4_t*>(p.o + row * D + d0);
+#pragma unroll
+    for (int u = 0; u < DPT / 4; ++u) {
+      const f32x4_t a = *reinterpret_cast<const f32x4_t*>(w0 + d0 + 4 * u);
+      const f32x4_t c = *reinterpret_cast<const f32x4_t*>(w1 + d0 + 4 * u);
+      dst[u] = a * g0 + c * g1;
+    }
+    if (d0 == 0) p.lse[row] = (logf(L) + M * 0.69314718055994530942f);
+  }
 }
 
-// D = head dim (64 or 128), HT = head tiles of 16, ALIGNED = S is a
-// multiple of 4 (8-byte K chunks start on 8-byte boundaries).
-//
-// Each wave walks its 64-key blocks as NSTEPS load steps of eight loads:
-// DSTEPS steps of K (eight d rows x 4 keys per lane, 8-byte loads) then two
-// steps of V (eight keys x VEC d per lane).  Loads run one step ahead of the
-// math through a two-slot register ring, continuing into the wave's next
-// block; with two waves per SIMD the other wave's math covers the rest of
-// the latency.  All loads are raw buffer loads: anything past the tensor
-// reads as zero, and keys past the split end are masked to -inf before the
-// softmax (so their V rows are multiplied by exactly 0).
 template <int D, int HT, bool ALIGNED, bool F16>
 __global__ void __launch_bounds__(64 * kWaves) decode_split_kernel(DecodeParams p) {
   constexpr int VEC = D / 16;     // d values per lane per V row, also # of d tiles
   constexpr int DSTEPS = D / 32;  // 32-deep MFMA steps over d
   constexpr int NSTEPS = DSTEPS + 2;
-#ifndef LOOM_DECODE_RING
-#define LOOM_DECODE_RING 3
-#endif
-  // ring slots (a divisor of the step count)
-  constexpr int R = NSTEPS % LOOM_DECODE_RING == 0 ? LOOM_DECODE_RING : 2;
+  // ring slots: three (loads two steps ahead) where they divide the step
+  // count, else two
+  constexpr int R = NSTEPS % 3 == 0 ? 3 : 2;
   static_assert(NSTEPS % R == 0, "ring must divide the step count");
   constexpr int HP = HT * 16;     // padded head count
   constexpr int ACC_STRIDE = D + 1;
@@ -409,17 +660,26 @@ int flash_decode_impl(const void* k, const void* v, const void* q, void* out,
   p.tile_s = (int)tile_s;
   p.ns = (int)ns;
   p.c2 = scale * 1.4426950408889634f;
-  const bool al = S % 4 == 0;
   if (loom_validate_only()) return loom_ok(err, errlen);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (D == 128) {
-    if (H > 16) launch_split<128, 2, F16>(p, al, st); else launch_split<128, 1, F16>(p, al, st);
+  if (S % 8 == 0) {
+    // LDS-DMA split kernel: K rows start on 16-byte boundaries
+    const dim3 grid((unsigned)ns, (unsigned)B), block(256);
+    if (D == 128)
+      hipLaunchKernelGGL((decode_dma_kernel<128, F16>), grid, block, 0, st, p);
+    else
+      hipLaunchKernelGGL((decode_dma_kernel<64, F16>), grid, block, 0, st, p);
   } else {
-    if (H > 16) launch_split<64, 2, F16>(p, al, st); else launch_split<64, 1, F16>(p, al, st);
+    const bool al = S % 4 == 0;
+    if (D == 128) {
+      if (H > 16) launch_split<128, 2, F16>(p, al, st); else launch_split<128, 1, F16>(p, al, st);
+    } else {
+      if (H > 16) launch_split<64, 2, F16>(p, al, st); else launch_split<64, 1, F16>(p, al, st);
+    }
   }
   int rc = loom_check_launch(err, errlen, "flash_decode (split)");
   if (rc) return rc;
-  const dim3 cgrid((unsigned)cdiv64(B * H, 4)), cblock(256);
+  const dim3 cgrid((unsigned)cdiv64(B * H * D / 2, 256)), cblock(256);
   if (D == 128)
     hipLaunchKernelGGL((decode_combine_kernel<128, F16>), cgrid, cblock, 0, st, p);
   else

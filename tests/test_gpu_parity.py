@@ -361,6 +361,38 @@ def test_decode_partials_match_oracle(lh, golden):
     assert_close(o.cpu().numpy(), o_ref, **ATTN_TOL, what="o_s")
 
 
+@pytest.mark.parametrize("S,ts", [(1001, 256), (1004, 128)])
+def test_decode_register_path(lh, S, ts):
+    """S not a multiple of 8: K rows do not start on 16-byte boundaries, so the
+    register-load split kernel runs (2-byte K loads for S % 4 != 0, 8-byte
+    for S % 4 == 0) instead of the LDS-DMA one."""
+    rng = np.random.default_rng(S)
+    B, H, D = 2, 32, 128
+    k, v, q = rng_bf16(rng, (B, D, S)), rng_bf16(rng, (B, S, D)), rng_bf16(rng, (B, H, D))
+    ref, lse_r, o_r = oracle.flash_decode(k, v, q, 1 / math.sqrt(D), 1, ts, 64)
+    got, lse, o = lh.flash_decode(dev(k), dev(v), dev(q), tile_s=ts, tile_n=64,
+                                  return_partials=True)
+    assert_close(from_bf16(host(got)), from_bf16(ref), **ATTN_TOL, what=f"decode S={S}")
+    assert_close(lse.cpu().numpy(), lse_r, atol=1e-2, rtol=1e-3, what=f"lse S={S}")
+
+
+@pytest.mark.parametrize("D,H,ts", [(128, 32, 100), (64, 12, 44), (128, 5, 8)])
+def test_decode_split_boundaries(lh, D, H, ts):
+    """LDS-DMA split kernel with splits that start off 8-key boundaries
+    (stages start at the split's first key rounded down, the keys before it
+    masked), splits shorter than a 32-key half (waves that see no key), and
+    fewer than 16 heads; every split's partials against the oracle."""
+    rng = np.random.default_rng(D + H + ts)
+    B, S = 3, 1024
+    k, v, q = rng_bf16(rng, (B, D, S)), rng_bf16(rng, (B, S, D)), rng_bf16(rng, (B, H, D))
+    ref, lse_r, o_r = oracle.flash_decode(k, v, q, 1 / math.sqrt(D), 1, ts, min(ts, 64))
+    got, lse, o = lh.flash_decode(dev(k), dev(v), dev(q), tile_s=ts, tile_n=min(ts, 64),
+                                  return_partials=True)
+    assert_close(from_bf16(host(got)), from_bf16(ref), **ATTN_TOL, what=f"decode ts={ts}")
+    assert_close(lse.cpu().numpy(), lse_r, atol=1e-2, rtol=1e-3, what=f"lse ts={ts}")
+    assert_close(o.cpu().numpy(), o_r, **ATTN_TOL, what=f"o_s ts={ts}")
+
+
 def test_decode_baseline(lh):
     """B32, H32 on one KV head, D128, S8192 (the bench config) vs the oracle."""
     rng = np.random.default_rng(9)
@@ -370,6 +402,9 @@ def test_decode_baseline(lh):
     for ts in (512, 1024):
         got = lh.flash_decode(dev(k), dev(v), dev(q), tile_s=ts, tile_n=128)
         assert_close(from_bf16(host(got)), from_bf16(ref), **ATTN_TOL, what=f"decode tile_s={ts}")
+        # run to run: the same inputs give the same bits
+        again = lh.flash_decode(dev(k), dev(v), dev(q), tile_s=ts, tile_n=128)
+        assert torch.equal(got.view(torch.int16), again.view(torch.int16)), ts
 
 
 def test_decode_workspace_reuse_and_garbage(lh):
