@@ -11,16 +11,24 @@ of one call each, inputs resident in HBM.  It carries
   cpu_baseline  the fp32 C oracle (OpenMP, all host threads) on a bounded
                 sample of the same batches;
   kernels       every BASELINE configuration (mm, bmm, split-K, flashattn,
-                mqa_decode, mamba_chunk_scan): mean GPU time of calls enqueued
-                back to back, each call on a different copy of its inputs so
-                operands never stay in the 256 MB Infinity Cache between
-                calls, with its roofline fraction.
+                mqa_decode, mamba_chunk_scan, SSD prologue): mean GPU time of
+                calls enqueued back to back, each call on a different copy of
+                its inputs so operands never stay in the 256 MB Infinity Cache
+                between calls, with its roofline fraction, the dominant
+                kernel's HBM bytes per launch from the committed counter
+                summaries (profiles/hbm_traffic.json), and the CPU oracle on a
+                stated slice of the same configuration (measured, then scaled
+                to the whole; cores and GPU/CPU speed-up stated);
+  ceilings      what this part sustains (HBM read over 2 GiB and over one
+                cache-flushed 134.7 MB pass; bf16 MFMA chains), next to the
+                published peaks the fractions use.
 
 Before timing, each measurement runs its own call untimed for --settle-ms of
 GPU time (clocks take on the order of 100 ms of load to settle).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
-                       [--kernels all|none|mm,bmm,...]
+                       [--no-ceilings] [--kernels all|none|mm,bmm,...]
+       python bench.py --profile-workload all|mm,bmm,...   (for rocprofv3 --pmc)
 """
 import argparse
 import json
@@ -47,12 +55,19 @@ def parse():
     ap.add_argument("--settle-ms", type=float, default=150.0,
                     help="untimed GPU work before each measurement (clocks and power settle)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    ap.add_argument("--no-ceilings", action="store_true",
+                    help="skip the on-box HBM and MFMA ceiling measurement")
     ap.add_argument("--kernels", default="all", help="per-kernel table: all, none or a list")
     ap.add_argument("--iters", type=int, default=20, help="timed calls per kernel in the table")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only run the workload profiled for roofline.traffic: a 256 MiB "
                          "device copy (the calibration kernel), three headline bmm launches "
                          "and three split-K launches (cache flushed before each)")
+    ap.add_argument("--profile-workload", default=None,
+                    help="only run the workload a counter profile attributes: the 256 MiB "
+                         "calibration copy, then three calls of each listed kernel (comma "
+                         "list of the table's names, or 'all'), the Infinity Cache flushed "
+                         "by a read-only pass before each call")
     return ap.parse_args()
 
 
@@ -151,14 +166,26 @@ def make_cases(torch, lh):
     def copies(nbytes):
         return max(1, min(4, -(-3 * MALL_BYTES // nbytes)))
 
+    def h16(t):
+        import numpy as np
+        return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+    def hf(t):
+        return t.contiguous().float().cpu().numpy()
+
     cases = {}
 
     def mm():
         x, y = unif(1024, 1024), unif(1024, 1024)
         out = torch.empty(1024, 1024, dtype=bf, device=cuda)
+        def cpu():
+            import oracle
+            hx, hy = h16(x), h16(y)
+            return 1.0, "the whole 1024^3 product", lambda: oracle.matmul(hx, hy, 128, 128, 64)
         return dict(fn=lambda i: lh.matmul(x, y, out, tile_m=64, tile_n=64, tile_k=64),
                     flop=2 * 1024 ** 3, bytes=3 * 1024 * 1024 * 2, bound="mfma", sets=1,
-                    desc="mm 1024^3 bf16, tile 64x64 (operands cache resident)")
+                    desc="mm 1024^3 bf16, tile 64x64 (operands cache resident)", cpu=cpu,
+                    kernel="gemm_pipe_kernel<64, false>")
     cases["mm"] = mm
 
     def bmm():
@@ -166,9 +193,14 @@ def make_cases(torch, lh):
         n = copies(nb)
         sets = [(randn(16, 2048, 2048, std=0.02), randn(16, 2048, 2048, std=0.02),
                  torch.empty(16, 2048, 2048, dtype=bf, device=cuda)) for _ in range(n)]
+        def cpu():
+            import oracle
+            a0, a1 = h16(sets[0][0][:1]), h16(sets[0][1][:1])
+            return 1 / 16, "1 of 16 batches", lambda: oracle.batch_matmul(a0, a1, 1, 256, 256, 64)
         return dict(fn=lambda i: lh.batch_matmul(*sets[i % n], tile_m=256, tile_n=256),
                     flop=2 * 16 * 2048 ** 3, bytes=nb, bound="mfma", sets=n,
-                    desc="bmm 16x2048^3 bf16, tile 256x256")
+                    desc="bmm 16x2048^3 bf16, tile 256x256", cpu=cpu,
+                    kernel="gemm_persist_kernel<false>")
     cases["bmm"] = bmm
 
     def splitk():
@@ -177,10 +209,16 @@ def make_cases(torch, lh):
         sets = [(randn(512, 16384, std=0.02), randn(16384, 512, std=0.02),
                  torch.empty(512, 512, dtype=bf, device=cuda),
                  torch.empty(16, 512, 512, dtype=torch.float32, device=cuda)) for _ in range(n)]
+        def cpu():
+            import oracle
+            a, b = h16(sets[0][0]), h16(sets[0][1])
+            return 1.0, "all 16 slabs and the reduction", \
+                lambda: oracle.split_k_matmul_gather(a, b, 128, 128, 1024)
         return dict(fn=lambda i: lh.split_k_matmul_gather(*sets[i % n], tile_m=128, tile_n=128,
                                                           tile_k=1024),
                     flop=2 * 512 * 512 * 16384, bytes=nb, bound="hbm", sets=n,
-                    desc="split-K 512x512x16384, 16 slabs, fp32 partials")
+                    desc="split-K 512x512x16384, 16 slabs, fp32 partials", cpu=cpu,
+                    kernel="gemm_pipe_kernel<128, false>")
     cases["split_k"] = splitk
 
     def flashattn():
@@ -189,9 +227,15 @@ def make_cases(torch, lh):
         n = min(2, copies(nb))
         sets = [(randn(BH, D, S), randn(BH, S, D), randn(BH, S, D),
                  torch.empty(BH, S, D, dtype=bf, device=cuda)) for _ in range(n)]
+        def cpu():
+            import oracle
+            k, v, q = (h16(t[:4]) for t in sets[0][:3])
+            return 4 / BH, "4 of 128 (b, h) heads", \
+                lambda: oracle.attention(k, v, q, 1 / math.sqrt(D), True, 1, 128, 64)
         return dict(fn=lambda i: lh.attention(*sets[i % n], causal=True, tile_m=256, tile_n=64),
                     flop=4 * BH * S * S * D // 2, bytes=nb, bound="mfma", sets=n,
-                    desc="flashattn fwd B4 H32 S4096 D128 causal, tile_m 256")
+                    desc="flashattn fwd B4 H32 S4096 D128 causal, tile_m 256", cpu=cpu,
+                    kernel="attention_dma_kernel<128, 2, 8, false>")
     cases["flashattn"] = flashattn
 
     def decode():
@@ -201,9 +245,15 @@ def make_cases(torch, lh):
         sets = [(randn(B, D, S), randn(B, S, D), randn(B, H, D),
                  torch.empty(B, H, D, dtype=bf, device=cuda),
                  lh.flash_decode_workspace(B, H, D, S, 1024, cuda)) for _ in range(n)]
+        def cpu():
+            import oracle
+            k, v, q = (h16(t) for t in sets[0][:3])
+            return 1.0, "the whole call (8 splits per batch and the combine)", \
+                lambda: oracle.flash_decode(k, v, q, 1 / math.sqrt(D), 1, 1024, 128)
         return dict(fn=lambda i: lh.flash_decode(*sets[i % n], tile_s=1024, tile_n=128),
                     flop=4 * B * H * S * D, bytes=nb, bound="hbm", sets=n,
-                    desc="mqa_decode B32 H32/1KV D128 S8192, tile_s 1024")
+                    desc="mqa_decode B32 H32/1KV D128 S8192, tile_s 1024", cpu=cpu,
+                    kernel="decode_dma_kernel<128, false>")
     cases["mqa_decode"] = decode
 
     def mamba():
@@ -226,10 +276,17 @@ def make_cases(torch, lh):
         n = copies(nb)
         sets = [first] + [one() for _ in range(n - 1)]
         flop = 2 * b * H * L * N * P + b * H * nc * Q * Q * P + 2 * b * H * L * P
+
+        def cpu():
+            import oracle
+            cb, x, dt, dA, C, Dh, prev = sets[0][:7]
+            a = (h16(cb[:1]), h16(x[:1]), hf(dt[:1]), hf(dA[:1]), h16(C[:1]), hf(Dh), hf(prev[:1]))
+            return 1 / b, "batch 1 of 4", lambda: oracle.mamba_chunk_scan(*a, 64, 64, 64)
         return dict(fn=lambda i: lh.helion_mamba2_chunk_scan_kernel(
             *sets[i % n], tile_m=256, tile_n=64, tile_k=64),
             flop=flop, bytes=nb, bound="hbm", sets=n,
-            desc="mamba chunk_scan b4 L4096 h32 P64 N128 g1 Q256")
+            desc="mamba chunk_scan b4 L4096 h32 P64 N128 g1 Q256", cpu=cpu,
+            kernel="mamba_chunk_scan_kernel<4, false>")
     cases["mamba_chunk_scan"] = mamba
 
     def ssd():
@@ -254,9 +311,15 @@ def make_cases(torch, lh):
             x, dt, A, Bm, C, dA, cb, prev = sets[i % n]
             lh.ssd_prologue(x, dt, A, Bm, C, Q, dA_cumsum=dA, cb=cb, prev_states_T=prev)
         flop = b * nc * Q * Q * N + 2 * b * H * L * N * P
+
+        def cpu():
+            import oracle
+            x, dt, A, Bm, C = sets[0][:5]
+            a = (h16(x[:1]), hf(dt[:1]), hf(A), h16(Bm[:1]), h16(C[:1]))
+            return 1 / b, "batch 1 of 4", lambda: oracle.mamba_prologue(*a, Q)
         return dict(fn=fn, flop=flop, bytes=nb, bound="hbm", sets=n,
                     desc="mamba SSD prologue (cumsum, cb, states + passing) b4 L4096 h32 P64 "
-                         "N128 g1 Q256")
+                         "N128 g1 Q256", cpu=cpu, kernel="ssd_state_kernel")
     cases["mamba_prologue"] = ssd
     return cases
 
@@ -279,7 +342,87 @@ def report(case, ms, calls=None):
         out["ms_median"] = round(median(calls), 5)
         out["ms_p10"] = round(quantile(calls, 0.1), 5)
         out["ms_p90"] = round(quantile(calls, 0.9), 5)
+    kern = case.get("kernel")
+    if kern:
+        out["kernel"] = kern
+        t = traffic_for(kern)
+        # HBM bytes per launch of the dominant kernel, from the committed
+        # rocprofv3 counter summaries (null where none is recorded)
+        out["traffic"] = t
     return out
+
+
+def cpu_column(case, gpu_ms, reps=3, max_run_s=4.0):
+    """The fp32 C oracle (OpenMP, all host threads) on a stated slice of the
+    same configuration: median of `reps` runs after one warm-up (a single run
+    when one takes longer than `max_run_s`), scaled to the whole
+    configuration."""
+    import oracle
+    frac, what, run = case["cpu"]()
+    t0 = time.perf_counter()
+    run()                      # warm-up (page-in, thread pool)
+    first = time.perf_counter() - t0
+    times = [first]
+    if first < max_run_s:
+        times = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            run()
+            times.append(time.perf_counter() - t0)
+    slice_s = median(times)
+    full_s = slice_s / frac
+    out = {"slice": what, "slice_ms": round(slice_s * 1e3, 3), "ms": round(full_s * 1e3, 3),
+           "extrapolated": frac < 1.0, "cores": oracle.num_threads(), "kind": "port",
+           "speedup": round(full_s * 1e3 / gpu_ms, 1)}
+    if case["bound"] == "mfma":
+        out["tflops"] = round(case["flop"] / full_s / 1e12, 4)
+    else:
+        out["gbs"] = round(case["bytes"] / full_s / 1e9, 2)
+    return out
+
+
+def measure_ceilings(torch, lh):
+    """What this part sustains: HBM read rate over 2 GiB (sustained) and over
+    one 134.7 MB pass after an Infinity Cache flush (the decode working set),
+    and the bf16 MFMA rate of independent chains.  Reported next to the
+    published peaks; the roofline fractions keep the published peaks."""
+    sink = torch.zeros(64, dtype=torch.float32, device="cuda")
+    big = torch.ones(1 << 29, dtype=torch.float32, device="cuda")   # 2 GiB
+    s = torch.cuda.current_stream()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+    def timed(fn, reps):
+        best = float("inf")
+        for _ in range(reps):
+            fn(None)
+            torch.cuda.synchronize()
+            a.record(s)
+            fn(True)
+            b.record(s)
+            torch.cuda.synchronize()
+            best = min(best, a.elapsed_time(b))
+        return best
+    settle(torch, lambda i: lh.peak_hbm_read(big, sink), 100)
+    ms_big = timed(lambda t: lh.peak_hbm_read(big, sink), 5)
+    nb = 134742016
+    part = big.view(torch.uint8)[:nb]
+    flush = big.view(torch.uint8)[nb:nb + (1 << 30)]
+    # the flush is a read of 1 GiB elsewhere: clean lines, no write-back
+    ms_pass = timed(lambda t: lh.peak_hbm_read(part if t else flush, sink), 10)
+    iters = 20000
+    flop = lh.peak_mfma_bf16(iters, sink)
+    settle(torch, lambda i: lh.peak_mfma_bf16(iters, sink), 100)
+    ms_mfma = timed(lambda t: lh.peak_mfma_bf16(iters, sink), 5)
+    del big
+    torch.cuda.empty_cache()
+    return {"hbm_read_gbs_2GiB": round((1 << 31) / ms_big / 1e6, 1),
+            "hbm_read_gbs_134MB_pass": round(nb / ms_pass / 1e6, 1),
+            "hbm_read_us_134MB_pass": round(ms_pass * 1e3, 2),
+            "mfma_bf16_tflops": round(flop / ms_mfma / 1e9, 1),
+            "published_hbm_gbs": PEAK_HBM_GBS, "published_bf16_tflops": PEAK_BF16_TFLOPS,
+            "how": "best of several single kernel runs after settling: a 16-byte streaming "
+                   "read (one workgroup of 512 per CU, 4 loads in flight per thread); "
+                   "independent 16x16x32 bf16 MFMA chains, 8 per wave, 2 waves per SIMD"}
 
 
 def cpu_baseline(torch, a0, a1, budget_s=12.0):
@@ -344,6 +487,31 @@ def main():
             lh.split_k_matmul_gather(sa, sb, so, sg, tile_m=128, tile_n=128, tile_k=1024)
         torch.cuda.synchronize()
         print("traffic probe done", file=sys.stderr, flush=True)
+        return
+
+    if args.profile_workload:
+        # counter runs (rocprofv3 --pmc): the calibration copy, then three
+        # calls of each kernel, each after a read-only pass over 1 GiB that
+        # evicts the Infinity Cache without leaving dirty lines
+        src = torch.ones(64 << 20, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+        flush = torch.ones(1 << 28, dtype=torch.float32, device="cuda")
+        sink = torch.zeros(64, dtype=torch.float32, device="cuda")
+        cases = make_cases(torch, lh)
+        names = list(cases) if args.profile_workload == "all" else \
+            args.profile_workload.split(",")
+        for name in names:
+            case = cases[name]()
+            for i in range(3):
+                lh.peak_hbm_read(flush, sink)
+                case["fn"](i)
+            torch.cuda.synchronize()
+            print(f"profile workload {name} done", file=sys.stderr, flush=True)
+            del case
+            torch.cuda.empty_cache()
         return
 
     cases = make_cases(torch, lh)
@@ -413,10 +581,15 @@ def main():
             ms = time_back_to_back(torch, case["fn"], args.iters)
             calls = per_call_ms(torch, case["fn"], args.iters)
             table[name] = report(case, ms, calls)
+            if not args.no_cpu:
+                table[name]["cpu"] = cpu_column(case, ms)
             print(f"# {name}: {table[name]}", file=sys.stderr, flush=True)
             del case
             torch.cuda.empty_cache()
         line["kernels"] = table
+    if not args.no_ceilings:
+        line["ceilings"] = measure_ceilings(torch, lh)
+        print(f"# ceilings: {line['ceilings']}", file=sys.stderr, flush=True)
     print(json.dumps(line), flush=True)
 
 

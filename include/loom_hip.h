@@ -445,6 +445,19 @@ int loom_hip_constraint_scope(const char* func, const int64_t* dims, int ndims, 
 int loom_hip_preferred_block_sizes(const char* func, const int64_t* dims, int ndims, char* out,
                                    size_t outlen, char* err, size_t errlen);
 
+/* ---- on-box ceilings ---------------------------------------------------
+ * Measurement kernels with no counterpart in the reference: what one part
+ * sustains, next to the published peaks the roofline fractions use.
+ * loom_hip_peak_hbm_read streams `bytes` of `buf` (16-byte aligned) once;
+ * its rate is bytes / kernel time.  loom_hip_peak_mfma_bf16 runs `iters`
+ * rounds of independent bf16 MFMA chains on every CU and stores the FLOP it
+ * performs in *flop; its rate is *flop / kernel time.  `sink` is a device
+ * word the kernels may write (so their work cannot be optimised away). */
+int loom_hip_peak_hbm_read(const void* buf, size_t bytes, void* sink, void* stream, char* err,
+                           size_t errlen);
+int loom_hip_peak_mfma_bf16(int64_t iters, void* sink, double* flop, void* stream, char* err,
+                            size_t errlen);
+
 #ifdef __cplusplus
 }
 #endif

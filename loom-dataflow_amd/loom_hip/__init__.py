@@ -117,7 +117,12 @@ _lib.loom_hip_check_memref.argtypes = [ctypes.c_char_p, ctypes.POINTER(_vp), cty
                                        ctypes.c_int, _f32, *_ERR]
 _lib.loom_hip_check_memref.restype = ctypes.c_int
 
-EXPORTED = tuple(_SIGS) + tuple(_CIFACE) + ("loom_hip_dispatch_memref",
+_lib.loom_hip_peak_hbm_read.argtypes = [_vp, _sz, _vp, _vp, *_ERR]
+_lib.loom_hip_peak_hbm_read.restype = ctypes.c_int
+_lib.loom_hip_peak_mfma_bf16.argtypes = [_i64, _vp, ctypes.POINTER(ctypes.c_double), _vp, *_ERR]
+_lib.loom_hip_peak_mfma_bf16.restype = ctypes.c_int
+
+EXPORTED = tuple(_SIGS) + tuple(_CIFACE) + ("loom_hip_peak_hbm_read", "loom_hip_peak_mfma_bf16",) + ("loom_hip_dispatch_memref",
                                             "loom_hip_dispatch_memref_f16",
                                             "loom_hip_check_memref") + ("loom_hip_split_k_workspace_bytes",
                            "loom_hip_flash_decode_workspace_bytes", "loom_hip_version",
@@ -687,3 +692,23 @@ def check_memref(variant: str, *descs, f16=False, scale=1.0):
                                     float(scale), err, len(err))
     if rc != 0:
         raise LoomHipError("loom_hip_check_memref", rc, err.value.decode(errors="replace"))
+
+
+# ---------------------------------------------------------------------------
+# on-box ceilings
+# ---------------------------------------------------------------------------
+
+def peak_hbm_read(buf: torch.Tensor, sink: torch.Tensor) -> None:
+    """Streams ``buf`` (a contiguous ROCm tensor) once through
+    ``loom_hip_peak_hbm_read`` on the current stream."""
+    _call("loom_hip_peak_hbm_read", buf.data_ptr(), buf.numel() * buf.element_size(),
+          sink.data_ptr(), _stream(buf))
+
+
+def peak_mfma_bf16(iters: int, sink: torch.Tensor) -> float:
+    """Runs ``loom_hip_peak_mfma_bf16`` on the current stream; returns the FLOP
+    it performs."""
+    flop = ctypes.c_double()
+    _call("loom_hip_peak_mfma_bf16", int(iters), sink.data_ptr(), ctypes.byref(flop),
+          _stream(sink))
+    return flop.value
