@@ -500,6 +500,10 @@ def main():
         del src, dst
         flush = torch.ones(1 << 28, dtype=torch.float32, device="cuda")
         sink = torch.zeros(64, dtype=torch.float32, device="cuda")
+        # calibration of the MFMA-busy counter: independent MFMA chains, whose
+        # rate bench.py's ceilings measure
+        lh.peak_mfma_bf16(20000, sink)
+        torch.cuda.synchronize()
         cases = make_cases(torch, lh)
         names = list(cases) if args.profile_workload == "all" else \
             args.profile_workload.split(",")
