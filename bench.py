@@ -185,7 +185,7 @@ def make_cases(torch, lh):
         return dict(fn=lambda i: lh.matmul(x, y, out, tile_m=64, tile_n=64, tile_k=64),
                     flop=2 * 1024 ** 3, bytes=3 * 1024 * 1024 * 2, bound="mfma", sets=1,
                     desc="mm 1024^3 bf16, tile 64x64 (operands cache resident)", cpu=cpu,
-                    kernel="gemm_pipe_kernel<64, false>")
+                    kernel="gemm_pipe_kernel<64, false, false>")
     cases["mm"] = mm
 
     def bmm():
@@ -218,7 +218,7 @@ def make_cases(torch, lh):
                                                           tile_k=1024),
                     flop=2 * 512 * 512 * 16384, bytes=nb, bound="hbm", sets=n,
                     desc="split-K 512x512x16384, 16 slabs, fp32 partials", cpu=cpu,
-                    kernel="gemm_pipe_kernel<128, false>")
+                    kernel="gemm_pipe_kernel<128, true, false>")
     cases["split_k"] = splitk
 
     def flashattn():
@@ -319,7 +319,7 @@ def make_cases(torch, lh):
             return 1 / b, "batch 1 of 4", lambda: oracle.mamba_prologue(*a, Q)
         return dict(fn=fn, flop=flop, bytes=nb, bound="hbm", sets=n,
                     desc="mamba SSD prologue (cumsum, cb, states + passing) b4 L4096 h32 P64 "
-                         "N128 g1 Q256", cpu=cpu, kernel="ssd_state_kernel")
+                         "N128 g1 Q256", cpu=cpu, kernel="ssd_state_kernel<4, 2, false>")
     cases["mamba_prologue"] = ssd
     return cases
 
