@@ -44,17 +44,21 @@ struct AttnParams {
 // raises it by more than 8 in the log2 domain, which keeps P <= 2^8 and the
 // result exact (numerator and denominator share the stale base).
 // Ks rows (128 B) and Vs rows (2 D bytes) XOR their 16-byte chunk index with
-// k_swz / v_swz so that each 32-lane pass of a transposed read touches 32
-// distinct 16-byte slots of the LDS's 512-byte bank window.
+// k_swz / v_swz so that the 32 lanes of each pass of a transposed read touch
+// distinct banks.  The banks repeat every 256 bytes (measured: rows 256 bytes
+// apart conflict, SQ_LDS_BANK_CONFLICT), so a 32-byte row piece has eight
+// positions per window.
 // ---------------------------------------------------------------------------
-// One pass of a K^T read covers Ks rows d..d+3 and d+8..d+11 (128 B apart:
-// rows d and d+8 share a window position), 32 bytes each: bit 3 of the row
-// flips the chunk pair.
-LOOM_DEV int k_swz(int d) { return 2 * ((d >> 3) & 1); }
-// One pass of a V^T read covers 8 consecutive Vs rows, 32 bytes each; rows r,
-// r^2, r^4, r^6 (D 128: 256-byte rows) or r, r^4 (D 64: 128-byte rows) share
-// a window position: row bits 1-2 pick the chunk pair.
-LOOM_DEV int v_swz(int k) { return 2 * ((k >> 1) & 3); }
+// One pass of a K^T read covers Ks rows d..d+3 and d+8..d+11, 32 bytes each;
+// 128-byte rows put the even rows on one half of the window and the odd rows
+// on the other, so rows d, d^2, d^8, d^10 must take distinct chunk pairs:
+// row bits 1 and 3 pick them (bit 0 only repeats the half's pattern).
+LOOM_DEV int k_swz(int d) { return (2 * (d & 3)) ^ (2 * ((d >> 3) & 1)); }
+// One pass of a V^T read covers 8 consecutive Vs rows, 32 bytes each.  D 128
+// (256-byte rows): all eight share a window position, row bits 0-2 pick the
+// pair.  D 64 (128-byte rows): rows r, r^2, r^4, r^6 share one, bits 1-2.
+template <int D>
+LOOM_DEV int v_swz(int k) { return D == 128 ? 2 * (k & 7) : 2 * ((k >> 1) & 3); }
 
 template <int D, int QT, int W, bool H>
 __global__ void __launch_bounds__(64 * W) attention_dma_kernel(AttnParams p) {
@@ -118,7 +122,7 @@ __global__ void __launch_bounds__(64 * W) attention_dma_kernel(AttnParams p) {
     for (int i = 0; i < V_INSTR; ++i) {
       const int j = wave * V_INSTR + i;
       const int kr = j * V_ROWS_PER_I + lane / (D / 8);   // Vs row (key)
-      const int c = (lane % (D / 8)) ^ v_swz(kr);
+      const int c = (lane % (D / 8)) ^ v_swz<D>(kr);
       const int key = min(kv0 + kr, Skv - 1);
       dma_load16(vg + (int64_t)key * D + c * 8, lv + j * 1024);
     }
@@ -261,7 +265,7 @@ __global__ void __launch_bounds__(64 * W) attention_dma_kernel(AttnParams p) {
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
         const int k0r = 32 * h + 4 * g + a4;
-        const int ch = (2 * dt + (c4 >> 1)) ^ v_swz(k0r);
+        const int ch = (2 * dt + (c4 >> 1)) ^ v_swz<D>(k0r);
         const lds_char_t* q = vs + k0r * VROW + ch * 16 + (c4 & 1) * 8;
         const u32x2_t lo = lds_read_tr16(q);                // keys 32h + 4g + 0..3
         const u32x2_t hi = lds_read_tr16(q + 16 * VROW);    // keys 32h + 16 + 4g + 0..3

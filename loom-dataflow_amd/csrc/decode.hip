@@ -118,11 +118,14 @@ __global__ void __launch_bounds__(256) decode_combine_kernel(DecodeParams p) {
 // Blocks start at the split's first key rounded down to a multiple of 8;
 // keys outside [s0, s1) are masked to -inf, reads past S are clamped.
 // ---------------------------------------------------------------------------
-// 16-byte chunk swizzles of the Ks and Vs rows (as in attention.hip): each
-// 32-lane pass of a transposed read touches 32 distinct 16-byte slots of the
-// 512-byte LDS bank window.
-LOOM_DEV int dk_swz(int d) { return 2 * ((d >> 3) & 1); }
-LOOM_DEV int dv_swz(int k) { return 2 * ((k >> 1) & 3); }
+// 16-byte chunk swizzles of the Ks and Vs rows, as in attention.hip: the
+// banks repeat every 256 bytes, and each 32-lane pass of a transposed read
+// must touch distinct ones.  Ks (128-byte rows): rows d, d^2, d^8, d^10 share
+// a window position.  Vs: D 128 (256-byte rows) all eight rows of a pass, D 64
+// rows r, r^2, r^4, r^6.
+LOOM_DEV int dk_swz(int d) { return (2 * (d & 3)) ^ (2 * ((d >> 3) & 1)); }
+template <int D>
+LOOM_DEV int dv_swz(int k) { return D == 128 ? 2 * (k & 7) : 2 * ((k >> 1) & 3); }
 
 template <int D, bool F16>
 __global__ void __launch_bounds__(256) decode_dma_kernel(DecodeParams p) {
@@ -177,7 +180,7 @@ __global__ void __launch_bounds__(256) decode_dma_kernel(DecodeParams p) {
     for (int i = 0; i < V_INSTR; ++i) {
       const int j = wave * V_INSTR + i;
       const int kr = j * V_ROWS_PER_I + lane / (D / 8); // Vs row (key)
-      const int c = (lane % (D / 8)) ^ dv_swz(kr);
+      const int c = (lane % (D / 8)) ^ dv_swz<D>(kr);
       const int key = min(kv0 + kr, S - 1);
       dma_load16(vg + (int64_t)key * D + c * 8, lv + j * 1024);
     }
@@ -283,7 +286,7 @@ __global__ void __launch_bounds__(256) decode_dma_kernel(DecodeParams p) {
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
       const int k0r = 32 * kh + 4 * g + a4;
-      const int ch = (2 * dt + (c4 >> 1)) ^ dv_swz(k0r);
+      const int ch = (2 * dt + (c4 >> 1)) ^ dv_swz<D>(k0r);
       const lds_char_t* q = vs + k0r * VROW + ch * 16 + (c4 & 1) * 8;
       const u32x2_t lo = lds_read_tr16(q);                // keys 4 g + 0..3
       const u32x2_t hi = lds_read_tr16(q + 16 * VROW);    // keys 16 + 4 g + 0..3
