@@ -264,6 +264,21 @@ LOOM_DEV void dma_load16(const void* g, uint32_t lds) {
       : "memory", "m0");
 }
 
+// LDS banks repeat every 256 bytes.  A transposed read (below) serves 32
+// lanes per pass; when each of its 16-lane groups reads rows r..r+3 of one
+// tile and the two groups rows r+4..r+7, the pass touches 32-byte pieces of 8
+// consecutive rows, and rows that sit at the same offset of the 256-byte
+// window must take distinct 16-byte chunk pairs.  tr_swz(k, rb) is the XOR a
+// row k of rb bytes (a multiple of 32) applies to its chunk index.  With
+// g = gcd(rb, 256), rows 256/g apart share a window offset and g/32 of them
+// fall among 8 consecutive rows; the XOR takes g/32 values below g/16, and
+// since rb is a multiple of g it keeps every chunk index inside its row.
+LOOM_DEV int tr_swz(int k, int rb) {
+  const int g = (rb & -rb) < 256 ? (rb & -rb) : 256;  // gcd(rb, 256)
+  const int pr = g >= 32 ? g / 32 : 1;                 // rows of a pass sharing an offset
+  return 2 * ((k / (256 / g)) % pr);
+}
+
 // ds_read_b64_tr_b16: in each 16-lane group, lanes 4a..4a+3 address the four
 // 8-byte pieces of row a of a 4x16 matrix of 16-bit values; lane j receives
 // column j, (row0[j], row1[j], row2[j], row3[j]).

@@ -16,7 +16,10 @@
 // whole (b, c) groups: the heads that share cb and C then run together on
 // one L2.  Per workgroup:
 //   - x[k, p] (k < m-tile end) is copied to LDS transposed (xT [p][k]) by
-//     8x8 register transposes: the B operand of W . x;
+//     8x8 register transposes: the B operand of W . x; xT and pT rows XOR
+//     their 16-byte chunk index with row & 15, so the 16 rows a ds_read_b128
+//     pass reads (every row at the same offset of the 256-byte bank window)
+//     hit distinct banks;
 //   - prevT[n, p] (fp32) is split into bf16 hi + lo halves, transposed into
 //     LDS (pT [p][n]): the B operand of C . prevT, so the state term keeps
 //     about 16 mantissa bits;
@@ -161,7 +164,10 @@ __global__ void __launch_bounds__(64 * kWaves) mamba_chunk_scan_kernel(MambaPara
     u32x4_t tr[8];
     transpose8x8(xr, tr);
 #pragma unroll
-    for (int u = 0; u < 8; ++u) xT[(x_pc * 8 + u) * XROW + (x_kc ^ u)] = tr[u];  // row & 7 == u
+    for (int u = 0; u < 8; ++u) {
+      const int row = x_pc * 8 + u;
+      xT[row * XROW + (x_kc ^ (row & 15))] = tr[u];
+    }
   }
   if (do_p) {
     // prevT split into bf16 hi + lo (the state term keeps ~16 mantissa bits);
@@ -183,8 +189,8 @@ __global__ void __launch_bounds__(64 * kWaves) mamba_chunk_scan_kernel(MambaPara
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const int pp = p_pc * 8 + u;
-      pT[0][pp * PROW + (p_nc ^ u)] = thi[u];
-      if constexpr (!F16) pT[1][pp * PROW + (p_nc ^ u)] = tlo[u];
+      pT[0][pp * PROW + (p_nc ^ (pp & 15))] = thi[u];
+      if constexpr (!F16) pT[1][pp * PROW + (p_nc ^ (pp & 15))] = tlo[u];
     }
   }
   __syncthreads();
@@ -253,7 +259,7 @@ __global__ void __launch_bounds__(64 * kWaves) mamba_chunk_scan_kernel(MambaPara
 #pragma unroll
       for (int pt = 0; pt < PT; ++pt) {
         const int pp = pt * 16 + rr;
-        const int ch = (ns * 4 + g4) ^ (pp & 7);
+        const int ch = (ns * 4 + g4) ^ (pp & 15);
         acc_s[pt] = mfma16t<F16>(pT[0][pp * PROW + ch], rw.c[ns], acc_s[pt]);
         if constexpr (!F16) acc_s[pt] = mfma16t<F16>(pT[1][pp * PROW + ch], rw.c[ns], acc_s[pt]);
       }
@@ -310,7 +316,7 @@ __global__ void __launch_bounds__(64 * kWaves) mamba_chunk_scan_kernel(MambaPara
 #pragma unroll
       for (int pt = 0; pt < PT; ++pt) {
         const int pp = pt * 16 + rr;
-        const u32x4_t xb = xT[pp * XROW + ((ks * 4 + g4) ^ (pp & 7))];
+        const u32x4_t xb = xT[pp * XROW + ((ks * 4 + g4) ^ (pp & 15))];
         acc[pt] = mfma16t<F16>(xb, ahi, acc[pt]);
         acc[pt] = mfma16t<F16>(xb, alo, acc[pt]);
       }

@@ -206,13 +206,17 @@ __global__ void __launch_bounds__(64 * kSsdWaves) ssd_state_kernel(SsdStateParam
   for (int i = 0; i < kSsdMaxLpw; ++i) {
     const int j = wave + kSsdWaves * i;
     if (j < xinstr) {
+      // LDS slot (row, chunk) of the [QSP][P] unit holds global chunk
+      // chunk ^ tr_swz(row): transposed reads of 8 rows then hit distinct banks
       const int e = (j * 64 + lane) * 8;          // element offset in the [QSP][P] unit
-      goff[i] = min(e / P, QS - 1) * P + e % P;
+      const int row = e / P, cc = (e % P) / 8;
+      goff[i] = min(row, QS - 1) * P + (cc ^ tr_swz(row, XR)) * 8;
       loff[i] = j * 1024;
       kind[i] = 0;
     } else if (j < xinstr + binstr) {
       const int idx = (j - xinstr) * 64 + lane;
-      goff[i] = min(idx / (nb / 8), QS - 1) * N + (idx % (nb / 8)) * 8;
+      const int row = idx / (nb / 8), cc = idx % (nb / 8);
+      goff[i] = min(row, QS - 1) * N + (cc ^ tr_swz(row, BR)) * 8;
       loff[i] = p.xbytes + (j - xinstr) * 1024;
       kind[i] = 1;
     } else {
@@ -316,7 +320,8 @@ __global__ void __launch_bounds__(64 * kSsdWaves) ssd_state_kernel(SsdStateParam
   };
   auto load_ops = [&](const lds_char_t* xs, const lds_char_t* bs, int ks, int pt, Ops& o) {
     const int k0 = 32 * ks + 4 * gq;          // this lane's keys: k0 + 0..3, k0 + 16..19
-    const lds_char_t* qx = xs + (k0 + a4) * XR + (2 * pt + (c4 >> 1)) * 16 + (c4 & 1) * 8;
+    const lds_char_t* qx =
+        xs + (k0 + a4) * XR + ((2 * pt + (c4 >> 1)) ^ tr_swz(k0 + a4, XR)) * 16 + (c4 & 1) * 8;
     o.x0 = lds_read_tr16(qx);
     o.x1 = lds_read_tr16(qx + 16 * XR);
     o.w0 = *reinterpret_cast<const f32x4_t*>(sw + k0);
@@ -324,7 +329,8 @@ __global__ void __launch_bounds__(64 * kSsdWaves) ssd_state_kernel(SsdStateParam
 #pragma unroll
     for (int t = 0; t < TPW; ++t) {
       const int nt = MODE == 2 ? t : min(wave + kSsdWaves * t, tiles - 1) / ptiles;
-      const lds_char_t* qb = bs + (k0 + a4) * BR + (2 * nt + (c4 >> 1)) * 16 + (c4 & 1) * 8;
+      const lds_char_t* qb =
+          bs + (k0 + a4) * BR + ((2 * nt + (c4 >> 1)) ^ tr_swz(k0 + a4, BR)) * 16 + (c4 & 1) * 8;
       o.b0[t] = lds_read_tr16(qb);
       o.b1[t] = lds_read_tr16(qb + 16 * BR);
     }
@@ -413,12 +419,14 @@ __global__ void __launch_bounds__(64 * kSsdWaves) ssd_state_kernel(SsdStateParam
           const int tt = wave + kSsdWaves * t;
           if (tt < tiles) {
             const int pt = tt % ptiles, nt = tt / ptiles;
-            const lds_char_t* qx = xs + (k0 + a4) * XR + (2 * pt + (c4 >> 1)) * 16 + (c4 & 1) * 8;
+            const lds_char_t* qx = xs + (k0 + a4) * XR +
+                                   ((2 * pt + (c4 >> 1)) ^ tr_swz(k0 + a4, XR)) * 16 + (c4 & 1) * 8;
             u32x4_t xh, xl;
             scale_x(lds_read_tr16(qx), lds_read_tr16(qx + 16 * XR),
                     *reinterpret_cast<const f32x4_t*>(sw + k0),
                     *reinterpret_cast<const f32x4_t*>(sw + k0 + 16), xh, xl);
-            const lds_char_t* qb = bs + (k0 + a4) * BR + (2 * nt + (c4 >> 1)) * 16 + (c4 & 1) * 8;
+            const lds_char_t* qb = bs + (k0 + a4) * BR +
+                                   ((2 * nt + (c4 >> 1)) ^ tr_swz(k0 + a4, BR)) * 16 + (c4 & 1) * 8;
             const u32x2_t blo = lds_read_tr16(qb), bhi = lds_read_tr16(qb + 16 * BR);
             const u32x4_t bf = u32x4_t{blo[0], blo[1], bhi[0], bhi[1]};
             R[t] = mfma16t<F16>(xh, bf, R[t]);
