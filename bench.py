@@ -284,7 +284,7 @@ def make_cases(torch, lh):
             return 1 / b, "batch 1 of 4", lambda: oracle.mamba_chunk_scan(*a, 64, 64, 64)
         return dict(fn=lambda i: lh.helion_mamba2_chunk_scan_kernel(
             *sets[i % n], tile_m=256, tile_n=64, tile_k=64),
-            flop=flop, bytes=nb, bound="hbm", sets=n,
+            flop=flop, bytes=nb, bound="hbm", sets=n, inputs=sets,
             desc="mamba chunk_scan b4 L4096 h32 P64 N128 g1 Q256", cpu=cpu,
             kernel="mamba_chunk_scan_kernel<4, false>")
     cases["mamba_chunk_scan"] = mamba

@@ -159,7 +159,9 @@ struct JParser {
     // a real number that happens to be integral (e.g. 64.0) is still an
     // integer value, as llvm::json::Value::getAsInteger accepts it
     const double d = strtod(t.c_str(), nullptr);
-    if (d == (double)(long long)d && d > -9.2e18 && d < 9.2e18) {
+    // range first: converting a double outside long long's range (or inf)
+    // to long long is undefined
+    if (d > -9.2e18 && d < 9.2e18 && d == (double)(long long)d) {
       v.kind = JVal::Int;
       v.i = (long long)d;
     } else {

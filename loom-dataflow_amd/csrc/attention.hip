@@ -349,7 +349,8 @@ int attention_impl(const void* k, const void* v, const void* q, void* out, int64
     return loom_fail(err, errlen, LOOM_EUNSUP, "attention: Skv must be a multiple of 8");
   if (!aligned16(k) || !aligned16(v) || !aligned16(q) || (reinterpret_cast<uintptr_t>(out) & 7u))
     return loom_fail(err, errlen, LOOM_EINVAL, "attention: tensors must be 16-byte aligned");
-  if (Sq > (1 << 30) || Skv > (1 << 30) || BH * cdiv64(Sq, tile_m) > 0x7fffffff)
+  if (Sq > (1 << 30) || Skv > (1 << 30) || !loom_prod_le({BH, cdiv64(Sq, tile_m)}, 0x7fffffff) ||
+      !loom_prod_le({BH, Sq, D}, (int64_t)1 << 50) || !loom_prod_le({BH, Skv, D}, (int64_t)1 << 50))
     return loom_fail(err, errlen, LOOM_EINVAL, "attention: problem too large");
   AttnParams p{};
   p.k = static_cast<const uint16_t*>(k);

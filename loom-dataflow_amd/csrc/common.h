@@ -14,6 +14,7 @@
 #include <stdio.h>
 
 #include <algorithm>
+#include <initializer_list>
 
 #include "../../include/loom_hip.h"   // every entry point matches its declaration
 
@@ -177,6 +178,16 @@ static inline int loom_check_launch(char* err, size_t errlen, const char* what) 
 }
 
 static inline int64_t cdiv64(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Whether the product of non-negative extents stays within `limit`, computed
+// without signed overflow (caller-supplied extents can be anything).
+static inline bool loom_prod_le(std::initializer_list<int64_t> xs, int64_t limit) {
+  int64_t p = 1;
+  for (int64_t x : xs) {
+    if (x < 0 || __builtin_mul_overflow(p, x, &p) || p > limit) return false;
+  }
+  return true;
+}
 static inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 // The reference bounds every loom.sym by the extent of the loop it tiles

@@ -639,7 +639,7 @@ int flash_decode_impl(const void* k, const void* v, const void* q, void* out,
   if (H > 32)
     return loom_fail(err, errlen, LOOM_EUNSUP, "flash_decode: at most 32 query heads (got %lld)",
                      (long long)H);
-  if (S * D * 2 > 0x7fffffffll || B > 65535)
+  if (!loom_prod_le({S, D, 2}, 0x7fffffffll) || B > 65535)
     return loom_fail(err, errlen, LOOM_EINVAL, "flash_decode: S*D or B too large");
   if (!aligned16(k) || !aligned16(v) || !aligned16(q) || !aligned16(out))
     return loom_fail(err, errlen, LOOM_EINVAL, "flash_decode: tensors must be 16-byte aligned");
@@ -780,6 +780,8 @@ int loom_hip_flash_decode_noalloc(const void* k, const void* v, const void* q, v
 size_t loom_hip_flash_decode_workspace_bytes(int64_t B, int64_t H, int64_t D, int64_t S,
                                              int64_t tile_s) {
   if (B <= 0 || H <= 0 || D <= 0 || S <= 0 || tile_s <= 0) return 0;
+  // a product that does not fit is reported as no size at all fits
+  if (!loom_prod_le({cdiv64(S, tile_s), B, H, D + 1, 4}, (int64_t)1 << 60)) return SIZE_MAX;
   const size_t ns = (size_t)cdiv64(S, tile_s);
   return align256(ns * B * H * sizeof(float)) + ns * B * H * D * sizeof(float);
 }

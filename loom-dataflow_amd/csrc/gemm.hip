@@ -1105,8 +1105,8 @@ int check_gemm_common(const void* a, const void* b, const void* c, int64_t M, in
   if (M <= 0 || N <= 0 || K <= 0)
     return loom_fail(err, errlen, LOOM_EINVAL, "%s: extents must be positive (M=%lld N=%lld K=%lld)",
                      fn, (long long)M, (long long)N, (long long)K);
-  if (M > (1 << 30) || N > (1 << 30))
-    return loom_fail(err, errlen, LOOM_EINVAL, "%s: M and N must be below 2^30", fn);
+  if (M > (1 << 30) || N > (1 << 30) || K > (1 << 30))
+    return loom_fail(err, errlen, LOOM_EINVAL, "%s: M, N and K must be below 2^30", fn);
   if (tile_m <= 0 || tile_n <= 0 || tile_k <= 0)
     return loom_fail(err, errlen, LOOM_EINVAL, "%s: tile sizes must be positive", fn);
   const int64_t em = loom_fit_tile(tile_m, M, kGemmTiles, 3);
@@ -1169,9 +1169,10 @@ int batch_matmul_impl(const void* arg0, const void* arg1, void* arg2, int64_t Bt
     return loom_fail(err, errlen, LOOM_EINVAL,
                      "batch_matmul: tile_b=%lld exceeds its extent B=%lld (natural_ub)",
                      (long long)tile_b, (long long)Bt);
-  const int64_t tiles = cdiv64(M, wg) * cdiv64(N, wg) * Bt;
-  if (tiles > 0x7fffffff)
-    return loom_fail(err, errlen, LOOM_EINVAL, "batch_matmul: grid too large");
+  if (!loom_prod_le({cdiv64(M, wg), cdiv64(N, wg), Bt}, 0x7fffffff) ||
+      !loom_prod_le({Bt, M, K}, (int64_t)1 << 50) || !loom_prod_le({Bt, N, K}, (int64_t)1 << 50) ||
+      !loom_prod_le({Bt, M, N}, (int64_t)1 << 50))
+    return loom_fail(err, errlen, LOOM_EINVAL, "batch_matmul: problem too large");
   GemmParams p{};
   p.A = static_cast<const uint16_t*>(arg0);
   p.B = static_cast<const uint16_t*>(arg1);
@@ -1206,13 +1207,15 @@ int split_k_matmul_gather_impl(const void* a, const void* b, void* out, void* pa
                              "split_k_matmul_gather", err, errlen);
   if (rc) return rc;
   const int64_t S = cdiv64(K, tile_k);
+  if (!loom_prod_le({S, cdiv64(M, wg), cdiv64(N, wg)}, 0x7fffffff) ||
+      !loom_prod_le({S, M, N}, (int64_t)1 << 46) || !loom_prod_le({M, K}, (int64_t)1 << 50) ||
+      !loom_prod_le({N, K}, (int64_t)1 << 50))
+    return loom_fail(err, errlen, LOOM_EINVAL, "split_k_matmul_gather: problem too large");
   const size_t need = loom_hip_split_k_workspace_bytes(M, N, K, tile_k);
   if (!partials || partials_bytes < need)
     return loom_fail(err, errlen, LOOM_EINVAL,
                      "split_k_matmul_gather: partials workspace needs %zu bytes, got %zu", need,
                      partials_bytes);
-  if (S * cdiv64(M, wg) * cdiv64(N, wg) > 0x7fffffff)
-    return loom_fail(err, errlen, LOOM_EINVAL, "split_k_matmul_gather: grid too large");
   hipStream_t st = static_cast<hipStream_t>(stream);
   GemmParams p{};
   p.A = static_cast<const uint16_t*>(a);
@@ -1255,6 +1258,8 @@ extern "C" {
 
 size_t loom_hip_split_k_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t tile_k) {
   if (M <= 0 || N <= 0 || K <= 0 || tile_k <= 0) return 0;
+  // a product that does not fit is reported as no size at all fits
+  if (!loom_prod_le({cdiv64(K, tile_k), M, N, 4}, INT64_MAX)) return SIZE_MAX;
   return (size_t)cdiv64(K, tile_k) * (size_t)M * (size_t)N * sizeof(float);
 }
 

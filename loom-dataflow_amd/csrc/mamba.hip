@@ -397,8 +397,10 @@ int chunk_scan_impl(
       !aligned16(out))
     return loom_fail(err, errlen, LOOM_EINVAL, "%s: tensors must be 16-byte aligned", fn);
   const int64_t nmt = cdiv64(chunk_size, tile_m), npt = cdiv64(headdim, tile_n);
-  const int64_t nblocks = batch * nchunks * nheads * nmt * npt;
-  if (nblocks > 0x7fffffff || batch * nheads * nchunks * chunk_size * headdim > (1ll << 40))
+  if (!loom_prod_le({batch, nchunks, nheads, nmt, npt}, 0x7fffffff) ||
+      !loom_prod_le({batch, nheads, nchunks, chunk_size, headdim}, (int64_t)1 << 40) ||
+      !loom_prod_le({batch, nchunks, nheads, dstate, headdim}, (int64_t)1 << 40) ||
+      !loom_prod_le({batch, nchunks, ngroups, chunk_size, chunk_size}, (int64_t)1 << 40))
     return loom_fail(err, errlen, LOOM_EINVAL, "%s: problem too large", fn);
   MambaParams p{};
   p.cb = static_cast<const uint16_t*>(cb);

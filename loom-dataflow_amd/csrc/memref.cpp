@@ -149,6 +149,14 @@ int unpack(const Func& f, const void* const* descs, int ndescs, bool f16,
     if (!descs[i])
       return fail(err, errlen, LOOM_HIP_EINVAL, "%s: %s: null descriptor", f.name, f.args[i].name);
     v[i] = view_of(descs[i], f.args[i].rank);
+    // bounded before any arithmetic on them (no extent reaches 2^31)
+    for (int r = 0; r < f.args[i].rank; ++r)
+      if (v[i].sizes[r] < 0 || v[i].sizes[r] >= ((int64_t)1 << 31))
+        return fail(err, errlen, LOOM_HIP_EINVAL, "%s: %s: size %lld out of range", f.name,
+                    f.args[i].name, (long long)v[i].sizes[r]);
+    if (v[i].offset < 0 || v[i].offset >= ((int64_t)1 << 56))
+      return fail(err, errlen, LOOM_HIP_EINVAL, "%s: %s: %s offset %lld", f.name, f.args[i].name,
+                  v[i].offset < 0 ? "negative" : "out-of-range", (long long)v[i].offset);
   }
   dims = dims_of(f.name, v);
   const auto shapes = shapes_of(f.name, dims);
@@ -164,9 +172,6 @@ int unpack(const Func& f, const void* const* descs, int ndescs, bool f16,
                     list(m.sizes, a.rank).c_str(), list(want.data(), a.rank).c_str());
     if (!m.aligned)
       return fail(err, errlen, LOOM_HIP_EINVAL, "%s: %s: null aligned pointer", f.name, a.name);
-    if (m.offset < 0)
-      return fail(err, errlen, LOOM_HIP_EINVAL, "%s: %s: negative offset %lld", f.name, a.name,
-                  (long long)m.offset);
     int64_t expect = 1;
     for (int r = a.rank - 1; r >= 0; --r) {
       if (m.sizes[r] != 1 && m.strides[r] != expect) {
@@ -174,7 +179,7 @@ int unpack(const Func& f, const void* const* descs, int ndescs, bool f16,
         int64_t e = 1;
         for (int q = a.rank - 1; q >= 0; --q) {
           rowmajor[q] = e;
-          e *= m.sizes[q];
+          if (__builtin_mul_overflow(e, m.sizes[q], &e)) e = INT64_MAX;
         }
         return fail(err, errlen, LOOM_HIP_EINVAL,
                     "%s: %s: strides %s are not the row-major contiguous layout %s the kernels "
@@ -183,7 +188,8 @@ int unpack(const Func& f, const void* const* descs, int ndescs, bool f16,
                     list(rowmajor.data(), a.rank).c_str(),
                     r == a.rank - 1 ? " (innermost stride must be 1)" : "");
       }
-      expect *= m.sizes[r];
+      if (__builtin_mul_overflow(expect, m.sizes[r], &expect))
+        return fail(err, errlen, LOOM_HIP_EINVAL, "%s: %s: too many elements", f.name, a.name);
     }
     const size_t esize = (a.kind == kSide && !f16) ? 4 : 2;
     ptrs[i] = static_cast<const char*>(m.aligned) + m.offset * (int64_t)esize;

@@ -481,7 +481,9 @@ int check_ssd(const char* fn, int64_t batch, int64_t nchunks, int64_t nheads, in
                      "%s: built for chunk_size <= %d, headdim <= %d, dstate <= 128 "
                      "(a multiple of 32 above 32)",
                      fn, kSsdQmax, kSsdPmax);
-  if (batch * nheads * nchunks * chunk_size * headdim >= (int64_t)1 << 40)
+  if (!loom_prod_le({batch, nheads, nchunks, chunk_size, headdim}, ((int64_t)1 << 40) - 1) ||
+      !loom_prod_le({batch, nchunks, nheads, dstate, headdim}, (int64_t)1 << 40) ||
+      !loom_prod_le({batch, ngroups, nchunks, chunk_size, dstate}, (int64_t)1 << 40))
     return loom_fail(err, errlen, LOOM_EINVAL, "%s: problem too large", fn);
   return LOOM_OK;
 }
@@ -499,7 +501,8 @@ int loom_hip_ssd_chunk_cumsum(const void* dt, const void* A, void* dA_cumsum, in
     return loom_fail(err, errlen, LOOM_EINVAL, "ssd_chunk_cumsum: extents must be positive");
   if (chunk_size > 512)
     return loom_fail(err, errlen, LOOM_EUNSUP, "ssd_chunk_cumsum: chunk_size above 512");
-  if (batch * nheads * nchunks > 0x7fffffff / 64)
+  if (!loom_prod_le({batch, nheads, nchunks, chunk_size}, (int64_t)1 << 40) ||
+      !loom_prod_le({batch, nheads, nchunks}, 0x7fffffff / 64))
     return loom_fail(err, errlen, LOOM_EINVAL, "ssd_chunk_cumsum: problem too large");
   const int per_lane = (int)((chunk_size + 63) / 64);
   if (loom_validate_only()) return loom_ok(err, errlen);

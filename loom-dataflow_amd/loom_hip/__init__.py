@@ -23,7 +23,9 @@ import os
 import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(os.path.dirname(_HERE), "libloom_hip.so")
+# LOOM_HIP_LIB selects another build of the same library (the host-side
+# sanitizer build used by tests/test_sanitizers.py)
+LIB_PATH = os.environ.get("LOOM_HIP_LIB") or os.path.join(os.path.dirname(_HERE), "libloom_hip.so")
 
 if not os.path.exists(LIB_PATH):
     raise ImportError(f"loom_hip: {LIB_PATH} is not built (run __graft_entry__.build())")
