@@ -29,6 +29,7 @@ GPU time (clocks take on the order of 100 ms of load to settle).
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
                        [--no-ceilings] [--kernels all|none|mm,bmm,...]
        python bench.py --profile-workload all|mm,bmm,...   (for rocprofv3 --pmc)
+       python bench.py --library-baselines   (PyTorch / hipBLASLt / SDPA on the same shapes)
 """
 import argparse
 import json
@@ -68,7 +69,59 @@ def parse():
                          "calibration copy, then three calls of each listed kernel (comma "
                          "list of the table's names, or 'all'), the Infinity Cache flushed "
                          "by a read-only pass before each call")
+    ap.add_argument("--library-baselines", action="store_true",
+                    help="only time the libraries of this image on the table's shapes: "
+                         "torch.matmul / torch.bmm (hipBLASLt) for mm, bmm and the split-K "
+                         "shape, scaled_dot_product_attention for flashattn (causal) and "
+                         "mqa_decode (enable_gqa, one KV head); one JSON line")
     return ap.parse_args()
+
+
+def library_baselines(torch, iters=30):
+    """The same shapes through the libraries this image ships (no counterpart
+    exists for the Mamba-2 kernels): a reference point for each kernel, not a
+    parity check."""
+    import torch.nn.functional as F
+    bf = torch.bfloat16
+    g = torch.Generator(device="cuda")
+    g.manual_seed(7)
+
+    def randn(*shape, std=1.0):
+        return (torch.randn(*shape, generator=g, device="cuda") * std).to(bf)
+
+    def timed(fn):
+        settle(torch, lambda i: fn(), 100)
+        return time_back_to_back(torch, lambda i: fn(), iters)
+
+    out = {}
+    a, b = randn(1024, 1024), randn(1024, 1024)
+    ms = timed(lambda: torch.matmul(a, b))
+    out["mm"] = {"library": "torch.matmul (hipBLASLt)", "ms": round(ms, 5),
+                 "tflops": round(2 * 1024 ** 3 / ms / 1e9, 2)}
+    a, b = randn(16, 2048, 2048, std=0.02), randn(16, 2048, 2048, std=0.02)
+    ms = timed(lambda: torch.bmm(a, b))
+    out["bmm"] = {"library": "torch.bmm (hipBLASLt)", "ms": round(ms, 5),
+                  "tflops": round(16 * 2 * 2048 ** 3 / ms / 1e9, 2)}
+    a, b = randn(512, 16384, std=0.02), randn(16384, 512, std=0.02)
+    ms = timed(lambda: torch.matmul(a, b))
+    out["split_k"] = {"library": "torch.matmul (hipBLASLt), same product", "ms": round(ms, 5),
+                      "tflops": round(2 * 512 * 512 * 16384 / ms / 1e9, 2)}
+    del a, b
+    B, H, S, D = 4, 32, 4096, 128
+    q, k, v = randn(B, H, S, D), randn(B, H, S, D), randn(B, H, S, D)
+    with torch.nn.attention.sdpa_kernel(torch.nn.attention.SDPBackend.FLASH_ATTENTION):
+        ms = timed(lambda: F.scaled_dot_product_attention(q, k, v, is_causal=True))
+    out["flashattn"] = {"library": "scaled_dot_product_attention, flash backend, causal",
+                        "ms": round(ms, 5), "tflops": round(2 * B * H * S * S * D / ms / 1e9, 2)}
+    del q, k, v
+    Bd, Hd, Sd = 32, 32, 8192
+    qd, kd, vd = randn(Bd, Hd, 1, D), randn(Bd, 1, Sd, D), randn(Bd, 1, Sd, D)
+    with torch.nn.attention.sdpa_kernel(torch.nn.attention.SDPBackend.FLASH_ATTENTION):
+        ms = timed(lambda: F.scaled_dot_product_attention(qd, kd, vd, enable_gqa=True))
+    out["mqa_decode"] = {"library": "scaled_dot_product_attention, flash backend, enable_gqa",
+                         "ms": round(ms, 5), "gbs": round(2 * Bd * Sd * D * 2 / ms / 1e6, 1)}
+    out["mamba_chunk_scan"] = out["mamba_prologue"] = None   # no library implementation here
+    return out
 
 
 def traffic_for(kernel):
@@ -462,6 +515,11 @@ def main():
     torch.cuda.set_device(0)
     print(f"# device: {torch.cuda.get_device_name(0)}; {lh.__version__}", file=sys.stderr,
           flush=True)
+
+    if args.library_baselines:
+        print(json.dumps({"library_baselines": library_baselines(torch),
+                          "device": torch.cuda.get_device_name(0)}), flush=True)
+        return
 
     if args.traffic_probe:
         # profiled under rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE: the copy
