@@ -14,6 +14,7 @@
 #include <stdio.h>
 
 #include <algorithm>
+#include <atomic>
 #include <initializer_list>
 
 #include "../../include/loom_hip.h"   // every entry point matches its declaration
@@ -178,6 +179,29 @@ static inline int loom_check_launch(char* err, size_t errlen, const char* what) 
 }
 
 static inline int64_t cdiv64(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// CU count of the device `st` belongs to (the null stream: the current
+// device), cached per device; 0 when unknown.
+inline int stream_cus(hipStream_t st) {
+  static std::atomic<int> cache[64];   // count + 1; 0 = not queried yet
+  int dev = 0;
+  if (st != nullptr) {
+    hipDevice_t d = 0;
+    if (hipStreamGetDevice(st, &d) != hipSuccess) return 0;
+    dev = (int)d;
+  } else if (hipGetDevice(&dev) != hipSuccess) {
+    return 0;
+  }
+  if (dev < 0 || dev >= 64) return 0;
+  int c = cache[dev].load(std::memory_order_relaxed);
+  if (c == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) n = 0;
+    c = n + 1;
+    cache[dev].store(c, std::memory_order_relaxed);
+  }
+  return c - 1;
+}
 
 // Whether the product of non-negative extents stays within `limit`, computed
 // without signed overflow (caller-supplied extents can be anything).

@@ -956,36 +956,12 @@ __global__ void __launch_bounds__(256) gemm_persist_kernel(GemmParams p, int nr)
   }
 }
 
-// CU count of the device `st` belongs to (the null stream: the current
-// device), cached per device; 0 when unknown (the persistent kernel is then
-// not used).
-int device_cus(hipStream_t st) {
-  static std::atomic<int> cache[64];   // count + 1; 0 = not queried yet
-  int dev = 0;
-  if (st != nullptr) {
-    hipDevice_t d = 0;
-    if (hipStreamGetDevice(st, &d) != hipSuccess) return 0;
-    dev = (int)d;
-  } else if (hipGetDevice(&dev) != hipSuccess) {
-    return 0;
-  }
-  if (dev < 0 || dev >= 64) return 0;
-  int c = cache[dev].load(std::memory_order_relaxed);
-  if (c == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) n = 0;
-    c = n + 1;
-    cache[dev].store(c, std::memory_order_relaxed);
-  }
-  return c - 1;
-}
-
 // Launches the persistent kernel when every tile is whole, the tiles divide
 // evenly over one workgroup per CU (at least two each) and the pipelined
 // kernel's conditions hold; the caller falls back otherwise.
 template <bool H>
 bool launch_persist(const GemmParams& p, bool aligned, bool out_f32, hipStream_t st) {
-  const int cus = device_cus(st);
+  const int cus = stream_cus(st);   // 0 when unknown: the persistent kernel is then not used
   const int64_t ntiles = (int64_t)p.tiles_m * p.tiles_n * p.nz;
   const bool ok = aligned && !out_f32 && !p.split && cus >= 8 && cus % 8 == 0 &&
                   p.M % 256 == 0 && p.N % 256 == 0 && p.k_total % 128 == 0 && ntiles % cus == 0 &&
