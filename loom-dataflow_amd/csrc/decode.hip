@@ -9,22 +9,21 @@
 //   (:147-199): M = max_s lse_s, w_s = exp(lse_s - M) / sum exp(. - M),
 //   out = sum_s w_s o_s.
 //
-// gfx950 mapping.  Decode is bound by streaming K and V from HBM (the 32
-// heads give 32 FLOP per KV byte), so nothing goes through LDS on the way
-// in: each wave walks 64-key blocks, pulling K and V straight into
-// registers with raw buffer loads, and builds the MFMA operands with
-// register transposes (v_perm_b32):
-//   S^T[key, head] = K^T . Q^T  -- A operand from 8-byte K loads (four keys
-//                                 of eight d rows) transposed 8x4
-//   O^T[d, head]  += V^T . P^T  -- B operand P^T comes straight from the
-//                                 S^T accumulators, A operand V^T from
-//                                 16-byte V row loads transposed.
-// Keys are permuted inside a block and the permutation is undone only where
-// results are addressed, which is sound because softmax and P.V do not
-// depend on the order of the keys.  Softmax runs in the log2 domain in fp32.
-// One workgroup (4 waves) per (batch, split); the waves' partial states
-// are merged through LDS into (lse_s, o_s), exactly the reference's
-// gathered tensors; a second kernel performs the split-0 combine.
+// gfx950 mapping.  Decode is bound by streaming K and V from HBM; the 32
+// heads sharing the KV head give 32 FLOP per KV byte, which at 8 TB/s is
+// more arithmetic than the fp32 VALU peak, so S^T = K^T . Q^T and
+// O^T += V^T . P^T run on MFMA and the kernel stays bound by the stream.
+// One workgroup (4 waves) per (batch, split):
+//   - decode_dma_kernel (S a multiple of 8): K and V stream through
+//     a four-stage ring of LDS-DMA stages and reach the MFMAs by transposed
+//     LDS reads (described at the kernel);
+//   - decode_split_kernel (S not a multiple of 8): raw buffer loads straight into
+//     registers, MFMA operands built by register transposes (v_perm_b32),
+//     keys permuted inside a block and the permutation undone only where
+//     results are addressed (softmax and P.V do not depend on key order).
+// Softmax runs in the log2 domain in fp32.  The waves' partial states merge
+// through LDS into (lse_s, o_s), exactly the reference's gathered tensors;
+// decode_combine_kernel performs the split-0 combine.
 #include "common.h"
 
 #include <cmath>
