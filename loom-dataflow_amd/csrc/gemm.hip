@@ -589,6 +589,8 @@ __global__ void __launch_bounds__(256) gemm_pipe_kernel(GemmParams p) {
   for (int i = 0; i < TT; ++i)
 #pragma unroll
     for (int j = 0; j < TT; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  // the zeros above are written by ordinary instructions; the first
+  // inline-asm MFMA that reads them as srcC needs them retired
   mfma_drain();
 
   // ---- prologue: NS stages in flight, fragments of stage 0
@@ -647,6 +649,8 @@ __global__ void __launch_bounds__(256) gemm_pipe_kernel(GemmParams p) {
       step(u, it0 + u, af[u & 1], bfr[u & 1], af[(u & 1) ^ 1], bfr[(u & 1) ^ 1]);
   }
   LOOM_WAIT_VMCNT(0);   // the trailing re-reads land before the workgroup ends
+  // every MFMA has written its accumulator before the epilogue reads them
+  // (acc_fence keeps those reads after the drain)
   mfma_drain();
   acc_fence(acc);
 
@@ -915,7 +919,10 @@ __global__ void __launch_bounds__(256) gemm_persist_kernel(GemmParams p, int nr)
             last ? sa : BK, last ? sb : (int64_t)BK * p.ldb);
     }
 
-    // ---- epilogue of tile r
+    // ---- epilogue of tile r: every MFMA of the tile has written its
+    // accumulator before they are read (acc_fence keeps the reads after the
+    // drain); the next tile's first MFMAs start from srcC = 0, so nothing
+    // clears them
     LOOM_WAIT_VMCNT(0);
     mfma_drain();
     acc_fence(acc);

@@ -66,6 +66,19 @@ def test_matmul_f16(lh, tile):
                                   oracle.matmul(xi, yi, 64, 64, 64))
 
 
+def test_batch_matmul_f16_persistent_bit_exact(lh):
+    """The f16 form of the persistent 256x256 kernel (16 x 2048^2 x 128: 1024
+    tiles, four per CU on a 256-CU part) on integer-valued inputs: every
+    output element exact."""
+    rng = np.random.default_rng(53)
+    a = to_f16(rng.integers(-4, 5, (16, 2048, 128)).astype(np.float32))
+    b = to_f16(rng.integers(-4, 5, (16, 128, 2048)).astype(np.float32))
+    out = host(lh.batch_matmul(dev(a), dev(b), tile_m=256, tile_n=256))
+    with oracle.element_type("f16"):
+        for z in (0, 7, 15):
+            np.testing.assert_array_equal(out[z], oracle.matmul(a[z], b[z]), err_msg=str(z))
+
+
 def test_batch_matmul_f16(lh):
     rng = np.random.default_rng(52)
     a, b = rnd(rng, (2, 256, 128)), rnd(rng, (2, 128, 512))
