@@ -308,10 +308,13 @@ LOOM_DEV void dma_load16(const void* g, uint32_t lds) {
 // g = gcd(rb, 256), rows 256/g apart share a window offset and g/32 of them
 // fall among 8 consecutive rows; the XOR takes g/32 values below g/16, and
 // since rb is a multiple of g it keeps every chunk index inside its row.
+// g and pr are powers of two, so the division and the modulo are a shift and
+// a mask (k >= 0): no integer-division sequence when rb is only known at run
+// time.
 LOOM_DEV int tr_swz(int k, int rb) {
   const int g = (rb & -rb) < 256 ? (rb & -rb) : 256;  // gcd(rb, 256)
   const int pr = g >= 32 ? g / 32 : 1;                 // rows of a pass sharing an offset
-  return 2 * ((k / (256 / g)) % pr);
+  return 2 * ((k >> (8 - __builtin_ctz(g))) & (pr - 1));   // (k / (256 / g)) % pr
 }
 
 // ds_read_b64_tr_b16: in each 16-lane group, lanes 4a..4a+3 address the four
