@@ -30,7 +30,7 @@
 //                      exp(dA[c,Q-1]) and accumulates states(c), so the
 //                      chunk states never reach HBM.  x and B chunks are
 //                      staged in LDS ([k][p], [k][n]) and read as MFMA
-//                      operands with ds_read_b64_tr_b16; w_c scales B in
+//                      operands with ds_read_b64_tr_b16; w_c scales x in
 //                      fp32 and enters the MFMA as a bf16 hi + lo pair.
 #include "common.h"
 
@@ -285,15 +285,28 @@ __global__ void __launch_bounds__(64 * kSsdWaves) ssd_state_kernel(SsdStateParam
   const int nst = MODE == 2 ? (kq == 0 ? TPW : 0) : ntw;
   // w_c[k] = exp(dA[c, Q-1] - dA[c, k]) dt[c, k] of the current unit (zero
   // past its QS keys), one copy per wave in s_w[wave]: a wave writes and
-  // reads only its own row, so no barrier is involved.  dAs: the stage's dA
-  // (keys 0..127), dt (128..255) and dA[c, Q-4 .. Q-1] (256..259).
+  // reads only its own row, so no barrier is involved, and its LDS
+  // operations execute in order, so its reads of the row see its writes
+  // without a wait.  dAs: the stage's dA (keys 0..127), dt (128..255) and
+  // dA[c, Q-4 .. Q-1] (256..259); every one of the 256 was written by the
+  // unit's DMA (keys past QS repeat the last ones).  A wave computes the
+  // keys of its own k steps only: in MODE 2 steps kq and kq + 2, one key per
+  // lane; otherwise all QSP <= 128 keys, two per lane, both loads issued
+  // before either exp.
   float* const sw = s_w[wave];
+  const float kLog2e = 1.4426950408889634f;
   auto make_w = [&](const float* dAs) {
     const float last = dAs[256 + 3];
-    for (int i = lane; i < QSP; i += 64)
-      sw[i] = i < QS ? fast_exp2((last - dAs[i]) * 1.4426950408889634f) * dAs[128 + i] : 0.f;
-    LOOM_WAIT_LGKM0();
-    __asm__ volatile("" ::: "memory");
+    if constexpr (MODE == 2) {
+      const int s = kq + 2 * (lane >> 5), i = 32 * s + (lane & 31);
+      const float a = dAs[i], t = dAs[128 + i];
+      if (32 * s < QSP) sw[i] = i < QS ? fast_exp2((last - a) * kLog2e) * t : 0.f;
+    } else {
+      const int i0 = lane, i1 = lane + 64;
+      const float a0 = dAs[i0], t0 = dAs[128 + i0], a1 = dAs[i1], t1 = dAs[128 + i1];
+      if (i0 < QSP) sw[i0] = i0 < QS ? fast_exp2((last - a0) * kLog2e) * t0 : 0.f;
+      if (i1 < QSP) sw[i1] = i1 < QS ? fast_exp2((last - a1) * kLog2e) * t1 : 0.f;
+    }
   };
 
   // x^T operand (keys k0 + 0..3 from x0, k0 + 16..19 from x1) scaled by w
@@ -349,7 +362,7 @@ __global__ void __launch_bounds__(64 * kSsdWaves) ssd_state_kernel(SsdStateParam
     make_w(dAs);
     if (part == 0) {
       // prev(c) out, then R = exp(dA[c, Q-1]) R; states(c) accumulate below
-      const float decay = fast_exp2(dAs[256 + 3] * 1.4426950408889634f);
+      const float decay = fast_exp2(dAs[256 + 3] * kLog2e);
       float* outc = p.prevT + (((int64_t)(b * nc + c) * H + h) * N + n0) * P;
       if constexpr (MODE == 2) {
         const int pt = wave % ptiles;
