@@ -167,7 +167,9 @@ struct SsdStateParams {
 //         tiles (p tile w % (P/16), every n tile) and split the k steps
 //         between them (even / odd), so each scaled x operand is built once
 //         per workgroup; at each chunk start the odd wave hands its partial
-//         sums to the even wave through LDS, which stores prev(c).
+//         sums to the even wave through LDS, which stores prev(c).  The
+//         host picks MODE 2 only for P = 64 (four p tiles) with nb = 16 TPW,
+//         so both are compile-time constants there.
 template <int TPW, int MODE, bool F16>
 __global__ void __launch_bounds__(64 * kSsdWaves) ssd_state_kernel(SsdStateParams p) {
   __shared__ __attribute__((aligned(1024))) char smem[kSsdRing];
@@ -177,7 +179,8 @@ __global__ void __launch_bounds__(64 * kSsdWaves) ssd_state_kernel(SsdStateParam
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = lane & 15, gq = lane >> 4, a4 = r >> 2, c4 = r & 3;
   const int bh = blockIdx.x, nblk = blockIdx.y;
-  const int H = p.H, Q = p.Q, P = p.P, N = p.N, nb = p.nb, nc = p.nc;
+  const int H = p.H, Q = p.Q, N = p.N, nc = p.nc;
+  const int P = MODE == 2 ? 16 * (kSsdWaves / 2) : p.P, nb = MODE == 2 ? 16 * TPW : p.nb;
   const int b = bh / H, h = bh % H, g = h / (H / p.G);
   const int n0 = nblk * nb;
   const int L = nc * Q;
@@ -331,19 +334,35 @@ __global__ void __launch_bounds__(64 * kSsdWaves) ssd_state_kernel(SsdStateParam
     f32x4_t w0, w1;
     u32x2_t b0[TPW], b1[TPW];
   };
-  auto load_ops = [&](const lds_char_t* xs, const lds_char_t* bs, int ks, int pt, Ops& o) {
+  // Byte offset, within a stage's x (row width XR) or B (BR) rows, of the
+  // operand this lane reads for p or n tile `tile` at k step 0: row
+  // kk = 4 gq + a4, 16-byte chunk 2 tile + c4/2 under the row's swizzle.
+  // Step ks reads 32 ks rows further on, with the same swizzle: tr_swz reads
+  // bits 0..2 of the row only, so rows kk, kk + 16 and kk + 32 ks share it.
+  const int kk = 4 * gq + a4;
+  auto op_off = [&](int tile, int rb) {
+    return kk * rb + ((2 * tile + (c4 >> 1)) ^ tr_swz(kk, rb)) * 16 + (c4 & 1) * 8;
+  };
+  // the offsets of the wave's own tiles (MODES 1 and 2), computed once
+  int xo = 0, bo[TPW];
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) bo[t] = 0;
+  if constexpr (MODE >= 1) {
+    xo = op_off(wave % ptiles, XR);
+#pragma unroll
+    for (int t = 0; t < TPW; ++t)
+      bo[t] = op_off(MODE == 2 ? t : min(wave + kSsdWaves * t, tiles - 1) / ptiles, BR);
+  }
+  auto load_ops = [&](const lds_char_t* xs, const lds_char_t* bs, int ks, Ops& o) {
     const int k0 = 32 * ks + 4 * gq;          // this lane's keys: k0 + 0..3, k0 + 16..19
-    const lds_char_t* qx =
-        xs + (k0 + a4) * XR + ((2 * pt + (c4 >> 1)) ^ tr_swz(k0 + a4, XR)) * 16 + (c4 & 1) * 8;
+    const lds_char_t* qx = xs + 32 * ks * XR + xo;
     o.x0 = lds_read_tr16(qx);
     o.x1 = lds_read_tr16(qx + 16 * XR);
     o.w0 = *reinterpret_cast<const f32x4_t*>(sw + k0);
     o.w1 = *reinterpret_cast<const f32x4_t*>(sw + k0 + 16);
 #pragma unroll
     for (int t = 0; t < TPW; ++t) {
-      const int nt = MODE == 2 ? t : min(wave + kSsdWaves * t, tiles - 1) / ptiles;
-      const lds_char_t* qb =
-          bs + (k0 + a4) * BR + ((2 * nt + (c4 >> 1)) ^ tr_swz(k0 + a4, BR)) * 16 + (c4 & 1) * 8;
+      const lds_char_t* qb = bs + 32 * ks * BR + bo[t];
       o.b0[t] = lds_read_tr16(qb);
       o.b1[t] = lds_read_tr16(qb + 16 * BR);
     }
@@ -398,26 +417,31 @@ __global__ void __launch_bounds__(64 * kSsdWaves) ssd_state_kernel(SsdStateParam
       // all tiles of the wave share p tile wave % ptiles: one scaled x
       // operand per step (MODE 2: every other step); the next step's
       // operands are read while this step's MFMAs run
+      // (two operand sets alternate, so nothing is copied between steps,
+      // and the last step reads nothing ahead)
       constexpr int KSTEP = MODE == 2 ? 2 : 1;
-      const int ptw = wave % ptiles;
-      if (kq < nks) {
-        Ops cur;
-        load_ops(xs, bs, kq, ptw, cur);
-        for (int ks = kq; ks < nks; ks += KSTEP) {
-          Ops nxt;
-          load_ops(xs, bs, ks + KSTEP < nks ? ks + KSTEP : ks, ptw, nxt);
-          u32x4_t xh, xl;
-          scale_x(cur.x0, cur.x1, cur.w0, cur.w1, xh, xl);
+      auto step = [&](const Ops& o) {
+        u32x4_t xh, xl;
+        scale_x(o.x0, o.x1, o.w0, o.w1, xh, xl);
 #pragma unroll
-          for (int t = 0; t < TPW; ++t) {
-            if (t < ntw) {
-              const u32x4_t bf = u32x4_t{cur.b0[t][0], cur.b0[t][1], cur.b1[t][0], cur.b1[t][1]};
-              R[t] = mfma16t<F16>(xh, bf, R[t]);
-              R[t] = mfma16t<F16>(xl, bf, R[t]);
-            }
+        for (int t = 0; t < TPW; ++t) {
+          if (t < ntw) {
+            const u32x4_t bf = u32x4_t{o.b0[t][0], o.b0[t][1], o.b1[t][0], o.b1[t][1]};
+            R[t] = mfma16t<F16>(xh, bf, R[t]);
+            R[t] = mfma16t<F16>(xl, bf, R[t]);
           }
+        }
+      };
+      if (kq < nks) {
+        Ops oa, ob;
+        load_ops(xs, bs, kq, oa);
+        for (int ks = kq; ks < nks; ks += 2 * KSTEP) {
+          if (ks + KSTEP < nks) load_ops(xs, bs, ks + KSTEP, ob);
+          step(oa);
           if (ks == kq && pre) issue(sn, un, 0, half);
-          cur = nxt;
+          if (ks + KSTEP >= nks) break;
+          if (ks + 2 * KSTEP < nks) load_ops(xs, bs, ks + 2 * KSTEP, oa);
+          step(ob);
         }
       } else if (pre) {
         issue(sn, un, 0, half);
@@ -432,14 +456,12 @@ __global__ void __launch_bounds__(64 * kSsdWaves) ssd_state_kernel(SsdStateParam
           const int tt = wave + kSsdWaves * t;
           if (tt < tiles) {
             const int pt = tt % ptiles, nt = tt / ptiles;
-            const lds_char_t* qx = xs + (k0 + a4) * XR +
-                                   ((2 * pt + (c4 >> 1)) ^ tr_swz(k0 + a4, XR)) * 16 + (c4 & 1) * 8;
+            const lds_char_t* qx = xs + 32 * ks * XR + op_off(pt, XR);
             u32x4_t xh, xl;
             scale_x(lds_read_tr16(qx), lds_read_tr16(qx + 16 * XR),
                     *reinterpret_cast<const f32x4_t*>(sw + k0),
                     *reinterpret_cast<const f32x4_t*>(sw + k0 + 16), xh, xl);
-            const lds_char_t* qb = bs + (k0 + a4) * BR +
-                                   ((2 * nt + (c4 >> 1)) ^ tr_swz(k0 + a4, BR)) * 16 + (c4 & 1) * 8;
+            const lds_char_t* qb = bs + 32 * ks * BR + op_off(nt, BR);
             const u32x2_t blo = lds_read_tr16(qb), bhi = lds_read_tr16(qb + 16 * BR);
             const u32x4_t bf = u32x4_t{blo[0], blo[1], bhi[0], bhi[1]};
             R[t] = mfma16t<F16>(xh, bf, R[t]);
