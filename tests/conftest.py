@@ -42,6 +42,22 @@ def assert_close(actual, expected, atol, rtol, what=""):
             f"worst at {idx}: got {a[idx]!r} expected {e[idx]!r}; max abs err {err.max():.3e}")
 
 
+def assert_close_gpu(actual, expected, atol, rtol, what=""):
+    """assert_close for torch tensors on the GPU (full BASELINE-size outputs,
+    too large to copy and compare in numpy): compared in fp32 there."""
+    import torch
+    a, e = actual.float(), expected.float()
+    assert a.shape == e.shape, (tuple(a.shape), tuple(e.shape))
+    err = (a - e).abs()
+    bad = ~(err <= atol + rtol * e.abs())
+    nbad = int(bad.sum())
+    if nbad:
+        i = int(torch.argmax(torch.where(bad, err, torch.zeros_like(err))))
+        raise AssertionError(
+            f"{what}: {nbad}/{a.numel()} elements outside atol={atol} rtol={rtol}; worst at flat "
+            f"index {i}: got {float(a.flatten()[i])!r} expected {float(e.flatten()[i])!r}")
+
+
 GEMM_TILES = (64, 128, 256)
 ATTN_TILES = (64, 128, 192, 256)
 MAMBA_M_TILES = (64, 128, 192, 256)
