@@ -11,10 +11,14 @@
 // The k <= m mask is the Mamba-2 intra-chunk causal mask, applied with a
 // select; the reference loop has none and would overflow exp() there.
 //
-// gfx950 mapping.  One workgroup (4 waves) per (b, h, c, m-tile, p-tile);
-// logical ids are ordered (b, c, h, tile) and remapped so that each XCD owns
-// whole (b, c) groups: the heads that share cb and C then run together on
-// one L2.  Per workgroup:
+// gfx950 mapping.  One workgroup per (b, h, c, m-tile, p-tile): 8 waves when
+// the m-tile holds 8 or more 16-row tiles, else 4; logical ids are ordered
+// (b, c, h, tile) and remapped so that each XCD owns whole (b, c) groups:
+// the heads that share cb and C then run together on one L2.  The 8-wave
+// form fits 128 VGPRs, so two of its workgroups (67 KB of LDS each at
+// tile_n 64) give every SIMD four waves to switch between while one waits
+// on its row loads or LDS reads (BASELINE shape: 93.8 -> 83.0 us against two
+// 4-wave workgroups per CU).  Per workgroup:
 //   - x[k, p] (k < m-tile end) is copied to LDS transposed (xT [p][k]) by
 //     8x8 register transposes: the B operand of W . x; xT and pT rows XOR
 //     their 16-byte chunk index with row & 15, so the 16 rows a ds_read_b128
@@ -40,7 +44,6 @@ namespace {
 
 constexpr int kQmax = 256;   // chunk length
 constexpr int kNmax = 128;   // state size
-constexpr int kWaves = 4;
 
 struct MambaParams {
   const uint16_t* cb;
@@ -67,8 +70,12 @@ LOOM_DEV float side_at(const void* __restrict__ t, int64_t i) {
     return reinterpret_cast<const float* __restrict__>(t)[i];
 }
 
-template <int PT, bool F16>  // p tiles of 16 per workgroup (tile_n = 16 PT); F16: f16 elements
-__global__ void __launch_bounds__(64 * kWaves) mamba_chunk_scan_kernel(MambaParams p) {
+// PT: p tiles of 16 per workgroup (tile_n = 16 PT); F16: f16 elements;
+// kWaves: 4 or 8 waves (the 8-wave form is held to 128 VGPRs: four waves per
+// SIMD)
+template <int PT, bool F16, int kWaves>
+__global__ void __launch_bounds__(64 * kWaves, kWaves == 8 ? 4 : 1)
+    mamba_chunk_scan_kernel(MambaParams p) {
   constexpr int TN = 16 * PT;
   constexpr int XROW = kQmax / 8;   // 16-byte chunks per xT row
   constexpr int PROW = kNmax / 8;   // 16-byte chunks per pT row
@@ -112,12 +119,15 @@ __global__ void __launch_bounds__(64 * kWaves) mamba_chunk_scan_kernel(MambaPara
   // ---- staging: every global load first, then conversions and LDS stores.
   // One 8x8 block of x per thread (k-chunk fastest; k rounded up to the
   // 32-deep MFMA step, rows past the chunk zero-filled), one 8x8 block of
-  // prevT for the first nch*pch threads, one dA and dt value per thread.
+  // prevT for the first nch*pch threads (from thread 256 on with 8 waves, so
+  // no thread stages both), one dA and dt value per thread.
   const int kch = ((mend + 31) / 32) * 4, pch = TN / 8;
   const int nch = ((N + 31) / 32) * 4;
-  const bool do_x = tid < kch * pch, do_p = tid < nch * pch;
+  constexpr int pbase = kWaves == 8 ? 256 : 0;   // kch * pch <= 256
+  const int tp = tid - pbase;
+  const bool do_x = tid < kch * pch, do_p = tp >= 0 && tp < nch * pch;
   const int x_kc = tid % kch, x_pc = tid / kch;
-  const int p_nc = tid % nch, p_pc = tid / nch;
+  const int p_nc = tp % nch, p_pc = tp / nch;
   u32x4_t xr[8];
   f32x4_t pr[8][2];
   float dA_v = 0.f, dt_v = 0.f, dA_e = 0.f;
@@ -207,12 +217,17 @@ __global__ void __launch_bounds__(64 * kWaves) mamba_chunk_scan_kernel(MambaPara
     return kWaves * ti + ((ti & 1) ? (kWaves - 1 - wave) : wave);
   };
   // C and cb rows come straight from global memory as MFMA operands.  A
-  // tile's loads are issued while the previous tile computes (two register
-  // sets); buffer loads read rows past the chunk as zeros.
+  // tile's C rows are loaded while the previous tile computes (two register
+  // sets); so are its cb rows with 4 waves, while with 8 waves (128 VGPRs)
+  // they are loaded at the tile's start, behind its state term's MFMAs.
+  // Buffer loads read rows past the chunk as zeros.
   const rsrc_t rC = make_rsrc(Cg, (uint32_t)(Q * N * 2));
   const rsrc_t rCB = make_rsrc(cbg, (uint32_t)(Q * Q * 2));
-  struct Rows {
+  constexpr bool kCbAhead = kWaves == 4;
+  struct CRows {
     u32x4_t c[NSN];
+  };
+  struct BRows {
     u32x4_t cb[NKS];
   };
   // Every load is issued, unneeded ones with an offset past the
@@ -220,13 +235,16 @@ __global__ void __launch_bounds__(64 * kWaves) mamba_chunk_scan_kernel(MambaPara
   // count the loads younger than the ones it waits for, where a
   // conditional load makes it wait for all of them, prefetch included.
   constexpr uint32_t kNone = 0x7ffffff0u;
-  auto fetch = [&](int ti, Rows& rw) {
-    const int mrow0 = m0 + 16 * tile_of(ti);
-    const int am = mrow0 + rr;
-    const int kend = min(mrow0 + 16, Q);
+  auto fetch_c = [&](int ti, CRows& rw) {
+    const int am = m0 + 16 * tile_of(ti) + rr;
 #pragma unroll
     for (int ns = 0; ns < NSN; ++ns)
       rw.c[ns] = buf_load16(rC, ns * 32 < N ? (uint32_t)(am * N + ns * 32 + g4 * 8) * 2 : kNone);
+  };
+  auto fetch_cb = [&](int ti, BRows& rw) {
+    const int mrow0 = m0 + 16 * tile_of(ti);
+    const int am = mrow0 + rr;
+    const int kend = min(mrow0 + 16, Q);
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks)
       rw.cb[ks] = buf_load16(rCB, ks * 32 < kend ? (uint32_t)(am * Q + ks * 32 + g4 * 8) * 2 : kNone);
@@ -236,13 +254,20 @@ __global__ void __launch_bounds__(64 * kWaves) mamba_chunk_scan_kernel(MambaPara
   // as the column operand): lane (rr, g4) of tile (ti, pt) accumulates
   // out[m = mrow0 + rr][p = 16 pt + 4 g4 + i], four consecutive columns.
   uint16_t* og = p.out + ((int64_t)(b * H + h) * L + (int64_t)c * Q) * P;
-  Rows rowbuf[2];
-  fetch(0, rowbuf[0]);
+  CRows cbuf[2];
+  BRows bbuf[kCbAhead ? 2 : 1];
+  fetch_c(0, cbuf[0]);
+  if constexpr (kCbAhead) fetch_cb(0, bbuf[0]);
 #pragma unroll
   for (int ti = 0; ti < MAXT; ++ti) {
     if (tile_of(ti) >= nmt16) continue;
-    if (ti + 1 < MAXT) fetch(ti + 1, rowbuf[(ti + 1) & 1]);
-    const Rows& rw = rowbuf[ti & 1];
+    if constexpr (!kCbAhead) fetch_cb(ti, bbuf[0]);
+    if (ti + 1 < MAXT) {
+      fetch_c(ti + 1, cbuf[(ti + 1) & 1]);
+      if constexpr (kCbAhead) fetch_cb(ti + 1, bbuf[(ti + 1) & 1]);
+    }
+    const u32x4_t(&rc)[NSN] = cbuf[ti & 1].c;
+    const u32x4_t(&rcb)[NKS] = bbuf[kCbAhead ? (ti & 1) : 0].cb;
     const int mrow0 = m0 + 16 * tile_of(ti);
     const int am = mrow0 + rr;  // this lane's output row
     // state and intra-chunk terms accumulate separately and meet only at the
@@ -262,8 +287,8 @@ __global__ void __launch_bounds__(64 * kWaves) mamba_chunk_scan_kernel(MambaPara
       for (int pt = 0; pt < PT; ++pt) {
         const int pp = pt * 16 + rr;
         const int ch = (ns * 4 + g4) ^ (pp & 15);
-        acc_s[pt] = mfma16t<F16>(pT[0][pp * PROW + ch], rw.c[ns], acc_s[pt]);
-        if constexpr (!F16) acc_s[pt] = mfma16t<F16>(pT[1][pp * PROW + ch], rw.c[ns], acc_s[pt]);
+        acc_s[pt] = mfma16t<F16>(pT[0][pp * PROW + ch], rc[ns], acc_s[pt]);
+        if constexpr (!F16) acc_s[pt] = mfma16t<F16>(pT[1][pp * PROW + ch], rc[ns], acc_s[pt]);
       }
     }
     const float dAm = am < Q ? s_dA[am] : 0.f;
@@ -287,7 +312,7 @@ __global__ void __launch_bounds__(64 * kWaves) mamba_chunk_scan_kernel(MambaPara
         const float vm = fast_exp2(dAm - s_dA[ks * 32 + 31]);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const uint32_t word = rw.cb[ks][e >> 1];
+          const uint32_t word = rcb[ks][e >> 1];
           const float cbf = (e & 1) ? hi16<F16>(word) : lo16<F16>(word);
           wv[e] = cbf * (e < 4 ? u0[e] : u1[e - 4]) * vm;
         }
@@ -299,7 +324,7 @@ __global__ void __launch_bounds__(64 * kWaves) mamba_chunk_scan_kernel(MambaPara
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const int k = kb + e;
-          const uint32_t word = rw.cb[ks][e >> 1];
+          const uint32_t word = rcb[ks][e >> 1];
           const float cbf = (e & 1) ? hi16<F16>(word) : lo16<F16>(word);
           const float dAk = e < 4 ? dA0[e] : dA1[e - 4];
           const float dtk = e < 4 ? dt0[e] : dt1[e - 4];
@@ -341,8 +366,13 @@ __global__ void __launch_bounds__(64 * kWaves) mamba_chunk_scan_kernel(MambaPara
 template <int PT, bool F16>
 void launch_mamba(const MambaParams& p, hipStream_t st) {
   const int64_t nblocks = (int64_t)p.Bb * p.nc * p.H * p.nmt * p.npt;
-  hipLaunchKernelGGL((mamba_chunk_scan_kernel<PT, F16>), dim3((unsigned)nblocks), dim3(64 * kWaves), 0,
-                     st, p);
+  // 8 waves when the m-tile holds 8 or more 16-row tiles (tile_m >= 128)
+  if (p.tile_m >= 128)
+    hipLaunchKernelGGL((mamba_chunk_scan_kernel<PT, F16, 8>), dim3((unsigned)nblocks), dim3(512), 0,
+                       st, p);
+  else
+    hipLaunchKernelGGL((mamba_chunk_scan_kernel<PT, F16, 4>), dim3((unsigned)nblocks), dim3(256), 0,
+                       st, p);
 }
 
 template <bool F16>
