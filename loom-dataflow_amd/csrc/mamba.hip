@@ -118,18 +118,19 @@ __global__ void __launch_bounds__(64 * kWaves, kWaves == 8 ? 4 : 1)
 
   // ---- staging: every global load first, then conversions and LDS stores.
   // One 8x8 block of x per thread (k-chunk fastest; k rounded up to the
-  // 32-deep MFMA step, rows past the chunk zero-filled), one 8x8 block of
-  // prevT for the first nch*pch threads (from thread 256 on with 8 waves, so
-  // no thread stages both), one dA and dt value per thread.
+  // 32-deep MFMA step, rows past the chunk zero-filled); half an 8x8 block
+  // of prevT (rows n = 8 p_nc + 0..7, columns p = 8 p_pc + 4 p_h + 0..3) for
+  // each of the first 2*nch*pch threads, from thread 256 on with 8 waves so
+  // no thread stages both; one dA and dt value per thread.
   const int kch = ((mend + 31) / 32) * 4, pch = TN / 8;
   const int nch = ((N + 31) / 32) * 4;
-  constexpr int pbase = kWaves == 8 ? 256 : 0;   // kch * pch <= 256
+  constexpr int pbase = kWaves == 8 ? 256 : 0;   // kch * pch <= 256, 2 nch pch <= 256
   const int tp = tid - pbase;
-  const bool do_x = tid < kch * pch, do_p = tp >= 0 && tp < nch * pch;
+  const bool do_x = tid < kch * pch, do_p = tp >= 0 && tp < 2 * nch * pch;
   const int x_kc = tid % kch, x_pc = tid / kch;
-  const int p_nc = tp % nch, p_pc = tp / nch;
+  const int p_h = tp & 1, p_nc = (tp >> 1) % nch, p_pc = (tp >> 1) / nch;
   u32x4_t xr[8];
-  f32x4_t pr[8][2];
+  f32x4_t pr[8];
   float dA_v = 0.f, dt_v = 0.f, dA_e = 0.f;
   if (tid < Q) {
     dA_v = side_at<F16>(p.dA, sidx + tid);
@@ -146,21 +147,19 @@ __global__ void __launch_bounds__(64 * kWaves, kWaves == 8 ? 4 : 1)
     }
   }
   if (do_p) {
-    const int pg = p0 + p_pc * 8;
+    const int pg = p0 + p_pc * 8 + 4 * p_h;   // P % 8 == 0: pg < P covers pg + 3
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const int n = p_nc * 8 + e;
       if (n < N && pg < P) {
         if constexpr (F16) {
-          const u32x4_t w = *reinterpret_cast<const u32x4_t*>(pvh + (int64_t)n * P + pg);
-          pr[e][0] = f32x4_t{lo16<true>(w[0]), hi16<true>(w[0]), lo16<true>(w[1]), hi16<true>(w[1])};
-          pr[e][1] = f32x4_t{lo16<true>(w[2]), hi16<true>(w[2]), lo16<true>(w[3]), hi16<true>(w[3])};
+          const u32x2_t w = *reinterpret_cast<const u32x2_t*>(pvh + (int64_t)n * P + pg);
+          pr[e] = f32x4_t{lo16<true>(w[0]), hi16<true>(w[0]), lo16<true>(w[1]), hi16<true>(w[1])};
         } else {
-          pr[e][0] = *reinterpret_cast<const f32x4_t*>(pvg + (int64_t)n * P + pg);
-          pr[e][1] = *reinterpret_cast<const f32x4_t*>(pvg + (int64_t)n * P + pg + 4);
+          pr[e] = *reinterpret_cast<const f32x4_t*>(pvg + (int64_t)n * P + pg);
         }
       } else {
-        pr[e][0] = pr[e][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        pr[e] = f32x4_t{0.f, 0.f, 0.f, 0.f};
       }
     }
   }
@@ -182,27 +181,23 @@ __global__ void __launch_bounds__(64 * kWaves, kWaves == 8 ? 4 : 1)
     }
   }
   if (do_p) {
-    // prevT split into bf16 hi + lo (the state term keeps ~16 mantissa bits);
-    // an f16 prevT is exact in f16, so its lo half is zero and never used
-    u32x4_t hi[8], lo[8], thi[8], tlo[8];
+    // prevT split into bf16 hi + lo (the state term keeps ~16 mantissa bits),
+    // packed straight into the transposed layout: dword j of pT row p holds
+    // n = 8 p_nc + 2j, 2j + 1.  An f16 prevT is exact in f16, so its lo half
+    // is zero and never used.
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float v[8] = {pr[e][0][0], pr[e][0][1], pr[e][0][2], pr[e][0][3],
-                          pr[e][1][0], pr[e][1][1], pr[e][1][2], pr[e][1][3]};
+    for (int i = 0; i < 4; ++i) {
+      const int pp = p_pc * 8 + 4 * p_h + i;
+      u32x4_t hi, lo;
 #pragma unroll
-      for (int z = 0; z < 4; ++z) {
-        const uint32_t hw = pack2<F16>(v[2 * z], v[2 * z + 1]);
-        hi[e][z] = hw;
-        lo[e][z] = pack2<F16>(v[2 * z] - lo16<F16>(hw), v[2 * z + 1] - hi16<F16>(hw));
+      for (int j = 0; j < 4; ++j) {
+        const float a = pr[2 * j][i], c = pr[2 * j + 1][i];
+        const uint32_t hw = pack2<F16>(a, c);
+        hi[j] = hw;
+        lo[j] = pack2<F16>(a - lo16<F16>(hw), c - hi16<F16>(hw));
       }
-    }
-    transpose8x8(hi, thi);
-    if constexpr (!F16) transpose8x8(lo, tlo);
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int pp = p_pc * 8 + u;
-      pT[0][pp * PROW + (p_nc ^ (pp & 15))] = thi[u];
-      if constexpr (!F16) pT[1][pp * PROW + (p_nc ^ (pp & 15))] = tlo[u];
+      pT[0][pp * PROW + (p_nc ^ (pp & 15))] = hi;
+      if constexpr (!F16) pT[1][pp * PROW + (p_nc ^ (pp & 15))] = lo;
     }
   }
   __syncthreads();
