@@ -394,7 +394,7 @@ def make_cases(torch, lh):
             *sets[i % n], tile_m=256, tile_n=64, tile_k=64),
             flop=flop, bytes=nb, bound="hbm", sets=n, inputs=sets,
             desc="mamba chunk_scan b4 L4096 h32 P64 N128 g1 Q256", cpu=cpu,
-            kernel="mamba_chunk_scan_kernel<4, false>")
+            kernel="mamba_chunk_scan_kernel<4, false, 8>")
     cases["mamba_chunk_scan"] = mamba
 
     def ssd():
