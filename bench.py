@@ -466,7 +466,7 @@ def report(case, ms, calls=None, ms_graph=None):
     return out
 
 
-def cpu_column(case, gpu_ms, reps=3, max_run_s=4.0):
+def cpu_column(case, gpu_ms, reps=5, max_run_s=4.0):
     """The fp32 C oracle (OpenMP, all host threads) on a stated slice of the
     same configuration: median of `reps` runs after one warm-up (a single run
     when one takes longer than `max_run_s`), scaled to the whole

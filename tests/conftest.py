@@ -27,6 +27,15 @@ def golden():
     return load_golden
 
 
+# every tolerance check of the run: (what, elements, max |err|, max |err|/|ref|
+# over |ref| >= atol, largest err / (atol + rtol |ref|)), printed at the end
+ERRORS = []
+
+
+def _record(what, n, max_abs, max_rel, used):
+    ERRORS.append((what, n, max_abs, max_rel, used))
+
+
 def assert_close(actual, expected, atol, rtol, what=""):
     """|actual - expected| <= atol + rtol * |expected| elementwise (NaN fails)."""
     a = np.asarray(actual, dtype=np.float64)
@@ -40,6 +49,11 @@ def assert_close(actual, expected, atol, rtol, what=""):
         raise AssertionError(
             f"{what}: {int(bad.sum())}/{a.size} elements outside atol={atol} rtol={rtol}; "
             f"worst at {idx}: got {a[idx]!r} expected {e[idx]!r}; max abs err {err.max():.3e}")
+    if a.size:
+        big = np.abs(e) >= atol
+        _record(what, a.size, float(err.max()),
+                float((err[big] / np.abs(e[big])).max()) if big.any() else 0.0,
+                float((err / bound).max()))
 
 
 def assert_close_gpu(actual, expected, atol, rtol, what=""):
@@ -49,13 +63,35 @@ def assert_close_gpu(actual, expected, atol, rtol, what=""):
     a, e = actual.float(), expected.float()
     assert a.shape == e.shape, (tuple(a.shape), tuple(e.shape))
     err = (a - e).abs()
-    bad = ~(err <= atol + rtol * e.abs())
+    bound = atol + rtol * e.abs()
+    bad = ~(err <= bound)
     nbad = int(bad.sum())
     if nbad:
         i = int(torch.argmax(torch.where(bad, err, torch.zeros_like(err))))
         raise AssertionError(
             f"{what}: {nbad}/{a.numel()} elements outside atol={atol} rtol={rtol}; worst at flat "
             f"index {i}: got {float(a.flatten()[i])!r} expected {float(e.flatten()[i])!r}")
+    if a.numel():
+        big = e.abs() >= atol
+        rel = float((err[big] / e.abs()[big]).max()) if bool(big.any()) else 0.0
+        _record(what, a.numel(), float(err.max()), rel, float((err / bound).max()))
+
+
+def pytest_terminal_summary(terminalreporter):
+    """The error margins of every tolerance check that passed: max abs and
+    max rel error against the reference, and the largest share of the
+    tolerance any element used."""
+    # pytest loads this file as `conftest`, the tests import it as
+    # `tests.conftest`: two module objects, each with its own list
+    mods = {id(m): m for m in (sys.modules.get("conftest"), sys.modules.get("tests.conftest"))
+            if m is not None and hasattr(m, "ERRORS")}
+    errors = [e for m in mods.values() for e in m.ERRORS]
+    if not errors:
+        return
+    tr = terminalreporter
+    tr.section("tolerance checks (max abs err, max rel err where |ref| >= atol, share of tolerance used)")
+    for what, n, ma, mr, used in errors:
+        tr.write_line(f"{what[:60]:60s} {n:>10d}  {ma:10.3e}  {mr:10.3e}  {used:6.3f}")
 
 
 GEMM_TILES = (64, 128, 256)
