@@ -50,6 +50,7 @@ for _p in (ROOT, os.path.join(ROOT, "loom-dataflow_amd")):
 PEAK_BF16_TFLOPS = 2516.6   # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+SEED_BASE = 0x5EED0000      # seed of the first synthetic input tensor
 
 
 def parse():
@@ -261,15 +262,22 @@ def quantile(xs, q):
 
 def make_cases(torch, lh):
     cuda = "cuda"
-    bf = torch.bfloat16
-    g = torch.Generator(device=cuda)
-    g.manual_seed(1234)
+    bf, f32 = torch.bfloat16, torch.float32
+    # Every input comes from the measurement protocol's counter-based
+    # generator (loom_hip.synth: splitmix64, Box-Muller, round to nearest
+    # even; bit-identical to the CPU oracle's oracle.synth), one stream per
+    # tensor: seed = SEED_BASE + the tensor's index in creation order.
+    seed = [SEED_BASE]
+
+    def nxt():
+        seed[0] += 1
+        return seed[0]
 
     def randn(*shape, std=1.0, dtype=bf):
-        return (torch.randn(*shape, generator=g, device=cuda) * std).to(dtype)
+        return lh.synth(shape, nxt(), "normal", 0.0, std, dtype)
 
-    def unif(*shape):
-        return (torch.rand(*shape, generator=g, device=cuda) * 2 - 1).to(bf)
+    def unif(*shape, lo=-1.0, hi=1.0, dtype=bf):
+        return lh.synth(shape, nxt(), "uniform", lo, hi, dtype)
 
     def copies(nbytes):
         return max(1, min(4, -(-3 * MALL_BYTES // nbytes)))
@@ -299,15 +307,20 @@ def make_cases(torch, lh):
     def bmm():
         nb = 3 * 16 * 2048 * 2048 * 2
         n = copies(nb)
-        sets = [(randn(16, 2048, 2048, std=0.02), randn(16, 2048, 2048, std=0.02),
-                 torch.empty(16, 2048, 2048, dtype=bf, device=cuda)) for _ in range(n)]
+        sets, seeds = [], []
+        for _ in range(n):
+            sa, sb = nxt(), nxt()
+            seeds.append((sa, sb))
+            sets.append((lh.synth((16, 2048, 2048), sa, "normal", 0.0, 0.02),
+                         lh.synth((16, 2048, 2048), sb, "normal", 0.0, 0.02),
+                         torch.empty(16, 2048, 2048, dtype=bf, device=cuda)))
         def cpu():
             import oracle
             a0, a1 = h16(sets[0][0][:1]), h16(sets[0][1][:1])
             return 1 / 16, "1 of 16 batches", lambda: oracle.batch_matmul(a0, a1, 1, 256, 256, 64)
         return dict(fn=lambda i: lh.batch_matmul(*sets[i % n], tile_m=256, tile_n=256),
                     flop=2 * 16 * 2048 ** 3, bytes=nb, bound="mfma", sets=n,
-                    desc="bmm 16x2048^3 bf16, tile 256x256", cpu=cpu,
+                    desc="bmm 16x2048^3 bf16, tile 256x256", cpu=cpu, seeds=seeds[0],
                     kernel="gemm_persist_kernel<false>")
     cases["bmm"] = bmm
 
@@ -372,11 +385,11 @@ def make_cases(torch, lh):
             x = randn(b, H, L, P)
             C = randn(b, 1, L, N)
             cb = randn(b, nc, 1, Q, Q)
-            dt = torch.nn.functional.softplus(torch.randn(b, H, nc, Q, generator=g, device=cuda))
-            A = -torch.exp(torch.rand(H, generator=g, device=cuda))
+            dt = torch.nn.functional.softplus(randn(b, H, nc, Q, dtype=f32))
+            A = -torch.exp(unif(H, lo=0.0, hi=1.0, dtype=f32))
             dA = torch.cumsum(dt * A[None, :, None, None], dim=-1)
-            Dh = torch.randn(H, generator=g, device=cuda)
-            prev = torch.randn(b, nc, H, N, P, generator=g, device=cuda)
+            Dh = randn(H, dtype=f32)
+            prev = randn(b, nc, H, N, P, dtype=f32)
             out = torch.empty(b, H, L, P, dtype=bf, device=cuda)
             return (cb, x, dt, dA, C, Dh, prev, out)
         first = one()
@@ -404,8 +417,8 @@ def make_cases(torch, lh):
         def one():
             x = randn(b, H, L, P)
             Bm, C = randn(b, 1, L, N), randn(b, 1, L, N)
-            dt = torch.nn.functional.softplus(torch.randn(b, H, L, generator=g, device=cuda))
-            A = -torch.exp(torch.rand(H, generator=g, device=cuda))
+            dt = torch.nn.functional.softplus(randn(b, H, L, dtype=f32))
+            A = -torch.exp(unif(H, lo=0.0, hi=1.0, dtype=f32))
             dA = torch.empty(b, H, nc, Q, dtype=torch.float32, device=cuda)
             cb = torch.empty(b, nc, 1, Q, Q, dtype=bf, device=cuda)
             prev = torch.empty(b, nc, H, N, P, dtype=torch.float32, device=cuda)
@@ -539,15 +552,14 @@ def measure_ceilings(torch, lh):
                    "independent 16x16x32 bf16 MFMA chains, 8 per wave, 2 waves per SIMD"}
 
 
-def cpu_baseline(torch, a0, a1, budget_s=12.0):
+def cpu_baseline(seeds, budget_s=12.0):
     """The fp32 C oracle on whole batches of the same workload until the time
-    budget is spent (at least one batch)."""
-    import numpy as np
-
+    budget is spent (at least one batch).  Its operands are the headline's
+    first input set, made on the host by the oracle's copy of the
+    counter-based generator from the same seeds (bit-identical to the GPU's)."""
     import oracle
-    h0 = a0.view(torch.int16).cpu().numpy().view(np.uint16)
-    h1 = a1.view(torch.int16).cpu().numpy().view(np.uint16)
-    oracle.lib()
+    h0 = oracle.synth((16, 2048, 2048), seeds[0], "normal", 0.0, 0.02)
+    h1 = oracle.synth((16, 2048, 2048), seeds[1], "normal", 0.0, 0.02)
     B, M, K = h0.shape
     N = h1.shape[2]
     done, t0 = 0, time.perf_counter()
@@ -672,7 +684,9 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic (seeded normal(0, 0.02) bf16, resident in HBM)",
+        "data": "synthetic: the counter-based generator (splitmix64, Box-Muller, bf16 RNE), "
+                "one seeded stream per tensor, the same bits on the GPU (loom_hip.synth) and the "
+                "CPU (oracle.synth); normal(0, 0.02) bf16 operands resident in HBM",
         "config": {"workload": "batch_matmul B16 M=N=K=2048 bf16, fp32 accumulate "
                                "(BASELINE configs[1])",
                    "tile_m": 256, "tile_n": 256, "tile_k": 64},
@@ -681,18 +695,12 @@ def main():
                      "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                      "traffic": traffic_for("gemm_persist_kernel<false>")},
     }
-    a0_a1 = None
     if not args.no_cpu:
-        gen = torch.Generator(device="cuda")
-        gen.manual_seed(1234)
-        a0 = (torch.randn(16, 2048, 2048, generator=gen, device="cuda") * 0.02).to(torch.bfloat16)
-        a1 = (torch.randn(16, 2048, 2048, generator=gen, device="cuda") * 0.02).to(torch.bfloat16)
-        a0_a1 = (a0, a1)
-        line["cpu_baseline"] = cpu_baseline(torch, a0, a1)
+        line["cpu_baseline"] = cpu_baseline(head["seeds"])
         print(f"# cpu baseline: {line['cpu_baseline']}", file=sys.stderr, flush=True)
     else:
         line["cpu_baseline"] = None
-    del head, a0_a1
+    del head
     torch.cuda.empty_cache()
 
     if args.kernels != "none":

@@ -458,6 +458,15 @@ int loom_hip_peak_hbm_read(const void* buf, size_t bytes, void* sink, void* stre
 int loom_hip_peak_mfma_bf16(int64_t iters, void* sink, double* flop, void* stream, char* err,
                             size_t errlen);
 
+/* ---- synthetic inputs --------------------------------------------------
+ * No counterpart in the reference: the measurement's seeded inputs.  Writes
+ * n elements (bf16 bits if bf16 != 0, else fp32) of stream `seed` of a
+ * counter-based generator: dist 0 uniform in [a, b), dist 1 normal with
+ * mean a and standard deviation b.  Element i depends on (seed, i) only and
+ * is bit-identical to the CPU oracle's loom_oracle_synth. */
+int loom_hip_synth(void* out, int64_t n, uint64_t seed, int dist, float a, float b, int bf16,
+                   void* stream, char* err, size_t errlen);
+
 #ifdef __cplusplus
 }
 #endif

@@ -123,8 +123,11 @@ _lib.loom_hip_peak_hbm_read.argtypes = [_vp, _sz, _vp, _vp, *_ERR]
 _lib.loom_hip_peak_hbm_read.restype = ctypes.c_int
 _lib.loom_hip_peak_mfma_bf16.argtypes = [_i64, _vp, ctypes.POINTER(ctypes.c_double), _vp, *_ERR]
 _lib.loom_hip_peak_mfma_bf16.restype = ctypes.c_int
+_lib.loom_hip_synth.argtypes = [_vp, _i64, ctypes.c_uint64, ctypes.c_int, _f32, _f32, ctypes.c_int,
+                                _vp, *_ERR]
+_lib.loom_hip_synth.restype = ctypes.c_int
 
-EXPORTED = tuple(_SIGS) + tuple(_CIFACE) + ("loom_hip_peak_hbm_read", "loom_hip_peak_mfma_bf16",) + ("loom_hip_dispatch_memref",
+EXPORTED = tuple(_SIGS) + tuple(_CIFACE) + ("loom_hip_peak_hbm_read", "loom_hip_peak_mfma_bf16", "loom_hip_synth") + ("loom_hip_dispatch_memref",
                                             "loom_hip_dispatch_memref_f16",
                                             "loom_hip_check_memref") + ("loom_hip_split_k_workspace_bytes",
                            "loom_hip_flash_decode_workspace_bytes", "loom_hip_version",
@@ -714,3 +717,20 @@ def peak_mfma_bf16(iters: int, sink: torch.Tensor) -> float:
     _call("loom_hip_peak_mfma_bf16", int(iters), sink.data_ptr(), ctypes.byref(flop),
           _stream(sink))
     return flop.value
+
+
+def synth(shape, seed: int, dist: str = "normal", a: float = 0.0, b: float = 1.0,
+          dtype: torch.dtype = torch.bfloat16, device="cuda") -> torch.Tensor:
+    """A seeded synthetic tensor from ``loom_hip_synth``'s counter-based
+    generator (bit-identical to the CPU oracle's ``oracle.synth``): dist
+    "uniform" draws U[a, b), "normal" N(a, b) (mean a, standard deviation b);
+    bf16 or float32."""
+    if dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError("synth: dtype must be torch.bfloat16 or torch.float32")
+    d = {"uniform": 0, "normal": 1}.get(dist)
+    if d is None:
+        raise ValueError(f"synth: dist must be 'uniform' or 'normal', not {dist!r}")
+    out = torch.empty(shape, dtype=dtype, device=device)
+    _call("loom_hip_synth", out.data_ptr(), out.numel(), int(seed) & ((1 << 64) - 1), d,
+          float(a), float(b), int(dtype == torch.bfloat16), _stream(out))
+    return out

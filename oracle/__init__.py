@@ -51,11 +51,15 @@ def lib():
             "loom_oracle_widen16": [_ptr, _ptr, _i64],
             "loom_oracle_round16": [_ptr, _ptr, _i64],
             "loom_oracle_set_element_type": [ctypes.c_int],
+            "loom_oracle_synth": [_ptr, _i64, ctypes.c_uint64, ctypes.c_int, _f32, _f32,
+                                  ctypes.c_int],
+            "loom_oracle_synth_sqrt": [_ptr, _ptr, _i64],
         }.items():
             fn = getattr(_lib, name)
             fn.argtypes = args
             fn.restype = None if name in ("loom_oracle_widen16", "loom_oracle_round16",
-                                          "loom_oracle_set_element_type") else ctypes.c_int
+                                          "loom_oracle_set_element_type",
+                                          "loom_oracle_synth_sqrt") else ctypes.c_int
         _lib.loom_oracle_num_threads.restype = ctypes.c_int
     return _lib
 
@@ -260,3 +264,24 @@ def mamba_prologue(x, dt, A, B, C, chunk_size):
                                             _p(dA), _p(cb), _p(prev), b, nc, H, G, Q, P, N),
            "mamba_prologue")
     return dt_out, dA, cb, prev
+
+
+def synth(shape, seed, dist="normal", a=0.0, b=1.0, bf16=True):
+    """The measurement protocol's synthetic tensor: element i of stream
+    `seed` from the counter-based generator (oracle.c, loom_oracle_synth).
+    dist "uniform": U[a, b); "normal": N(a, b) (mean a, standard deviation
+    b).  Returns bf16 bits (uint16) or float32, in C order."""
+    n = int(np.prod(shape, dtype=np.int64))
+    out = np.empty(shape, np.uint16 if bf16 else np.float32)
+    d = {"uniform": 0, "normal": 1}[dist]
+    _check(lib().loom_oracle_synth(_p(out), n, int(seed) & ((1 << 64) - 1), d, a, b, int(bf16)),
+           "synth")
+    return out
+
+
+def synth_sqrt(x) -> np.ndarray:
+    """The generator's integer-arithmetic square root (test hook)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty_like(x)
+    lib().loom_oracle_synth_sqrt(_p(x), _p(out), x.size)
+    return out

@@ -650,3 +650,153 @@ EXPORT int loom_oracle_mamba_prologue(const uint16_t *x, const float *dt, const 
     }
   return 0;
 }
+
+/* ------------------------------------------------------------------------ */
+/* Synthetic inputs: the counter-based generator of the measurement          */
+/* protocol (splitmix64 -> uniform, Box-Muller -> normal, round-to-nearest-  */
+/* even -> bf16), so the CPU baseline and the GPU harness can make the same  */
+/* tensors without sharing memory or a framework's random stream.  Not part */
+/* of the reference.  loom-dataflow_amd/csrc/synth.hip computes the same     */
+/* values on the GPU with the same operations in the same order (every       */
+/* multiply-add an explicit fmaf, division correctly rounded, the square    */
+/* root in integer arithmetic), so the two are bit-identical                 */
+/* (tests/test_gpu_synth.py).                                               */
+/*                                                                          */
+/* Element i of stream `seed`: z = mix64(seed * K1 + i * K2) with the        */
+/* splitmix64 finaliser; u = top 24 bits of z * 2^-24 (exact).  Normal:      */
+/* u1 = (top 24 bits + 1) * 2^-24 in (0, 1], u2 = next 24 bits * 2^-24,      */
+/* n = sqrt(-2 ln u1) cos(2 pi u2).  ln: exponent * ln 2 plus the odd        */
+/* series of ln((1+s)/(1-s)) on a mantissa in [sqrt(1/2), sqrt(2)); cos(2 pi  */
+/* u2): u2 splits exactly into an octant and a fraction of pi/4, then        */
+/* Taylor polynomials of sin and cos on [0, pi/4] (errors below 1e-7).       */
+/* ------------------------------------------------------------------------ */
+static inline uint64_t synth_mix(uint64_t z) {
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+static inline uint64_t synth_bits(uint64_t seed, int64_t i) {
+  return synth_mix(seed * 0xD1B54A32D192ED03ull + (uint64_t)i * 0x9E3779B97F4A7C15ull);
+}
+
+/* ln x for x in [2^-24, 1] */
+static inline float synth_ln(float x) {
+  uint32_t b;
+  memcpy(&b, &x, 4);
+  int e = (int)((b >> 23) & 0xff) - 127;
+  b = (b & 0x007fffffu) | 0x3f800000u;   /* mantissa m in [1, 2) */
+  float m;
+  memcpy(&m, &b, 4);
+  if (m > 1.41421356f) {                 /* m in [sqrt(1/2), sqrt(2)) */
+    m = m * 0.5f;
+    e += 1;
+  }
+  const float s = (m - 1.0f) / (m + 1.0f);
+  const float s2 = s * s;
+  float p = fmaf(s2, 0.11111111f, 0.14285715f);   /* 1/9, 1/7 */
+  p = fmaf(s2, p, 0.2f);
+  p = fmaf(s2, p, 0.33333334f);
+  p = fmaf(s2, p, 1.0f);
+  const float lnm = 2.0f * s * p;
+  return fmaf((float)e, 0.69314718f, lnm);
+}
+
+/* sin and cos of a in [0, pi/4] */
+static inline float synth_sin(float a) {
+  const float a2 = a * a;
+  float p = fmaf(a2, -2.5052108e-8f, 2.7557319e-6f);
+  p = fmaf(a2, p, -1.9841270e-4f);
+  p = fmaf(a2, p, 8.3333333e-3f);
+  p = fmaf(a2, p, -1.6666667e-1f);
+  return fmaf(a * a2, p, a);
+}
+static inline float synth_cos(float a) {
+  const float a2 = a * a;
+  float p = fmaf(a2, 2.0876757e-9f, -2.7557319e-7f);
+  p = fmaf(a2, p, 2.4801587e-5f);
+  p = fmaf(a2, p, -1.3888889e-3f);
+  p = fmaf(a2, p, 4.1666667e-2f);
+  p = fmaf(a2, p, -0.5f);
+  return fmaf(a2, p, 1.0f);
+}
+
+/* cos(2 pi t) for t = k * 2^-24, k in [0, 2^24) */
+static inline float synth_cos2pi(float t) {
+  const float t8 = t * 8.0f;             /* exact */
+  const int o = (int)t8;                 /* octant 0..7 */
+  const float f = t8 - (float)o;         /* exact, in [0, 1) */
+  const int k = o >> 1;
+  if ((o & 1) == 0) {                    /* angle k pi/2 + f pi/4 */
+    const float a = f * 0.78539816f;
+    switch (k) {
+      case 0: return synth_cos(a);
+      case 1: return -synth_sin(a);
+      case 2: return -synth_cos(a);
+      default: return synth_sin(a);
+    }
+  }
+  /* angle (k + 1) pi/2 - (1 - f) pi/4 */
+  const float a = (1.0f - f) * 0.78539816f;
+  switch (k) {
+    case 0: return synth_sin(a);
+    case 1: return -synth_cos(a);
+    case 2: return -synth_sin(a);
+    default: return synth_cos(a);
+  }
+}
+
+/* sqrt(x) rounded to nearest, for x = 0 or a positive normal float, in integer
+   arithmetic (the device's square root instruction is not correctly rounded):
+   x = M 2^E with M in [2^24, 2^26) and E even, R = floor(sqrt(M 2^24)) has 25
+   bits (a floating-point estimate corrected by integer steps, so any estimate
+   works), and the 24-bit significand is R / 2 rounded by R's last bit (a square
+   root of a float is never halfway between two floats). */
+static inline float synth_sqrt(float x) {
+  if (!(x > 0.0f)) return 0.0f;
+  uint32_t bx;
+  memcpy(&bx, &x, 4);
+  uint64_t m = (bx & 0x007fffffu) | 0x00800000u;  /* x = m 2^e, m in [2^23, 2^24) */
+  int e = (int)((bx >> 23) & 0xff) - 150;
+  if (e & 1) {
+    m <<= 1;
+    e -= 1;
+  } else {
+    m <<= 2;
+    e -= 2;
+  }
+  const uint64_t n = m << 24;                      /* [2^48, 2^50) */
+  uint64_t r = (uint64_t)sqrt((double)n);
+  while (r * r > n) --r;
+  while ((r + 1) * (r + 1) <= n) ++r;
+  const uint64_t q = (r >> 1) + (r & 1);           /* <= 2^24 */
+  return ldexpf((float)q, (e - 24) / 2 + 1);
+}
+
+/* value of element i: dist 0 uniform in [a, b), dist 1 normal(a, b) */
+static inline float synth_value(uint64_t seed, int64_t i, int dist, float a, float b) {
+  const uint64_t z = synth_bits(seed, i);
+  if (dist == 0) return fmaf(b - a, (float)(z >> 40) * 0x1p-24f, a);
+  const float u1 = (float)((z >> 40) + 1) * 0x1p-24f;
+  const float u2 = (float)((z >> 16) & 0xffffffu) * 0x1p-24f;
+  const float r = synth_sqrt(-2.0f * synth_ln(u1));
+  return fmaf(b, r * synth_cos2pi(u2), a);
+}
+
+/* n values into bf16 bits (bf16 = 1) or fp32 (bf16 = 0); dist as above */
+EXPORT int loom_oracle_synth(void *out, int64_t n, uint64_t seed, int dist, float a, float b,
+                             int bf16) {
+  if (!out || n < 0 || (dist != 0 && dist != 1)) return 1;
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < n; ++i) {
+    const float v = synth_value(seed, i, dist, a, b);
+    if (bf16) ((uint16_t *)out)[i] = f32_to_bf16_bits(v);
+    else ((float *)out)[i] = v;
+  }
+  return 0;
+}
+
+/* the generator's square root on n inputs (checked against IEEE sqrtf) */
+EXPORT void loom_oracle_synth_sqrt(const float *in, float *out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) out[i] = synth_sqrt(in[i]);
+}
