@@ -66,10 +66,8 @@ int loom_hip_peak_hbm_read(const void* buf, size_t bytes, void* sink, void* stre
     return loom_fail(err, errlen, LOOM_EINVAL,
                      "peak_hbm_read: a 16-byte-aligned buffer of at least 16 bytes and a sink "
                      "are needed");
-  int dev = 0, cus = 0;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-    cus = 256;
+  int cus = stream_cus(static_cast<hipStream_t>(stream));   // CUs of the stream's device
+  if (cus <= 0) cus = 256;
   hipLaunchKernelGGL(hbm_read_kernel, dim3((unsigned)cus), dim3(512), 0,
                      static_cast<hipStream_t>(stream), static_cast<const u32x4_t*>(buf),
                      bytes / 16, static_cast<uint32_t*>(sink));
@@ -80,10 +78,8 @@ int loom_hip_peak_mfma_bf16(int64_t iters, void* sink, double* flop, void* strea
                             size_t errlen) {
   if (iters <= 0 || iters > (1 << 30) || !sink)
     return loom_fail(err, errlen, LOOM_EINVAL, "peak_mfma_bf16: 1 <= iters <= 2^30 and a sink");
-  int dev = 0, cus = 0;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-    cus = 256;
+  int cus = stream_cus(static_cast<hipStream_t>(stream));
+  if (cus <= 0) cus = 256;
   // one workgroup of eight waves per CU: two waves per SIMD
   if (flop) *flop = (double)cus * 8 * 8 * 16384.0 * (double)iters;
   hipLaunchKernelGGL(mfma_kernel, dim3((unsigned)cus), dim3(512), 0,
