@@ -439,6 +439,16 @@ int loom_hip_check_variant(const char* variant, const int64_t* dims, int ndims, 
 int loom_hip_constraint_scope(const char* func, const int64_t* dims, int ndims, char* out,
                               size_t outlen, char* err, size_t errlen);
 
+/* The MI355X machine model the constraint scopes are written against, as
+ * JSON: LDS bytes per workgroup (the footprint constraint's capacity), wave
+ * size, SIMDs, MFMA shapes, the workgroup tiles each kernel builds and the
+ * published peaks; with device >= 0 also what that device reports (CU count,
+ * LDS per CU and per workgroup, L2, memory, clock), code 3 if it cannot be
+ * queried.  The counterpart of the reference's --hw_spec machine description
+ * (R/run_pipeline.sh:62,93, a 2-D mesh file in an external grammar) for
+ * this target. */
+int loom_hip_hw_spec(int device, char* out, size_t outlen, char* err, size_t errlen);
+
 /* The binding this library runs fastest for those extents on MI355X (one
  * JSON object {"tile_m": 256, ...} over the function's symbols; a legal
  * point of loom_hip_constraint_scope), usable as a block_sizes_json entry. */

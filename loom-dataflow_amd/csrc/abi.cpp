@@ -983,4 +983,47 @@ int loom_hip_dispatch_f16(const char* variant, void* const* tensors, int ntensor
                              workspace_bytes, stream, err, errlen);
 }
 
+int loom_hip_hw_spec(int device, char* out, size_t outlen, char* err, size_t errlen) {
+  // The machine model the gfx950 constraint scopes are written against
+  // (loom_hip_constraint_scope): the LDS capacity of their footprint
+  // constraint, the workgroup tiles the kernels build, the MFMA shapes the
+  // tiles are multiples of; with device >= 0, also what that device reports.
+  std::string j = "{\"target\":\"gfx950\",\"wave_size\":64,\"simds_per_cu\":4,"
+                  "\"vgprs_per_simd_lane\":512,\"max_workgroup_threads\":1024,"
+                  "\"lds_bytes_per_workgroup\":" + std::to_string(kLdsBytes) + ","
+                  "\"xcds\":8,\"mfma\":[{\"op\":\"v_mfma_f32_16x16x32_bf16\",\"m\":16,\"n\":16,"
+                  "\"k\":32,\"cycles\":16},{\"op\":\"v_mfma_f32_16x16x32_f16\",\"m\":16,\"n\":16,"
+                  "\"k\":32,\"cycles\":16}],"
+                  "\"published\":{\"compute_units\":256,\"clock_mhz\":2400,"
+                  "\"bf16_dense_tflops\":2516.6,\"hbm_gbs\":8000,\"hbm_bytes\":309237645312,"
+                  "\"infinity_cache_bytes\":268435456},"
+                  "\"built_tiles\":{\"matmul\":{\"tile_m\":[64,128,256],\"tile_n\":[64,128,256]},"
+                  "\"batch_matmul\":{\"tile_m\":[64,128,256],\"tile_n\":[64,128,256]},"
+                  "\"split_k_matmul_gather\":{\"tile_m\":[64,128,256],\"tile_n\":[64,128,256]},"
+                  "\"attention\":{\"tile_m\":[64,128,192,256]},"
+                  "\"helion_mamba2_chunk_scan_kernel\":{\"tile_m\":[64,128,192,256],"
+                  "\"tile_n\":[16,32,64]}}";
+  if (device >= 0) {
+    hipDeviceProp_t pr;
+    const hipError_t e = hipGetDeviceProperties(&pr, device);
+    if (e != hipSuccess)
+      return fail(err, errlen, LOOM_HIP_EHIP, "hw_spec: device %d: %s", device,
+                  hipGetErrorString(e));
+    std::string arch(pr.gcnArchName), name(pr.name);
+    for (auto* t : {&arch, &name})
+      for (char& ch : *t)
+        if (ch == '"' || ch == '\\' || (unsigned char)ch < 0x20) ch = ' ';
+    j += ",\"device\":{\"index\":" + std::to_string(device) + ",\"name\":\"" + name +
+         "\",\"arch\":\"" + arch + "\",\"compute_units\":" +
+         std::to_string(pr.multiProcessorCount) + ",\"lds_bytes_per_cu\":" +
+         std::to_string(pr.maxSharedMemoryPerMultiProcessor) + ",\"lds_bytes_per_workgroup\":" +
+         std::to_string(pr.sharedMemPerBlock) + ",\"l2_bytes\":" + std::to_string(pr.l2CacheSize) +
+         ",\"global_bytes\":" + std::to_string(pr.totalGlobalMem) + ",\"clock_mhz\":" +
+         std::to_string(pr.clockRate / 1000) + ",\"warp_size\":" + std::to_string(pr.warpSize) +
+         "}";
+  }
+  j += "}";
+  return copy_out(j, out, outlen, err, errlen, "hw_spec");
+}
+
 }  // extern "C"

@@ -17,6 +17,7 @@ from __future__ import annotations
 
 import ctypes
 import functools
+import json
 import math
 import os
 
@@ -82,7 +83,7 @@ _lib.loom_hip_dispatch_f16.argtypes = _lib.loom_hip_dispatch.argtypes
 _lib.loom_hip_dispatch_f16.restype = ctypes.c_int
 _lib.loom_hip_check_variant.argtypes = [ctypes.c_char_p, ctypes.POINTER(_i64), ctypes.c_int, *_ERR]
 _lib.loom_hip_check_variant.restype = ctypes.c_int
-for _fn in ("loom_hip_constraint_scope", "loom_hip_preferred_block_sizes"):
+for _fn in ("loom_hip_constraint_scope", "loom_hip_preferred_block_sizes", "loom_hip_hw_spec"):
     getattr(_lib, _fn).argtypes = [ctypes.c_char_p, ctypes.POINTER(_i64), ctypes.c_int,
                                    ctypes.c_char_p, _sz, *_ERR]
     getattr(_lib, _fn).restype = ctypes.c_int
@@ -126,6 +127,8 @@ _lib.loom_hip_peak_mfma_bf16.restype = ctypes.c_int
 _lib.loom_hip_synth.argtypes = [_vp, _i64, ctypes.c_uint64, ctypes.c_int, _f32, _f32, ctypes.c_int,
                                 _vp, *_ERR]
 _lib.loom_hip_synth.restype = ctypes.c_int
+_lib.loom_hip_hw_spec.argtypes = [ctypes.c_int, ctypes.c_char_p, _sz, *_ERR]
+_lib.loom_hip_hw_spec.restype = ctypes.c_int
 
 EXPORTED = tuple(_SIGS) + tuple(_CIFACE) + ("loom_hip_peak_hbm_read", "loom_hip_peak_mfma_bf16", "loom_hip_synth") + ("loom_hip_dispatch_memref",
                                             "loom_hip_dispatch_memref_f16",
@@ -133,7 +136,7 @@ EXPORTED = tuple(_SIGS) + tuple(_CIFACE) + ("loom_hip_peak_hbm_read", "loom_hip_
                            "loom_hip_flash_decode_workspace_bytes", "loom_hip_version",
                            "loom_hip_materialize_variants", "loom_hip_parse_variant",
                            "loom_hip_dispatch", "loom_hip_dispatch_f16", "loom_hip_check_variant",
-                           "loom_hip_constraint_scope", "loom_hip_preferred_block_sizes")
+                           "loom_hip_constraint_scope", "loom_hip_preferred_block_sizes", "loom_hip_hw_spec")
 
 #: block-size symbols in the slot order of loom_hip_parse_variant's tiles[]
 TILE_SYMBOLS = ("tile_b", "tile_m", "tile_n", "tile_k", "tile_s", "tile_h", "tile_c")
@@ -590,7 +593,6 @@ def check_variant(variant: str, dims) -> None:
 
 
 def _json_call(name, func, dims):
-    import json
     darr = (_i64 * max(len(dims), 1))(*dims)
     out = ctypes.create_string_buffer(1 << 16)
     err = ctypes.create_string_buffer(512)
@@ -734,3 +736,12 @@ def synth(shape, seed: int, dist: str = "normal", a: float = 0.0, b: float = 1.0
     _call("loom_hip_synth", out.data_ptr(), out.numel(), int(seed) & ((1 << 64) - 1), d,
           float(a), float(b), int(dtype == torch.bfloat16), _stream(out))
     return out
+
+
+def hw_spec(device: int = -1) -> dict:
+    """The MI355X machine model behind the constraint scopes
+    (``loom_hip_hw_spec``); with ``device`` >= 0 also that device's
+    reported properties."""
+    buf = ctypes.create_string_buffer(1 << 14)
+    _call("loom_hip_hw_spec", int(device), buf, len(buf))
+    return json.loads(buf.value.decode())

@@ -171,3 +171,38 @@ def test_every_symbol_bounded_by_natural_ub(func):
             with pytest.raises(RuntimeError) as ei:
                 loom_hip.check_variant(_variant(func, over), dims)
             assert ei.value.code == 1, (func, s, str(ei.value))
+
+
+def test_hw_spec_is_the_scopes_machine_model():
+    """loom_hip_hw_spec without a device: the LDS capacity is the one every
+    footprint constraint uses, and on large extents the values each tiled
+    symbol takes in some legal binding are exactly the built tiles hw_spec
+    lists for that function."""
+    spec = loom_hip.hw_spec()
+    assert spec["target"] == "gfx950" and spec["wave_size"] == 64 and "device" not in spec
+    big = {"matmul": (4096, 4096, 4096), "batch_matmul": (2, 4096, 4096, 4096),
+           "split_k_matmul_gather": (4096, 4096, 16384), "attention": (128, 4096, 4096, 128),
+           "helion_mamba2_chunk_scan_kernel": (4, 16, 32, 1, 256, 64, 128)}
+    cand = sorted(set(GRID + [16, 32, 64, 128, 192, 256, 320, 512]))
+    for func, dims in big.items():
+        scope = loom_hip.constraint_scope(func, dims)["constraint_scope"]
+        assert scope["metadata"]["capacity_bytes"] == spec["lds_bytes_per_workgroup"]
+        syms = sorted(scope["metadata"]["symbols"])
+        values = {s: (SMALL if s in ("tile_b", "tile_h", "tile_c") else cand) for s in syms}
+        seen = {s: set() for s in syms}
+        for combo in itertools.product(*(values[s] for s in syms)):
+            env = dict(zip(syms, combo))
+            if all(evaluate(c, env) for c in scope["hard_constraints"]):
+                for s in syms:
+                    seen[s].add(env[s])
+        for sym, built in spec["built_tiles"][func].items():
+            assert sorted(seen[sym]) == built, (func, sym, sorted(seen[sym]), built)
+
+
+def test_hw_spec_without_a_device_is_refused_cleanly():
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    with pytest.raises(RuntimeError) as ei:
+        loom_hip.hw_spec(0)
+    assert ei.value.code == 3 and "hw_spec" in str(ei.value)
