@@ -147,6 +147,8 @@ constexpr int kSsdMaxLpw = 5;                // DMA copies per wave per unit at 
 // is not a multiple of 32 is one unit zero-weighted up to QSP rows).  Unit u
 // lives in LDS stage u % NS: x rows [QSP][P] | B rows [QSP][nb] | dA, dt
 // (QSP floats each, 1 KB) | dA[c, Q-4 .. Q-1] of the unit's chunk (1 KB slot).
+// The WIDE form (P = 64, nb = 64, Q a multiple of 256) takes 256-key units
+// in two 67 KB stages: x 32 KB | B 32 KB | dA 1 KB | dt 1 KB | dA tail 1 KB.
 struct SsdStateParams {
   const uint16_t* x;
   const float* dt;
@@ -157,7 +159,7 @@ struct SsdStateParams {
   int QS, QSP, upc;          // keys per unit, LDS rows per unit, units per chunk
   int xbytes, bbytes;        // per stage
   int ninstr, lpw;           // DMA copies per unit; the most any wave issues
-  int ns;                    // stages in the ring (3 .. 8)
+  int ns;                    // stages in the ring (3 .. 8; 2 in the WIDE form)
 };
 
 // MODE 0: tile t of wave w is w + 8 t, each with its own p tile.
@@ -170,10 +172,14 @@ struct SsdStateParams {
 //         sums to the even wave through LDS, which stores prev(c).  The
 //         host picks MODE 2 only for P = 64 (four p tiles) with nb = 16 TPW,
 //         so both are compile-time constants there.
-template <int TPW, int MODE, bool F16>
+// WIDE (MODE 2, TPW 4, QS = 256): the unit layout and every wave's DMA
+//         slots are compile-time constants; one wait, barrier, w_c build and
+//         prev hand-over per 256 keys instead of two.
+template <int TPW, int MODE, bool F16, bool WIDE = false>
 __global__ void __launch_bounds__(64 * kSsdWaves) ssd_state_kernel(SsdStateParams p) {
+  static_assert(!WIDE || (MODE == 2 && TPW == 4), "256-key units: P = 64, nb = 64 only");
   __shared__ __attribute__((aligned(1024))) char smem[kSsdRing];
-  __shared__ __attribute__((aligned(16))) float s_w[kSsdWaves][128];
+  __shared__ __attribute__((aligned(16))) float s_w[kSsdWaves][WIDE ? 256 : 128];
   __shared__ f32x4_t s_x[MODE == 2 ? (kSsdWaves / 2) * TPW * 64 : 1];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -185,17 +191,21 @@ __global__ void __launch_bounds__(64 * kSsdWaves) ssd_state_kernel(SsdStateParam
   const int n0 = nblk * nb;
   const int L = nc * Q;
   const int XR = P * 2, BR = nb * 2;
-  const int stage_bytes = p.xbytes + p.bbytes + 2048;
-  const int xinstr = p.xbytes / 1024, binstr = p.bbytes / 1024;
+  const int QS = WIDE ? 256 : p.QS, QSP = WIDE ? 256 : p.QSP, upc = p.upc, nu = nc * upc;
+  const int xbytes = WIDE ? QSP * P * 2 : p.xbytes, bbytes = WIDE ? QSP * nb * 2 : p.bbytes;
+  const int stage_bytes = xbytes + bbytes + (WIDE ? 3072 : 2048);
+  const int xinstr = xbytes / 1024, binstr = bbytes / 1024;
   const int ptiles = P / 16, tiles = ptiles * (nb / 16);
-  const int QS = p.QS, QSP = p.QSP, upc = p.upc, nu = nc * upc;
+  // side region of a stage: dA of the unit's keys from float 0, dt from
+  // float DTO, dA[c, Q-4 .. Q-1] from float 2 DTO
+  constexpr int DTO = WIDE ? 256 : 128;
 
   const uint16_t* xg = p.x + (int64_t)bh * L * P;
   const uint16_t* bgp = p.B + (int64_t)(b * p.G + g) * L * N + n0;
   const float* dAg = p.dA + (int64_t)bh * nc * Q;
   const float* dtg = p.dt + (int64_t)bh * nc * Q;
   lds_char_t* const sm = (lds_char_t*)smem;
-  const int NS = p.ns;
+  const int NS = WIDE ? 2 : p.ns;
 
   // ---- DMA of unit u into stage s; rows past the unit's keys are clamped
   // (their weight is forced to zero).  Copy j of the unit belongs to wave
@@ -203,10 +213,12 @@ __global__ void __launch_bounds__(64 * kSsdWaves) ssd_state_kernel(SsdStateParam
   // its slots i = 0 .. nlw-1 (j = w + 8 i).  A slot's source offset within
   // the unit and its LDS offset within the stage are the same for every
   // unit: computed once here.
-  const int nlw = (p.ninstr - wave + kSsdWaves - 1) / kSsdWaves;
-  int goff[kSsdMaxLpw], loff[kSsdMaxLpw], kind[kSsdMaxLpw];  // kind: 0 x, 1 B, 2 dA|dt, 3 dA tail
+  const int ninstr = WIDE ? xinstr + binstr + 3 : p.ninstr;
+  const int nlw = (ninstr - wave + kSsdWaves - 1) / kSsdWaves;
+  constexpr int LPW = WIDE ? 8 : kSsdMaxLpw;
+  int goff[LPW], loff[LPW], kind[LPW];  // kind: 0 x, 1 B, 2 dA|dt, 3 dA tail
 #pragma unroll
-  for (int i = 0; i < kSsdMaxLpw; ++i) {
+  for (int i = 0; i < LPW; ++i) {
     const int j = wave + kSsdWaves * i;
     if (j < xinstr) {
       // LDS slot (row, chunk) of the [QSP][P] unit holds global chunk
@@ -220,11 +232,11 @@ __global__ void __launch_bounds__(64 * kSsdWaves) ssd_state_kernel(SsdStateParam
       const int idx = (j - xinstr) * 64 + lane;
       const int row = idx / (nb / 8), cc = idx % (nb / 8);
       goff[i] = min(row, QS - 1) * N + (cc ^ tr_swz(row, BR)) * 8;
-      loff[i] = p.xbytes + (j - xinstr) * 1024;
+      loff[i] = xbytes + (j - xinstr) * 1024;
       kind[i] = 1;
     } else {
       goff[i] = min(4 * (lane & 31), QS - 4);
-      loff[i] = p.xbytes + p.bbytes + (j == xinstr + binstr ? 0 : 1024);
+      loff[i] = xbytes + bbytes + (j == xinstr + binstr ? 0 : 1024);
       kind[i] = j == xinstr + binstr ? 2 : 3;
     }
   }
@@ -234,7 +246,7 @@ __global__ void __launch_bounds__(64 * kSsdWaves) ssd_state_kernel(SsdStateParam
     const int64_t key0 = (int64_t)c * Q + ko;   // first key of the unit within (b, h)
     const uint32_t base = lds_addr(sm + s * stage_bytes);
 #pragma unroll
-    for (int i = 0; i < kSsdMaxLpw; ++i) {
+    for (int i = 0; i < LPW; ++i) {
       if (i < i0 || i >= i1) continue;
       const uint32_t la = base + loff[i];
       if (kind[i] == 0) dma_load16(xg + key0 * P + goff[i], la);
@@ -243,8 +255,33 @@ __global__ void __launch_bounds__(64 * kSsdWaves) ssd_state_kernel(SsdStateParam
       else dma_load16(dAg + (int64_t)c * Q + Q - 4, la);
     }
   };
+  // 256-key units (P = 64, nb = 64): 32 x copies, 32 B copies and 3 side
+  // copies (dA, dt, dA tail), copy j of each kind on wave j % 8, so every
+  // wave's slots are compile-time: x slots 0..3 (part 0), B slots 4..7 and
+  // waves 0..2 one side copy (part 1).  Source: the unit's base in SGPRs
+  // plus the lane's 32-bit byte offset (kept from the setup above: goff is
+  // an element offset there).
+  auto issue_wide = [&](int s, int u, int part) {
+    const int c = u / upc;
+    const int64_t key0 = (int64_t)c * Q + (u % upc) * 256;
+    const uint32_t base = lds_addr(sm + s * stage_bytes);
+    if (part == 0) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        dma_load16_s(2u * goff[i], xg + key0 * P, base + (wave + kSsdWaves * i) * 1024);
+    } else {
+#pragma unroll
+      for (int i = 4; i < 8; ++i)
+        dma_load16_s(2u * goff[i], bgp + key0 * N, base + xbytes + (wave + kSsdWaves * (i - 4)) * 1024);
+      const uint32_t la = base + xbytes + bbytes + wave * 1024;
+      if (wave == 2) dma_load16_s(0u, dAg + (int64_t)c * Q + Q - 4, la);
+      else if (wave < 2) dma_load16_s(16u * lane, (wave ? dtg : dAg) + key0, la);
+    }
+  };
   auto wait_units = [&](int younger, int stores) {
-    const int n = younger * nlw + stores;
+    // two stages: the awaited unit's copies are this wave's youngest
+    // (issued after its prev stores), so the wait takes everything
+    const int n = WIDE ? 0 : younger * nlw + stores;
     switch (n) {
       case 0: LOOM_WAIT_VMCNT(0); break;
       case 1: LOOM_WAIT_VMCNT(1); break;
@@ -299,8 +336,15 @@ __global__ void __launch_bounds__(64 * kSsdWaves) ssd_state_kernel(SsdStateParam
   float* const sw = s_w[wave];
   const float kLog2e = 1.4426950408889634f;
   auto make_w = [&](const float* dAs) {
-    const float last = dAs[256 + 3];
-    if constexpr (MODE == 2) {
+    const float last = dAs[2 * DTO + 3];
+    if constexpr (WIDE) {
+      // 256 keys, every one inside the unit: steps kq + 2 m, m = 0..3, lanes
+      // 0-31 taking m = 0 and 2, lanes 32-63 m = 1 and 3
+      const int i0 = 32 * (kq + 2 * (lane >> 5)) + (lane & 31), i1 = i0 + 128;
+      const float a0 = dAs[i0], t0 = dAs[DTO + i0], a1 = dAs[i1], t1 = dAs[DTO + i1];
+      sw[i0] = fast_exp2((last - a0) * kLog2e) * t0;
+      sw[i1] = fast_exp2((last - a1) * kLog2e) * t1;
+    } else if constexpr (MODE == 2) {
       const int s = kq + 2 * (lane >> 5), i = 32 * s + (lane & 31);
       const float a = dAs[i], t = dAs[128 + i];
       if (32 * s < QSP) sw[i] = i < QS ? fast_exp2((last - a) * kLog2e) * t : 0.f;
@@ -371,8 +415,8 @@ __global__ void __launch_bounds__(64 * kSsdWaves) ssd_state_kernel(SsdStateParam
   auto compute = [&](int s, int u) {
     const int c = u / upc, part = u % upc;
     const lds_char_t* xs = sm + s * stage_bytes;
-    const lds_char_t* bs = xs + p.xbytes;
-    const float* dAs = reinterpret_cast<const float*>(smem + s * stage_bytes + p.xbytes + p.bbytes);
+    const lds_char_t* bs = xs + xbytes;
+    const float* dAs = reinterpret_cast<const float*>(smem + s * stage_bytes + xbytes + bbytes);
     // the DMA of unit u+NS-1 (into the stage unit u-1 used) is issued in two
     // halves between this unit's steps, so the address units work through
     // it while the waves compute
@@ -381,7 +425,7 @@ __global__ void __launch_bounds__(64 * kSsdWaves) ssd_state_kernel(SsdStateParam
     make_w(dAs);
     if (part == 0) {
       // prev(c) out, then R = exp(dA[c, Q-1]) R; states(c) accumulate below
-      const float decay = fast_exp2(dAs[256 + 3] * kLog2e);
+      const float decay = fast_exp2(dAs[2 * DTO + 3] * kLog2e);
       float* outc = p.prevT + (((int64_t)(b * nc + c) * H + h) * N + n0) * P;
       if constexpr (MODE == 2) {
         const int pt = wave % ptiles;
@@ -438,15 +482,22 @@ __global__ void __launch_bounds__(64 * kSsdWaves) ssd_state_kernel(SsdStateParam
         for (int ks = kq; ks < nks; ks += 2 * KSTEP) {
           if (ks + KSTEP < nks) load_ops(xs, bs, ks + KSTEP, ob);
           step(oa);
-          if (ks == kq && pre) issue(sn, un, 0, half);
+          if (ks == kq && pre) {
+            if constexpr (WIDE) issue_wide(sn, un, 0);
+            else issue(sn, un, 0, half);
+          }
           if (ks + KSTEP >= nks) break;
           if (ks + 2 * KSTEP < nks) load_ops(xs, bs, ks + 2 * KSTEP, oa);
           step(ob);
         }
       } else if (pre) {
-        issue(sn, un, 0, half);
+        if constexpr (WIDE) issue_wide(sn, un, 0);
+        else issue(sn, un, 0, half);
       }
-      if (pre) issue(sn, un, half, nlw);
+      if (pre) {
+        if constexpr (WIDE) issue_wide(sn, un, 1);
+        else issue(sn, un, half, nlw);
+      }
     } else {
       if (pre) issue(sn, un, 0, nlw);
       for (int ks = 0; ks < nks; ++ks) {
@@ -478,7 +529,14 @@ __global__ void __launch_bounds__(64 * kSsdWaves) ssd_state_kernel(SsdStateParam
   // u-1, whose reads every wave finished before that barrier.  prev stores
   // issued by compute(u) are younger than unit u+NS-2's DMA, so the next
   // wait (for unit u+1) leaves them outstanding too.
-  for (int u = 0; u < NS - 1 && u < nu; ++u) issue(u, u, 0, nlw);
+  for (int u = 0; u < NS - 1 && u < nu; ++u) {
+    if constexpr (WIDE) {
+      issue_wide(u, u, 0);
+      issue_wide(u, u, 1);
+    } else {
+      issue(u, u, 0, nlw);
+    }
+  }
   int stores = 0;
   for (int u = 0; u < nu; ++u) {
     wait_units(max(0, min(NS - 2, nu - 1 - u)), stores);
@@ -492,6 +550,12 @@ __global__ void __launch_bounds__(64 * kSsdWaves) ssd_state_kernel(SsdStateParam
 template <int TPW, bool F16>
 void launch_state(const SsdStateParams& p, int mode, int grid_x, int grid_y, hipStream_t st) {
   const dim3 grid((unsigned)grid_x, (unsigned)grid_y), block(64 * kSsdWaves);
+  if constexpr (TPW == 4) {
+    if (mode == 2 && p.QS == 256) {
+      hipLaunchKernelGGL((ssd_state_kernel<4, 2, F16, true>), grid, block, 0, st, p);
+      return;
+    }
+  }
   if (mode == 2)
     hipLaunchKernelGGL((ssd_state_kernel<TPW, 2, F16>), grid, block, 0, st, p);
   else if (mode == 1)
@@ -604,7 +668,8 @@ int state_passing_impl(const void* x, const void* dt, const void* dA_cumsum,
   p.prevT = static_cast<float*>(prev_states_T);
   p.H = (int)nheads; p.G = (int)ngroups; p.nc = (int)nchunks; p.Q = (int)chunk_size;
   p.P = (int)headdim; p.N = (int)dstate; p.nb = nb;
-  // unit: the largest of 128, 64 and 32 keys dividing Q whose stage fits
+  // unit (when the WIDE form does not apply): the largest of 128, 64 and 32
+  // keys dividing Q whose stage fits
   // (each unit costs a barrier and a wait, and the copies in flight per
   // workgroup, not the ring depth, bound the stream: 128-key units measured
   // faster than 64-key units with twice the stages); a Q that is not a
@@ -626,7 +691,22 @@ int state_passing_impl(const void* x, const void* dt, const void* dA_cumsum,
     return (q.ns - 1) * (q.xbytes + q.bbytes);
   };
   int best = -1;
+  // P = 64 with a 64-wide n block and Q a multiple of 256: 256-key units in
+  // two 67 KB stages (the kernel's WIDE form, its layout fixed at compile
+  // time); one barrier, wait and hand-over per 256 keys instead of two
+  if (mode == 2 && tpw == 4 && p.Q % 256 == 0) {
+    p.QS = p.QSP = 256;
+    p.upc = p.Q / 256;
+    p.xbytes = 256 * 64 * 2;
+    p.bbytes = 256 * 64 * 2;
+    p.ninstr = p.xbytes / 1024 + p.bbytes / 1024 + 3;
+    p.lpw = (p.ninstr + kSsdWaves - 1) / kSsdWaves;
+    p.ns = 2;
+    static_assert(2 * (256 * 64 * 2 * 2 + 3072) <= kSsdRing, "two 256-key stages fit the ring");
+    best = 0;
+  }
   for (int qs : {128, 64, 32}) {
+    if (best >= 0) break;
     if (p.Q % qs) continue;
     SsdStateParams q = p;
     if ((best = plan(qs, q)) >= 0) { p = q; break; }

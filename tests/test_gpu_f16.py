@@ -127,6 +127,21 @@ def _ssd_inputs(rng, b, H, G, L, P, N):
     return x, dt, A, Bm, C
 
 
+def test_ssd_prologue_f16_wide_units(lh):
+    """P = 64, N = 128, Q = 256 in f16: the state kernel's 256-key form."""
+    rng = np.random.default_rng(57)
+    b, H, G, Q, nc, P, N = 1, 4, 1, 256, 3, 64, 128
+    x, dt, A, Bm, C = _ssd_inputs(rng, b, H, G, nc * Q, P, N)
+    _, dA, cb, prev = lh.ssd_prologue(dev(x), devf(dt), devf(A), dev(Bm), dev(C), Q)
+    assert cb.dtype == torch.float16
+    _, dA_o, cb_o, prev_o = oracle.mamba_prologue(x, dt, A, Bm, C, Q)
+    cbg, cbr = from_f16(host(cb)), from_f16(cb_o)
+    assert np.all(np.abs(cbg - cbr) <= 2.0 ** -10 * np.abs(cbr) + 1e-5), "cb f16"
+    pg = prev.cpu().numpy()
+    scale = 1e-2 * float(np.abs(prev_o).max())
+    assert np.all(np.abs(pg - prev_o) <= 1e-3 * (np.abs(prev_o) + scale)), "prev_states f16"
+
+
 def test_ssd_prologue_and_chunk_scan_f16(lh):
     """The whole Mamba-2 chain in f16 (the reference example's geometry)."""
     rng = np.random.default_rng(56)

@@ -110,6 +110,16 @@ def test_paired_k_split_shapes(lh, Q, N):
     _check_prologue(lh, x, dt, A, Bm, C, Q, f"paired Q{Q} N{N}")
 
 
+@pytest.mark.parametrize("b,H,G,nc,N", [(2, 4, 2, 1, 64), (1, 6, 3, 3, 128)])
+def test_wide_unit_shapes(lh, b, H, G, nc, N):
+    """P = 64, Q = 256: the state kernel's 256-key form (two stages, one unit
+    per chunk).  A single chunk (the pipeline's one-unit case), several
+    groups, one and two n blocks."""
+    rng = np.random.default_rng(90 + nc)
+    x, dt, A, Bm, C = _raw_inputs(rng, b, H, G, nc * 256, 64, N)
+    _check_prologue(lh, x, dt, A, Bm, C, 256, f"wide b{b} H{H} G{G} nc{nc} N{N}")
+
+
 def test_zero_B_gives_zero_states(lh):
     rng = np.random.default_rng(44)
     x, dt, A, Bm, C = _raw_inputs(rng, 1, 2, 1, 4 * 64, 32, 64)
