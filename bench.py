@@ -443,7 +443,7 @@ def make_cases(torch, lh):
             return 1 / b, "batch 1 of 4", lambda: oracle.mamba_prologue(*a, Q)
         return dict(fn=fn, out=out, flop=flop, bytes=nb, bound="hbm", sets=n,
                     desc="mamba SSD prologue (cumsum, cb, states + passing) b4 L4096 h32 P64 "
-                         "N128 g1 Q256", cpu=cpu, kernel="ssd_state_kernel<4, 2, false>")
+                         "N128 g1 Q256", cpu=cpu, kernel="ssd_state_kernel<4, 2, false, true>")
     cases["mamba_prologue"] = ssd
     return cases
 

@@ -56,6 +56,7 @@ struct MambaParams {
   uint16_t* out;
   int Bb, nc, H, G, Q, P, N;
   int tile_m, tile_n, nmt, npt;
+  int cus;             // CUs of the launch's device (0: unknown)
 };
 
 // Element i of a side tensor (dt, dA_cumsum, D, prev_states_T) as fp32: fp32
@@ -89,6 +90,15 @@ __global__ void __launch_bounds__(64 * kWaves, kWaves == 8 ? 4 : 1)
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int rr = lane & 15, g4 = lane >> 4;
+  // Two 8-wave workgroups share a CU, and the dispatcher gives blocks
+  // 0 .. cus-1 every CU's first slot and cus .. 2 cus-1 the second.  The
+  // second starts ~1 us (2048 clocks) later, so the pair's staging bursts
+  // (every load of x and prev_states at once) do not coincide, in the first
+  // round or -- each finishing workgroup being replaced -- in later ones
+  // (BASELINE shape 82.7 -> 80.0 us; a 4x longer delay gains the same).
+  if constexpr (kWaves == 8) {
+    if ((int)blockIdx.x >= p.cus && (int)blockIdx.x < 2 * p.cus) __builtin_amdgcn_s_sleep(32);
+  }
   const int Q = p.Q, P = p.P, N = p.N, H = p.H;
   const int L = p.nc * Q;
 
@@ -451,6 +461,7 @@ int chunk_scan_impl(
   p.npt = (int)npt;
   if (loom_validate_only()) return loom_ok(err, errlen);
   hipStream_t st = static_cast<hipStream_t>(stream);
+  p.cus = stream_cus(st);
   if (tile_n == 64) launch_mamba<4, F16>(p, st);
   else if (tile_n == 32) launch_mamba<2, F16>(p, st);
   else launch_mamba<1, F16>(p, st);
