@@ -48,9 +48,10 @@ struct DecodeParams {
 // Split-0 combine of the reference (:147-199): M = max_s lse_s,
 // w_s = exp(lse_s - M) / sum_s exp(lse_s - M), out = sum_s w_s o_s (ascending
 // s).  One thread per two consecutive d of one (b, head): every split's lse
-// and o loads are independent and issued together (in chunks of 16 splits),
-// so the combine costs about one memory round trip.
-template <int D, bool F16>
+// and o loads are independent and issued together (in chunks of CH splits:
+// 8 when there are at most 8, else 16), so the combine costs about one
+// memory round trip.
+template <int D, bool F16, int CH>
 __global__ void __launch_bounds__(256) decode_combine_kernel(DecodeParams p) {
   constexpr int TPR = D / 2;   // threads per (b, head) row
   const int64_t BH = (int64_t)p.B * p.H;
@@ -59,7 +60,6 @@ __global__ void __launch_bounds__(256) decode_combine_kernel(DecodeParams p) {
   if (bh >= BH) return;
   const int d = (int)(t % TPR) * 2;
   const int ns = p.ns;
-  constexpr int CH = 16;
   // every load of a chunk of CH splits is issued before any is used; across
   // chunks the running max moves and the sums rescale (one chunk at BASELINE
   // shapes, so one memory round trip)
@@ -682,10 +682,13 @@ int flash_decode_impl(const void* k, const void* v, const void* q, void* out,
   int rc = loom_check_launch(err, errlen, "flash_decode (split)");
   if (rc) return rc;
   const dim3 cgrid((unsigned)cdiv64(B * H * D / 2, 256)), cblock(256);
-  if (D == 128)
-    hipLaunchKernelGGL((decode_combine_kernel<128, F16>), cgrid, cblock, 0, st, p);
-  else
-    hipLaunchKernelGGL((decode_combine_kernel<64, F16>), cgrid, cblock, 0, st, p);
+  if (D == 128) {
+    if (p.ns <= 8) hipLaunchKernelGGL((decode_combine_kernel<128, F16, 8>), cgrid, cblock, 0, st, p);
+    else hipLaunchKernelGGL((decode_combine_kernel<128, F16, 16>), cgrid, cblock, 0, st, p);
+  } else {
+    if (p.ns <= 8) hipLaunchKernelGGL((decode_combine_kernel<64, F16, 8>), cgrid, cblock, 0, st, p);
+    else hipLaunchKernelGGL((decode_combine_kernel<64, F16, 16>), cgrid, cblock, 0, st, p);
+  }
   return loom_check_launch(err, errlen, "flash_decode (combine)");
 }
 
