@@ -90,7 +90,7 @@ def test_split_k_random(lh, M, N, K, tk):
     if res is None:
         return
     out, parts = res
-    o_ref, p_ref = oracle.split_k_matmul_gather(a, b, 16, 16, tk)
+    o_ref, p_ref = oracle.split_k_matmul_gather(a, b, min(16, M), min(16, N), tk)
     assert np.array_equal(parts.cpu().numpy(), p_ref), (M, N, K, tk, "partials")
     assert np.array_equal(host(out), o_ref), (M, N, K, tk, "out")
 
@@ -169,3 +169,114 @@ def test_mamba_prologue_and_scan_random(lh, case):
         return
     ref = oracle.mamba_chunk_scan(cb_o, x, dt_o, dA_o, C, Dh, prev_o, 64, 64, 64)
     assert_close(from_bf16(host(out)), from_bf16(ref), **ATTN_TOL, what=f"chunk scan {case} tile_m {tm}")
+
+
+# ------------------------------------------------------------- f16 variants
+# The same draws for the *_f16 entry points (every 16-bit tensor IEEE
+# binary16; the chunk scan's dt, dA_cumsum, D and prev_states_T f16 too, the
+# reference's own signature), against the oracle in f16 mode.
+
+def _dev16(h):
+    return torch.from_numpy(np.ascontiguousarray(h).view(np.int16)).view(torch.float16).cuda()
+
+
+def _host16(t):
+    assert t.dtype == torch.float16
+    return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def _ints16(rng, shape, lo=-4, hi=4):
+    return oracle.to_f16(rng.integers(lo, hi + 1, shape).astype(np.float32))
+
+
+def _rnd16(rng, shape):
+    return oracle.to_f16(rng.standard_normal(shape).astype(np.float32))
+
+
+@pytest.mark.parametrize("M,N,K", [tuple(int(v) for v in SHAPES.integers(1, 300, 3))
+                                   for _ in range(3)])
+def test_matmul_f16_random(lh, M, N, K):
+    rng = np.random.default_rng(M * 7 + N * 13 + K)
+    x, y = _ints16(rng, (M, K)), _ints16(rng, (K, N))
+    with oracle.element_type("f16"):
+        ref = oracle.matmul(x, y)
+    assert np.array_equal(_host16(lh.matmul(_dev16(x), _dev16(y))), ref), (M, N, K)
+
+
+@pytest.mark.parametrize("M,N,K,tk", [tuple(int(v) for v in (*SHAPES.integers(1, 200, 2), k,
+                                                               SHAPES.integers(8, k + 1)))
+                                      for k in SHAPES.integers(8, 2000, 3)])
+def test_split_k_f16_random(lh, M, N, K, tk):
+    rng = np.random.default_rng(M * 3 + N * 5 + K + tk)
+    a, b = _ints16(rng, (M, K)), _ints16(rng, (K, N))
+    res = _call_or_unsupported(lambda: lh.split_k_matmul_gather(_dev16(a), _dev16(b), tile_k=tk),
+                               f"split-K f16 {M}x{N}x{K} tile_k {tk}")
+    if res is None:
+        return
+    out, parts = res
+    with oracle.element_type("f16"):
+        o_ref, p_ref = oracle.split_k_matmul_gather(a, b, min(16, M), min(16, N), tk)
+    assert np.array_equal(parts.cpu().numpy(), p_ref), (M, N, K, tk, "partials")
+    assert np.array_equal(_host16(out), o_ref), (M, N, K, tk, "out")
+
+
+@pytest.mark.parametrize("BH,S,D,causal", [(int(SHAPES.integers(1, 4)), int(s),
+                                            int(SHAPES.choice([64, 128])), bool(c))
+                                           for s, c in zip(SHAPES.integers(1, 600, 3), [1, 0, 1])])
+def test_attention_f16_random(lh, BH, S, D, causal):
+    rng = np.random.default_rng(BH * 11 + S + D)
+    k, v, q = _rnd16(rng, (BH, D, S)), _rnd16(rng, (BH, S, D)), _rnd16(rng, (BH, S, D))
+    got = _call_or_unsupported(lambda: lh.attention(_dev16(k), _dev16(v), _dev16(q), causal=causal),
+                               f"attention f16 BH{BH} S{S} D{D}")
+    if got is None:
+        return
+    with oracle.element_type("f16"):
+        ref = oracle.from_f16(oracle.attention(k, v, q, 1 / math.sqrt(D), causal, 1, 64, 64))
+    assert_close(oracle.from_f16(_host16(got)), ref, **ATTN_TOL,
+                 what=f"attention f16 BH{BH} S{S} D{D} causal={causal}")
+
+
+@pytest.mark.parametrize("B,H,D,S", [(int(SHAPES.integers(1, 5)), int(SHAPES.integers(1, 33)),
+                                      int(SHAPES.choice([64, 128])), int(s))
+                                     for s in SHAPES.integers(1, 3000, 3)])
+def test_decode_f16_random(lh, B, H, D, S):
+    rng = np.random.default_rng(B * 19 + H * 5 + D + S)
+    k, v, q = _rnd16(rng, (B, D, S)), _rnd16(rng, (B, S, D)), _rnd16(rng, (B, H, D))
+    scale = 1 / math.sqrt(D)
+    got = _call_or_unsupported(lambda: lh.flash_decode(_dev16(k), _dev16(v), _dev16(q), scale=scale),
+                               f"decode f16 B{B} H{H} D{D} S{S}")
+    if got is None:
+        return
+    ts = min(128, S)
+    with oracle.element_type("f16"):
+        ref, _, _ = oracle.flash_decode(k, v, q, scale, 1, ts, min(64, ts))
+    assert_close(oracle.from_f16(_host16(got)), oracle.from_f16(ref), **ATTN_TOL,
+                 what=f"decode f16 B{B} H{H} D{D} S{S}")
+
+
+@pytest.mark.parametrize("case", [_mamba_case(SHAPES) for _ in range(3)])
+def test_mamba_chunk_scan_f16_random(lh, case):
+    """The chunk scan's f16 signature (every tensor f16) on the oracle's f16
+    prologue outputs rounded to f16."""
+    b, nc, H, G, Q, P, N = case
+    rng = np.random.default_rng(hash(case) % (1 << 31) + 7)
+    L = nc * Q
+    x = _rnd16(rng, (b, H, L, P))
+    Bm, C = _rnd16(rng, (b, G, L, N)), _rnd16(rng, (b, G, L, N))
+    dt_raw = np.log1p(np.exp(rng.standard_normal((b, H, L)))).astype(np.float32)
+    A = (-np.exp(rng.uniform(0, 1, H))).astype(np.float32)
+    Dh = rng.standard_normal(H).astype(np.float32)
+    h16 = lambda a: np.asarray(a, np.float32).astype(np.float16).astype(np.float32)  # noqa: E731
+    with oracle.element_type("f16"):
+        dt_o, dA_o, cb_o, prev_o = oracle.mamba_prologue(x, dt_raw, A, Bm, C, Q)
+        dt_h, dA_h, D_h, prev_h = h16(dt_o), h16(dA_o), h16(Dh), h16(prev_o)
+        ref = oracle.mamba_chunk_scan(cb_o, x, dt_h, dA_h, C, D_h, prev_h, 64, 64, 64)
+    f16 = lambda a: torch.from_numpy(a).to(torch.float16).cuda()  # noqa: E731
+    out = _call_or_unsupported(
+        lambda: lh.helion_mamba2_chunk_scan_kernel(_dev16(cb_o), _dev16(x), f16(dt_h), f16(dA_h),
+                                                   _dev16(C), f16(D_h), f16(prev_h)),
+        f"chunk scan f16 {case}")
+    if out is None:
+        return
+    assert_close(oracle.from_f16(_host16(out)), oracle.from_f16(ref), **ATTN_TOL,
+                 what=f"chunk scan f16 {case}")
