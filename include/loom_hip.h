@@ -12,9 +12,12 @@
  * reference, every tile is bounded by the extent of the loop it tiles (the
  * symbol's upper_bound, exported as natural_ub by
  * lib/passes/lcs/src/staged_etg_builder.cpp:1420-1430): a larger value is
- * rejected with LOOM_HIP_EINVAL.  Where a kernel builds a fixed set of
- * workgroup tiles, a value equal to a whole extent below those tiles is also
- * accepted and runs as the smallest built tile covering the extent.
+ * rejected with LOOM_HIP_EINVAL.  A symbol that a kernel maps onto a
+ * workgroup tile takes any multiple of 16 (the MFMA tile edge; the gfx950
+ * counterpart of lib/passes/lcs/src/hw_alignment.cpp:16) up to its extent, or
+ * the extent itself, and runs on the smallest workgroup tile built for it
+ * that covers the value (the largest built tile above them all); other values
+ * are LOOM_HIP_EINVAL.  No result depends on that choice.
  *
  * Conventions shared by every entry point:
  *   - `stream` is a hipStream_t (NULL = the default stream); work is only
@@ -67,9 +70,9 @@ const char* loom_hip_version(void);
 /* @matmul -- examples/mm/IR/00_from_helion_frontend.mlir:2
  *   (x: memref<MxK>, y: memref<KxN>, out: memref<MxN>)
  * out = x . y, bf16 in, fp32 accumulate, bf16 out.
- * (tile_m, tile_n) is the workgroup output tile: (64,64), (128,128) or
- * (256,256), tile_m <= M and tile_n <= N (tile_m = M or tile_n = N below the
- * tile names it on that axis).  tile_k (1 <= tile_k <= K) is the K step of
+ * (tile_m, tile_n), each a multiple of 16 or its whole extent (tile_m <= M,
+ * tile_n <= N), runs as the smallest square workgroup output tile of (64,64),
+ * (128,128), (256,256) covering both.  tile_k (1 <= tile_k <= K) is the K step of
  * the reference loop; the kernel stages K in its own LDS steps (the result
  * does not depend on it). */
 int loom_hip_matmul(const void* x, const void* y, void* out, int64_t M, int64_t N, int64_t K,
@@ -106,8 +109,8 @@ int loom_hip_split_k_matmul_gather(const void* a, const void* b, void* out, void
  * Flash-attention forward with online softmax; `scale` multiplies q.k (the
  * reference hard-codes the f16 constant 0.08837890625 at :10); `causal`
  * (not in the reference; needs Sq == Skv) hides key j from query i < j.
- * tile_m (64, 128, 192 or 256, at most Sq; or Sq itself below 256) is the
- * workgroup's query tile; tile_b (<= BH) and tile_n (<= Skv, the
+ * tile_m (a multiple of 16 up to Sq, or Sq) runs as the smallest workgroup
+ * query tile of 64, 128, 192, 256 covering it; tile_b (<= BH) and tile_n (<= Skv, the
  * online-softmax step) are validated, the kernel streams KV in 64-key LDS
  * blocks.  D = 64 or 128, Skv a multiple of 8. */
 int loom_hip_attention(const void* k, const void* v, const void* q, void* out, int64_t BH,
@@ -145,8 +148,11 @@ int loom_hip_flash_decode(const void* k, const void* v, const void* q, void* out
  * loom_hip_flash_decode).  Nothing is allocated and no allocating routine is
  * called.  Every call on a device shares that device's array: calls that
  * overlap in time on one device (different streams, concurrent threads)
- * race and must be ordered by the caller.  bf16 only; arguments, validation
- * and results otherwise as loom_hip_flash_decode. */
+ * race and must be ordered by the caller.  The first call on each device
+ * looks up the array's device address and must be made outside HIP graph
+ * capture: made on a stream being captured it returns LOOM_HIP_EINVAL and
+ * records nothing; every later call may be captured.  bf16 only; arguments,
+ * validation and results otherwise as loom_hip_flash_decode. */
 int loom_hip_flash_decode_noalloc(const void* k, const void* v, const void* q, void* out,
                                   int64_t B, int64_t H, int64_t D, int64_t S, float scale,
                                   int64_t tile_b, int64_t tile_s, int64_t tile_n, void* stream,
@@ -158,10 +164,12 @@ int loom_hip_flash_decode_noalloc(const void* k, const void* v, const void* q, v
  *    prev_states_T: [b,c,H,N,P] fp32, out: [b,H,L,P] bf16), L = c*Q.
  * Mamba-2 SSD chunk scan with the intra-chunk causal mask k <= m.
  * tile_b = tile_h = tile_c = 1 (the reference's size-1 subviews skip work
- * otherwise); tile_m in {64,128,192,256} rows (<= Q, or Q itself) and
- * tile_n in {16,32,64} columns (<= P, or P itself) form the workgroup tile;
- * tile_k (1 <= tile_k <= Q) is the reference's k step and does not change
- * the result.  Q <= 256, N <= 128, Q, N, P multiples of 8. */
+ * otherwise); tile_m (a multiple of 16 up to Q, or Q) runs as the smallest
+ * of 64, 128, 192, 256 rows covering it and tile_n (a multiple of 16 up to
+ * P, or P) as the smallest of 16, 32, 64 columns covering it (64 above);
+ * tile_k (1 <= tile_k <= max(8192, Q), 8192 being the example's loom.sym
+ * upper_bound) is the reference's k step and does not change the result.
+ * Q <= 256, N <= 128, Q, N, P multiples of 8. */
 int loom_hip_helion_mamba2_chunk_scan_kernel(
     const void* cb, const void* x, const void* dt, const void* dA_cumsum, const void* C,
     const void* D, const void* prev_states_T, void* out, int64_t batch, int64_t nchunks,

@@ -491,12 +491,16 @@ std::string jlist(const char* op, const std::vector<std::string>& xs) {
 std::string jrange(const char* sym, long long lo, long long hi) {
   return std::string("{\"InRange\":{\"x\":") + js(sym) + ",\"lo\":" + jc(lo) + ",\"hi\":" + jc(hi) + "}}";
 }
+std::string jdivisible(const char* sym, long long by) {
+  return std::string("{\"Divisible\":{\"x\":") + js(sym) + ",\"by\":" + jc(by) + "}}";
+}
 std::string jsym(const char* name, long long ub, long long align) {
   return std::string("\"") + name + "\":{\"type\":\"int\",\"natural_ub\":" + std::to_string(ub) +
          ",\"alignment\":" + std::to_string(align) + "}";
 }
 
 constexpr long long kLdsBytes = 160 * 1024;   // LDS per workgroup on gfx950
+constexpr long long kTileAlign = 16;          // MFMA tile edge (16x16x32)
 
 struct Scope {
   std::vector<std::string> symbols, footprint, hard, temp_iter;
@@ -517,49 +521,26 @@ int build_scope(const std::string& f, const int64_t* d, int nd, Scope& sc, std::
     return true;
   };
   // Every symbol lies in [1, natural_ub] (the extent of the loop it tiles,
-  // staged_etg_builder.cpp:1420-1430).  A tiled axis takes one of the built
-  // workgroup tiles up to its extent, or the extent itself when it is below a
-  // built tile (it then runs as the smallest built tile covering it; see
-  // loom_fit_tile in csrc/common.h).
+  // staged_etg_builder.cpp:1420-1430).  A tiled axis takes any multiple of
+  // kTileAlign up to its extent, or the extent itself: the gfx950 analogue of
+  // the reference's 32-alignment of inner tile dimensions
+  // (hw_alignment.cpp:16).  It runs on the smallest built workgroup tile
+  // covering it, or the largest built one above them all (loom_fit_tile in
+  // csrc/common.h); no kernel's result depends on that choice.
   auto ub = [&](const char* sym, long long extent) { sc.hard.push_back(jrange(sym, 1, extent)); };
-  auto cover = [](long long extent, std::initializer_list<long long> built) {
-    for (long long t : built)
-      if (t >= extent) return t;
-    return -1LL;
+  auto tiled = [&](const char* sym, long long extent) {
+    ub(sym, extent);
+    sc.hard.push_back(jlist("Or", {jdivisible(sym, kTileAlign), jop("Eq", js(sym), jc(extent))}));
   };
-  // the values of `sym` that run as workgroup tile T along an axis of `extent`
-  auto runs_as = [&](const char* sym, long long extent, long long T,
-                     std::initializer_list<long long> built) {
-    std::vector<std::string> alts;
-    if (T <= extent) alts.push_back(jop("Eq", js(sym), jc(T)));
-    else if (cover(extent, built) == T) alts.push_back(jop("Eq", js(sym), jc(extent)));
-    return alts;
-  };
-  auto tile_choice = [&](const char* sym, long long extent, std::initializer_list<long long> built) {
-    std::vector<std::string> alts;
-    for (long long T : built) {
-      auto a = runs_as(sym, extent, T, built);
-      alts.insert(alts.end(), a.begin(), a.end());
-    }
-    sc.hard.push_back(jlist("Or", alts));
-  };
-  // the GEMM tile pairs (square workgroup tiles); both LDS-staged kernels
-  // hold 256 (tile_m + tile_n) bytes
+  // GEMM workgroup tiles are square (64, 128 or 256); both A and B stage
+  // rings hold 64 KB for every built tile
   auto gemm_tiles = [&](long long M, long long N) {
-    sc.symbols.push_back(jsym("tile_m", M, 64));
-    sc.symbols.push_back(jsym("tile_n", N, 64));
-    ub("tile_m", M);
-    ub("tile_n", N);
-    std::vector<std::string> pairs;
-    for (long long T : {64LL, 128LL, 256LL}) {
-      auto am = runs_as("tile_m", M, T, {64, 128, 256});
-      auto an = runs_as("tile_n", N, T, {64, 128, 256});
-      if (am.empty() || an.empty()) continue;
-      pairs.push_back(jlist("And", {jlist("Or", am), jlist("Or", an)}));
-    }
-    sc.hard.push_back(jlist("Or", pairs));
-    sc.footprint.push_back(jop("Mul", jc(256), js("tile_m")));
-    sc.footprint.push_back(jop("Mul", jc(256), js("tile_n")));
+    sc.symbols.push_back(jsym("tile_m", M, kTileAlign));
+    sc.symbols.push_back(jsym("tile_n", N, kTileAlign));
+    tiled("tile_m", M);
+    tiled("tile_n", N);
+    sc.footprint.push_back(jc(64 * 1024));
+    sc.footprint.push_back(jc(64 * 1024));
     sc.hard.push_back(jop("Le", jop("Add", sc.footprint[0], sc.footprint[1]), jc(kLdsBytes)));
     sc.temp_iter.push_back(jop("Div", jc(M), js("tile_m")));
     sc.temp_iter.push_back(jop("Div", jc(N), js("tile_n")));
@@ -592,11 +573,10 @@ int build_scope(const std::string& f, const int64_t* d, int nd, Scope& sc, std::
       return LOOM_HIP_EUNSUP;
     }
     sc.symbols.push_back(jsym("tile_b", d[0], 1));
-    sc.symbols.push_back(jsym("tile_m", d[1], 64));
+    sc.symbols.push_back(jsym("tile_m", d[1], kTileAlign));
     sc.symbols.push_back(jsym("tile_n", d[2], 1));
     ub("tile_b", d[0]);
-    ub("tile_m", d[1]);
-    tile_choice("tile_m", d[1], {64, 128, 192, 256});
+    tiled("tile_m", d[1]);
     ub("tile_n", d[2]);
     // four stages of 64-key K and V blocks
     sc.footprint.push_back(jc(4 * 64 * d[3] * 2));
@@ -627,9 +607,13 @@ int build_scope(const std::string& f, const int64_t* d, int nd, Scope& sc, std::
             "multiples of 8, and nheads a multiple of ngroups";
       return LOOM_HIP_EUNSUP;
     }
-    sc.symbols.push_back(jsym("tile_m", d[4], 64));
-    sc.symbols.push_back(jsym("tile_n", d[5], 16));
-    sc.symbols.push_back(jsym("tile_k", d[4], 1));
+    // tile_k is bounded by the example's loom.sym upper_bound (8192,
+    // EX(mamba_chunk_scan,00):3), or by the chunk where that is longer: the
+    // kernel walks a chunk's keys in 32-key blocks whatever tile_k is
+    const long long k_ub = std::max<long long>(8192, d[4]);
+    sc.symbols.push_back(jsym("tile_m", d[4], kTileAlign));
+    sc.symbols.push_back(jsym("tile_n", d[5], kTileAlign));
+    sc.symbols.push_back(jsym("tile_k", k_ub, 1));
     sc.symbols.push_back(jsym("tile_c", d[1], 1));
     sc.symbols.push_back(jsym("tile_b", d[0], 1));
     sc.symbols.push_back(jsym("tile_h", d[2], 1));
@@ -639,13 +623,9 @@ int build_scope(const std::string& f, const int64_t* d, int nd, Scope& sc, std::
     sc.hard.push_back(jop("Eq", js("tile_b"), jc(1)));
     sc.hard.push_back(jop("Eq", js("tile_h"), jc(1)));
     sc.hard.push_back(jop("Eq", js("tile_c"), jc(1)));
-    ub("tile_m", d[4]);
-    tile_choice("tile_m", d[4], {64, 128, 192, 256});
-    ub("tile_n", d[5]);
-    tile_choice("tile_n", d[5], {16, 32, 64});
-    // tile_k tiles the keys of one chunk (the example's loom.sym bound, 8192
-    // at :1, is looser than the chunk it indexes)
-    ub("tile_k", d[4]);
+    tiled("tile_m", d[4]);
+    tiled("tile_n", d[5]);
+    ub("tile_k", k_ub);
     sc.temp_iter.push_back(jop("Div", jc(d[4]), js("tile_m")));
     sc.temp_iter.push_back(jop("Div", jc(d[5]), js("tile_n")));
     sc.seq_iter = jop("Div", jc(d[4]), js("tile_k"));
@@ -991,6 +971,7 @@ int loom_hip_hw_spec(int device, char* out, size_t outlen, char* err, size_t err
   std::string j = "{\"target\":\"gfx950\",\"wave_size\":64,\"simds_per_cu\":4,"
                   "\"vgprs_per_simd_lane\":512,\"max_workgroup_threads\":1024,"
                   "\"lds_bytes_per_workgroup\":" + std::to_string(kLdsBytes) + ","
+                  "\"tile_alignment\":" + std::to_string(kTileAlign) + ","
                   "\"xcds\":8,\"mfma\":[{\"op\":\"v_mfma_f32_16x16x32_bf16\",\"m\":16,\"n\":16,"
                   "\"k\":32,\"cycles\":16},{\"op\":\"v_mfma_f32_16x16x32_f16\",\"m\":16,\"n\":16,"
                   "\"k\":32,\"cycles\":16}],"

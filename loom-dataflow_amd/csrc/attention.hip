@@ -328,8 +328,9 @@ int attention_impl(const void* k, const void* v, const void* q, void* out, int64
                      (long long)tile_b, (long long)tile_m, (long long)tile_n);
   if (causal && Sq != Skv)
     return loom_fail(err, errlen, LOOM_EINVAL, "attention: causal needs Sq == Skv");
-  // tile_m is bounded by Sq (natural_ub); a tile_m equal to a short Sq runs
-  // as the smallest built query tile covering it
+  // tile_m is bounded by Sq (natural_ub) and runs on the smallest built
+  // query tile covering it (256 above); a query row's result does not depend
+  // on the workgroup that holds it
   static const int64_t kQTiles[4] = {64, 128, 192, 256};
   const int64_t wm = loom_fit_tile(tile_m, Sq, kQTiles, 4);
   if (wm == 0)
@@ -337,9 +338,9 @@ int attention_impl(const void* k, const void* v, const void* q, void* out, int64
                      "attention: tile_m=%lld exceeds its extent Sq=%lld (natural_ub)",
                      (long long)tile_m, (long long)Sq);
   if (wm < 0)
-    return loom_fail(err, errlen, LOOM_EUNSUP,
-                     "attention: tile_m %lld not built for gfx950 (64, 128, 192, 256, or Sq "
-                     "itself below 256)",
+    return loom_fail(err, errlen, LOOM_EINVAL,
+                     "attention: tile_m=%lld must be a multiple of 16 (the MFMA tile edge) or Sq "
+                     "itself",
                      (long long)tile_m);
   tile_m = wm;
   if (!(D == 64 || D == 128))

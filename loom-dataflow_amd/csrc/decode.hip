@@ -712,6 +712,7 @@ constexpr int kMaxDevices = 64;
 std::once_flag g_scratch_once[kMaxDevices];
 void* g_scratch[kMaxDevices];
 hipError_t g_scratch_rc[kMaxDevices];
+std::atomic<bool> g_scratch_ready[kMaxDevices];
 
 // Device address of `scratch` on the device `stream` belongs to (the current
 // device for the null stream).
@@ -731,6 +732,19 @@ int scratch_on(void* stream, void** ptr, char* err, size_t errlen) {
   if (dev < 0 || dev >= kMaxDevices)
     return loom_fail(err, errlen, LOOM_EUNSUP, "flash_decode_noalloc: device %d above %d", dev,
                      kMaxDevices - 1);
+  // The address is looked up once per device, outside any graph capture: a
+  // first call made while `stream` is being captured is refused (nothing is
+  // recorded and nothing is cached, so a later call outside capture resolves
+  // it and every call after that may be captured).
+  if (!g_scratch_ready[dev].load(std::memory_order_acquire) && stream != nullptr) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(static_cast<hipStream_t>(stream), &cs) == hipSuccess &&
+        cs != hipStreamCaptureStatusNone)
+      return loom_fail(err, errlen, LOOM_EINVAL,
+                       "flash_decode_noalloc: the first call on device %d must be made outside "
+                       "graph capture (it looks up the scratch address)",
+                       dev);
+  }
   std::call_once(g_scratch_once[dev], [dev] {
     int cur = 0;
     hipError_t r = hipGetDevice(&cur);
@@ -740,6 +754,7 @@ int scratch_on(void* stream, void** ptr, char* err, size_t errlen) {
     if (cur != dev) (void)hipSetDevice(cur);
     g_scratch[dev] = ptr;
     g_scratch_rc[dev] = r;
+    g_scratch_ready[dev].store(true, std::memory_order_release);
   });
   if (g_scratch_rc[dev] != hipSuccess || g_scratch[dev] == nullptr)
     return loom_fail(err, errlen, LOOM_EHIP,

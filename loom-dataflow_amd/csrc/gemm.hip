@@ -1041,7 +1041,8 @@ hipError_t launch_tile(const GemmParams& p, bool aligned, bool out_f32, hipStrea
   return hipGetLastError();
 }
 
-// Square workgroup tiles built for gfx950 (tile_m = tile_n).
+// Square workgroup tiles built for gfx950; a (tile_m, tile_n) binding runs
+// on the smallest one covering both symbols (loom_fit_tile).
 constexpr int64_t kGemmTiles[3] = {64, 128, 256};
 
 // Depth of the DMA pipeline of the 256x256 fallback kernel: BK-deep stages,
@@ -1078,9 +1079,9 @@ hipError_t launch_gemm(GemmParams p, int64_t tile_m, int64_t tile_n, bool aligne
 }
 
 // Checks what every GEMM entry point shares.  On success *wg is the square
-// workgroup tile the (tile_m, tile_n) binding runs as: a built tile, or --
-// for a tile equal to a whole extent below it -- the smallest one covering
-// that extent.  Every tile is bounded by its loop extent (natural_ub).
+// workgroup tile the (tile_m, tile_n) binding runs as: the smallest built tile
+// covering both (the largest built one for bindings above it).  Every tile is
+// bounded by its loop extent (natural_ub).
 int check_gemm_common(const void* a, const void* b, const void* c, int64_t M, int64_t N,
                       int64_t K, int64_t tile_m, int64_t tile_n, int64_t tile_k, int64_t* wg,
                       const char* fn, char* err, size_t errlen) {
@@ -1100,12 +1101,13 @@ int check_gemm_common(const void* a, const void* b, const void* c, int64_t M, in
                      "tile_n=%lld (N=%lld), tile_k=%lld (K=%lld)",
                      fn, (long long)tile_m, (long long)M, (long long)tile_n, (long long)N,
                      (long long)tile_k, (long long)K);
-  if (em < 0 || en < 0 || em != en)
-    return loom_fail(err, errlen, LOOM_EUNSUP,
-                     "%s: workgroup tile %lldx%lld not built for gfx950 (built: 64x64, 128x128, "
-                     "256x256; a tile equal to a whole extent runs as the smallest covering it)",
+  if (em < 0 || en < 0)
+    return loom_fail(err, errlen, LOOM_EINVAL,
+                     "%s: tile_m=%lld, tile_n=%lld: each must be a multiple of 16 (the MFMA tile "
+                     "edge) or its whole extent",
                      fn, (long long)tile_m, (long long)tile_n);
-  *wg = em;
+  // square workgroup tiles: the larger of the two covers both symbols
+  *wg = std::max(em, en);
   return LOOM_OK;
 }
 

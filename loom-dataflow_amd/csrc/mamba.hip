@@ -44,6 +44,9 @@ namespace {
 
 constexpr int kQmax = 256;   // chunk length
 constexpr int kNmax = 128;   // state size
+// upper_bound of the example's tile_k symbol
+// (examples/mamba_chunk_scan/IR/00_from_helion_frontend.mlir:3)
+constexpr int64_t kMambaTileKBound = 8192;
 
 struct MambaParams {
   const uint16_t* cb;
@@ -401,28 +404,29 @@ int chunk_scan_impl(
     return loom_fail(err, errlen, LOOM_EINVAL, "%s: tile_b, tile_h and tile_c must be 1", fn);
   if (tile_m <= 0 || tile_n <= 0 || tile_k <= 0)
     return loom_fail(err, errlen, LOOM_EINVAL, "%s: tile sizes must be positive", fn);
-  // every tile is bounded by the extent of its loop (natural_ub): tile_m and
-  // tile_k by chunk_size (the m rows and k keys of one chunk), tile_n by
-  // headdim; a tile equal to a short extent runs as the smallest built tile
-  // covering it
+  // tile_m is bounded by chunk_size (the m rows of one chunk) and tile_n by
+  // headdim (natural_ub); each runs on the smallest built tile covering it
+  // (the largest built one above).  tile_k tiles the keys of a chunk and is
+  // only validated: the kernel walks a chunk's keys in 32-key blocks whatever
+  // it is, and its bound is the example's loom.sym upper_bound (8192,
+  // examples/mamba_chunk_scan/IR/00_from_helion_frontend.mlir:3), or
+  // chunk_size where that is larger.
   static const int64_t kMTiles[4] = {64, 128, 192, 256};
   static const int64_t kNTiles[3] = {16, 32, 64};
   const int64_t wm = loom_fit_tile(tile_m, chunk_size, kMTiles, 4);
   const int64_t wn = loom_fit_tile(tile_n, headdim, kNTiles, 3);
-  if (wm == 0 || wn == 0 || tile_k > chunk_size)
+  const int64_t k_ub = std::max<int64_t>(kMambaTileKBound, chunk_size);
+  if (wm == 0 || wn == 0 || tile_k > k_ub)
     return loom_fail(err, errlen, LOOM_EINVAL,
-                     "%s: tiles exceed their extents (natural_ub): tile_m=%lld and tile_k=%lld "
-                     "(chunk_size=%lld), tile_n=%lld (headdim=%lld)",
-                     fn, (long long)tile_m, (long long)tile_k, (long long)chunk_size,
-                     (long long)tile_n, (long long)headdim);
-  if (wm < 0)
-    return loom_fail(err, errlen, LOOM_EUNSUP,
-                     "%s: tile_m must be 64, 128, 192 or 256, or chunk_size itself (got %lld)", fn,
-                     (long long)tile_m);
-  if (wn < 0)
-    return loom_fail(err, errlen, LOOM_EUNSUP,
-                     "%s: tile_n must be 16, 32 or 64, or headdim itself (got %lld)", fn,
-                     (long long)tile_n);
+                     "%s: tiles exceed their bounds (natural_ub): tile_m=%lld (chunk_size=%lld), "
+                     "tile_n=%lld (headdim=%lld), tile_k=%lld (%lld)",
+                     fn, (long long)tile_m, (long long)chunk_size, (long long)tile_n,
+                     (long long)headdim, (long long)tile_k, (long long)k_ub);
+  if (wm < 0 || wn < 0)
+    return loom_fail(err, errlen, LOOM_EINVAL,
+                     "%s: tile_m=%lld, tile_n=%lld: each must be a multiple of 16 (the MFMA tile "
+                     "edge) or its whole extent",
+                     fn, (long long)tile_m, (long long)tile_n);
   tile_m = wm;
   tile_n = wn;
   if (chunk_size > kQmax || dstate > kNmax || chunk_size % 8 || dstate % 8 || headdim % 8)

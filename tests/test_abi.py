@@ -52,8 +52,9 @@ def _call(lh, name, *args):
 
 
 def test_matmul_rejections(lh):
-    rc, msg = _call(lh, "loom_hip_matmul", FAKE, FAKE, FAKE, 256, 256, 256, 96, 96, 64, None)
-    assert rc == 2 and "not built" in msg
+    # tiles are multiples of 16 (the MFMA edge) or the whole extent
+    rc, msg = _call(lh, "loom_hip_matmul", FAKE, FAKE, FAKE, 256, 256, 256, 40, 64, 64, None)
+    assert rc == 1 and "multiple of 16" in msg
     rc, msg = _call(lh, "loom_hip_matmul", None, FAKE, FAKE, 64, 64, 64, 64, 64, 64, None)
     assert rc == 1 and "null" in msg
     rc, msg = _call(lh, "loom_hip_matmul", FAKE, FAKE, FAKE, 0, 64, 64, 64, 64, 64, None)
@@ -104,8 +105,9 @@ def test_tile_above_natural_ub_rejected(lh, name, args, sym):
 
 
 def test_whole_extent_tile_accepted(lh):
-    """A tile equal to a short extent is legal (it runs as the smallest built
-    tile covering it); anything else below the built tiles is not."""
+    """A tiled symbol takes a multiple of 16 up to its extent, or the extent
+    itself (it runs on the smallest built tile covering it); any other value
+    is rejected."""
     lh.check_variant("matmul__tile_k24__tile_m48__tile_n40", [48, 40, 24])
     lh.check_variant("matmul__tile_k24__tile_m48__tile_n64", [48, 300, 24])
     lh.check_variant("attention__tile_b1__tile_m40__tile_n40", [2, 40, 40, 64])
@@ -113,10 +115,43 @@ def test_whole_extent_tile_accepted(lh):
                      "__tile_m48__tile_n32", [1, 2, 4, 1, 48, 32, 64])
     with pytest.raises(RuntimeError) as ei:
         lh.check_variant("matmul__tile_k24__tile_m48__tile_n40", [48, 300, 24])
-    assert ei.value.code == 2
+    assert ei.value.code == 1 and "multiple of 16" in str(ei.value)
     with pytest.raises(RuntimeError) as ei:
         lh.check_variant("matmul__tile_k24__tile_m64__tile_n64", [48, 40, 24])
     assert ei.value.code == 1
+
+
+def test_reference_emitted_variants_accepted(lh):
+    """Every in-bounds binding the reference's Materialize pass emitted
+    (tests/golden/variant_names.json, from examples/*/IR/06_after_canonicalize.mlir)
+    passes validation at the example's own extents: split-K's
+    __tile_k512__tile_m64__tile_n32 on 512x4096 . 4096x512 and mqa_decode's
+    __tile_b1__tile_n512__tile_s512 on B16 H32 D128 S8192.  The other
+    examples' emitted names carry placeholder sizes beyond their extents
+    (materialize.cpp:56-65) and are rejected as such."""
+    import json
+    with open(os.path.join(os.path.dirname(__file__), "golden", "variant_names.json")) as f:
+        names = json.load(f)
+    for ex, dims in (("split_k_mm_gather", [512, 512, 4096]), ("mqa_decode", [16, 32, 128, 8192])):
+        assert len(names[ex]["variants"]) >= 8
+        for n in names[ex]["variants"]:
+            lh.check_variant(n, dims)
+    with pytest.raises(RuntimeError) as ei:
+        lh.check_variant(names["mm"]["variants"][0], [2048, 256, 256])
+    assert ei.value.code == 1 and "natural_ub" in str(ei.value)
+
+
+def test_mamba_tile_k_bound(lh):
+    """tile_k is bounded by the example's loom.sym upper_bound (8192), not by
+    the chunk: tile_k = 256 at chunk_size 192 is a binding the reference
+    accepts."""
+    base = "helion_mamba2_chunk_scan_kernel__tile_b1__tile_c1__tile_h1__tile_k{}__tile_m64__tile_n32"
+    dims = [2, 8, 32, 4, 192, 160, 128]
+    lh.check_variant(base.format(256), dims)
+    lh.check_variant(base.format(8192), dims)
+    with pytest.raises(RuntimeError) as ei:
+        lh.check_variant(base.format(8193), dims)
+    assert ei.value.code == 1 and "tile_k" in str(ei.value)
 
 
 def test_split_k_rejections(lh):
@@ -133,8 +168,8 @@ def test_split_k_rejections(lh):
 def test_attention_rejections(lh):
     args = dict(BH=4, Sq=128, Skv=128, D=128)
     base = [FAKE] * 4 + [args["BH"], args["Sq"], args["Skv"], args["D"]]
-    rc, msg = _call(lh, "loom_hip_attention", *base, 0.1, 1, 1, 96, 64, None)
-    assert rc == 2 and "tile_m" in msg
+    rc, msg = _call(lh, "loom_hip_attention", *base, 0.1, 1, 1, 40, 64, None)
+    assert rc == 1 and "tile_m" in msg and "multiple of 16" in msg
     rc, msg = _call(lh, "loom_hip_attention", FAKE, FAKE, FAKE, FAKE, 4, 128, 64, 128, 0.1, 1,
                     1, 128, 64, None)
     assert rc == 1 and "causal" in msg
@@ -191,8 +226,8 @@ def test_mamba_rejections(lh):
                     1, 4, 1, 64, 64, 64, None)
     assert rc == 1 and "tile_b, tile_h and tile_c" in msg
     rc, msg = _call(lh, "loom_hip_helion_mamba2_chunk_scan_kernel", *([FAKE] * 8), *dims,
-                    1, 1, 1, 48, 64, 64, None)
-    assert rc == 2 and "tile_m" in msg
+                    1, 1, 1, 40, 64, 64, None)
+    assert rc == 1 and "tile_m" in msg and "multiple of 16" in msg
     rc, msg = _call(lh, "loom_hip_helion_mamba2_chunk_scan_kernel", *([FAKE] * 8),
                     1, 2, 6, 4, 64, 64, 128, 1, 1, 1, 64, 64, 64, None)
     assert rc == 1 and "ngroups" in msg

@@ -144,13 +144,15 @@ def test_unsupported_shapes_and_functions():
     with pytest.raises(RuntimeError) as ei:
         loom_hip.constraint_scope("matmul", (1, 2))
     assert ei.value.code == 1
-    # TT-style 32-alignment is gone; every symbol is bounded by its extent
-    # (natural_ub): on a 48x40 GEMM the whole extents are legal (they run as
-    # one 64x64 tile), 64 exceeds them and 32 is not a gfx950 tile
+    # the TT 32-alignment becomes the 16-element MFMA edge, and every symbol is
+    # bounded by its extent (natural_ub): on a 48x40 GEMM the whole extents
+    # are legal (they run as one 64x64 tile), 64 exceeds them, 32 and 16 are
+    # multiples of 16, 24 is neither that nor an extent
     hard = loom_hip.constraint_scope("matmul", (48, 40, 24))["constraint_scope"]["hard_constraints"]
     assert all(evaluate(c, {"tile_m": 48, "tile_n": 40, "tile_k": 24}) for c in hard)
+    assert all(evaluate(c, {"tile_m": 32, "tile_n": 16, "tile_k": 24}) for c in hard)
     assert not all(evaluate(c, {"tile_m": 64, "tile_n": 64, "tile_k": 24}) for c in hard)
-    assert not all(evaluate(c, {"tile_m": 32, "tile_n": 32, "tile_k": 24}) for c in hard)
+    assert not all(evaluate(c, {"tile_m": 24, "tile_n": 32, "tile_k": 24}) for c in hard)
     assert not all(evaluate(c, {"tile_m": 48, "tile_n": 40, "tile_k": 25}) for c in hard)
 
 
@@ -175,9 +177,10 @@ def test_every_symbol_bounded_by_natural_ub(func):
 
 def test_hw_spec_is_the_scopes_machine_model():
     """loom_hip_hw_spec without a device: the LDS capacity is the one every
-    footprint constraint uses, and on large extents the values each tiled
-    symbol takes in some legal binding are exactly the built tiles hw_spec
-    lists for that function."""
+    footprint constraint uses, the built tiles are multiples of its tile
+    alignment, and on large extents the values each tiled symbol takes in
+    some legal binding are exactly the multiples of that alignment (each runs
+    on the smallest listed tile covering it)."""
     spec = loom_hip.hw_spec()
     assert spec["target"] == "gfx950" and spec["wave_size"] == 64 and "device" not in spec
     big = {"matmul": (4096, 4096, 4096), "batch_matmul": (2, 4096, 4096, 4096),
@@ -195,8 +198,12 @@ def test_hw_spec_is_the_scopes_machine_model():
             if all(evaluate(c, env) for c in scope["hard_constraints"]):
                 for s in syms:
                     seen[s].add(env[s])
+        align = spec["tile_alignment"]
         for sym, built in spec["built_tiles"][func].items():
-            assert sorted(seen[sym]) == built, (func, sym, sorted(seen[sym]), built)
+            assert all(t % align == 0 for t in built), (func, sym, built)
+            ub = scope["metadata"]["symbols"][sym]["natural_ub"]
+            want = [c for c in cand if c % align == 0 and c <= ub]
+            assert sorted(seen[sym]) == want, (func, sym, sorted(seen[sym]), want)
 
 
 def test_hw_spec_without_a_device_is_refused_cleanly():

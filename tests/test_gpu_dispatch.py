@@ -123,10 +123,22 @@ def test_dispatch_mamba(lh, variants):
     assert_close(from_bf16(host(out)), from_bf16(ref), **ATTN_TOL, what=name)
 
 
-def test_dispatch_rejects_unbuilt_tiles(lh):
+def test_dispatch_runs_every_aligned_binding(lh):
+    """A binding with no workgroup tile of its own (tile_n 32 beside tile_m
+    64, the pair the reference emits for split-K) runs on the smallest built
+    tile covering it, bit-identical to that tile; a value that is neither a
+    multiple of 16 nor the extent is rejected with LOOM_HIP_EINVAL."""
     rng = np.random.default_rng(35)
-    x = dev(rng_bf16(rng, (64, 64)))
-    out = torch.empty((64, 64), dtype=torch.bfloat16, device="cuda")
+    x, y = rng_bf16(rng, (192, 320)), rng_bf16(rng, (320, 160))
+    ref = oracle.matmul(x, y, 64, 64, 64)
+    direct = lh.matmul(dev(x), dev(y), tile_m=64, tile_n=64, tile_k=64)
+    for tm, tn in ((64, 32), (16, 48), (48, 160), (192, 112)):
+        name = f"matmul__tile_k64__tile_m{tm}__tile_n{tn}"
+        out = torch.empty((192, 160), dtype=torch.bfloat16, device="cuda")
+        lh.dispatch(name, dev(x), dev(y), out)
+        assert torch.equal(out, direct), name
+        assert_close(from_bf16(host(out)), from_bf16(ref), **GEMM_TOL, what=name)
+    out = torch.empty((192, 160), dtype=torch.bfloat16, device="cuda")
     with pytest.raises(RuntimeError) as ei:
-        lh.dispatch("matmul__tile_k64__tile_m64__tile_n32", x, x, out)
-    assert ei.value.code == 2
+        lh.dispatch("matmul__tile_k64__tile_m64__tile_n40", dev(x), dev(y), out)
+    assert ei.value.code == 1

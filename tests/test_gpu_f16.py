@@ -119,6 +119,35 @@ def test_flash_decode_f16(lh):
     assert_close(lse.cpu().numpy(), lse_r, atol=1e-3, rtol=1e-4, what="decode f16 lse")
 
 
+@pytest.mark.parametrize("S,ts", [(1024, 44), (2048, 256)])
+def test_flash_decode_f16_d64_dma(lh, S, ts):
+    """f16 at D = 64 with S a multiple of 8: the LDS-DMA split kernel's f16
+    D = 64 instantiation, including splits that start off an 8-key boundary
+    (tile_s 44); output, lse_s and o_s against the oracle."""
+    rng = np.random.default_rng(S + ts)
+    B, H, D = 2, 12, 64
+    k, v, q = rnd(rng, (B, D, S)), rnd(rng, (B, S, D)), rnd(rng, (B, H, D))
+    out, lse, o = lh.flash_decode(dev(k), dev(v), dev(q), tile_s=ts, tile_n=ts,
+                                  return_partials=True)
+    ref, lse_r, o_r = oracle.flash_decode(k, v, q, 1 / math.sqrt(D), 1, ts, ts)
+    assert_close(from_f16(host(out)), from_f16(ref), **ATTN_TOL, what=f"decode f16 D64 S{S} ts{ts}")
+    assert_close(lse.cpu().numpy(), lse_r, atol=1e-2, rtol=1e-3, what=f"decode f16 D64 lse ts{ts}")
+    assert_close(o.cpu().numpy(), o_r, **ATTN_TOL, what=f"decode f16 D64 o_s ts{ts}")
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_attention_f16_d64(lh, causal):
+    """f16 attention at head_dim 64 (the D = 64 instantiations in f16)."""
+    rng = np.random.default_rng(58 + causal)
+    BH, S, D = 2, 456, 64
+    k, v, q = rnd(rng, (BH, D, S)), rnd(rng, (BH, S, D)), rnd(rng, (BH, S, D))
+    for tile_m in (64, 128, 192, 256):
+        out = host(lh.attention(dev(k), dev(v), dev(q), causal=causal, tile_m=tile_m))
+        ref = oracle.attention(k, v, q, 1 / math.sqrt(D), causal, 1, 64, 64)
+        assert_close(from_f16(out), from_f16(ref), **ATTN_TOL,
+                     what=f"attention f16 D64 causal={causal} tile_m={tile_m}")
+
+
 def _ssd_inputs(rng, b, H, G, L, P, N):
     x = rnd(rng, (b, H, L, P))
     Bm, C = rnd(rng, (b, G, L, N)), rnd(rng, (b, G, L, N))

@@ -442,7 +442,9 @@ def test_decode_baseline(lh):
 def test_decode_workspace_reuse_and_garbage(lh):
     """A workspace full of garbage, then the same workspace reused for
     different inputs, gives each call's own result; and 128 splits (the
-    combine's lane-parallel reduction taken in chunks of 64)."""
+    combine loads the splits in chunks of 16 and rescales its running sum
+    from one chunk to the next, so this case crosses eight chunk
+    boundaries)."""
     rng = np.random.default_rng(21)
     B, H, D, S = 3, 32, 128, 2048
     ts = 256
@@ -453,7 +455,7 @@ def test_decode_workspace_reuse_and_garbage(lh):
         ref, _, _ = oracle.flash_decode(k, v, q, 1 / math.sqrt(D), 1, ts, 128)
         got = lh.flash_decode(dev(k), dev(v), dev(q), workspace=ws, tile_s=ts, tile_n=128)
         assert_close(from_bf16(host(got)), from_bf16(ref), **ATTN_TOL, what=f"reuse {trial}")
-    # ns = 2048 / 16 = 128 > 64 splits: separate combine kernel
+    # ns = 2048 / 16 = 128 splits: eight 16-split chunks of the combine
     k, v, q = rng_bf16(rng, (B, D, S)), rng_bf16(rng, (B, S, D)), rng_bf16(rng, (B, H, D))
     ref, _, _ = oracle.flash_decode(k, v, q, 1 / math.sqrt(D), 1, 16, 16)
     got = lh.flash_decode(dev(k), dev(v), dev(q), tile_s=16, tile_n=16)

@@ -160,8 +160,8 @@ def test_dispatch_rejections():
     rc, msg = _dispatch_raw("matmul__tile_k64__tile_m128__tile_n128", 2, [256, 256, 256])
     assert rc == 1 and "takes 3 tensors and 3 extents" in msg
     # the entry point's own validation answers through dispatch
-    rc, msg = _dispatch_raw("matmul__tile_k64__tile_m96__tile_n96", 3, [256, 256, 256])
-    assert rc == 2 and "tile" in msg  # legal in the reference, not built here
+    rc, msg = _dispatch_raw("matmul__tile_k64__tile_m40__tile_n64", 3, [256, 256, 256])
+    assert rc == 1 and "multiple of 16" in msg  # neither MFMA-aligned nor the extent
     # the placeholder mamba variant binds tile_h=4, tile_c=8, which the
     # gfx950 kernel does not take
     rc, msg = _dispatch_raw("helion_mamba2_chunk_scan_kernel__tile_b1__tile_c8__tile_h4"
