@@ -568,8 +568,8 @@ int build_scope(const std::string& f, const int64_t* d, int nd, Scope& sc, std::
     sc.temp_iter.push_back(jop("Div", jc(d[2]), js("tile_k")));
   } else if (f == "attention") {
     if (!need(4)) return LOOM_HIP_EINVAL;
-    if (!(d[3] == 64 || d[3] == 128) || d[2] % 8) {
-      err = "constraint_scope: attention is built for head_dim 64 or 128 and Skv a multiple of 8";
+    if (!(d[3] == 64 || d[3] == 128)) {
+      err = "constraint_scope: attention is built for head_dim 64 or 128";
       return LOOM_HIP_EUNSUP;
     }
     sc.symbols.push_back(jsym("tile_b", d[0], 1));
@@ -587,8 +587,8 @@ int build_scope(const std::string& f, const int64_t* d, int nd, Scope& sc, std::
     sc.seq_iter = jop("Div", jc(d[2]), js("tile_n"));
   } else if (f == "flash_decode") {
     if (!need(4)) return LOOM_HIP_EINVAL;
-    if (!(d[2] == 64 || d[2] == 128) || d[1] > 32) {
-      err = "constraint_scope: flash_decode is built for head_dim 64 or 128 and H <= 32";
+    if (!(d[2] == 64 || d[2] == 128)) {
+      err = "constraint_scope: flash_decode is built for head_dim 64 or 128";
       return LOOM_HIP_EUNSUP;
     }
     sc.symbols.push_back(jsym("tile_b", d[0], 1));

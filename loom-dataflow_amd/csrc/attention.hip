@@ -60,7 +60,13 @@ LOOM_DEV int k_swz(int d) { return (2 * (d & 3)) ^ (2 * ((d >> 3) & 1)); }
 template <int D>
 LOOM_DEV int v_swz(int k) { return D == 128 ? 2 * (k & 7) : 2 * ((k >> 1) & 3); }
 
-template <int D, int QT, int W, bool H>
+// KREG (Skv not a multiple of 8): K rows [d][0..Skv) do not start on
+// 16-byte boundaries, so K cannot be copied by 16-byte LDS DMA.  Each lane
+// then loads its 16-byte piece of a K block into registers (one 16-byte
+// buffer load when Skv is even, eight 2-byte loads when it is odd), issued
+// before the block NS-1 stages ahead of the one being computed and written
+// to the same LDS position after that computation; V keeps its DMA.
+template <int D, int QT, int W, bool H, bool KREG>
 __global__ void __launch_bounds__(64 * W) attention_dma_kernel(AttnParams p) {
   constexpr int KB = 64;                        // keys per stage
   constexpr int NS = 4;                         // stages
@@ -110,13 +116,15 @@ __global__ void __launch_bounds__(64 * W) attention_dma_kernel(AttnParams p) {
   auto issue = [&](int s, int blk) {
     const int kv0 = blk * KB;
     const uint32_t lk = lds_addr(stK(s)), lv = lds_addr(stV(s));
+    if constexpr (!KREG) {
 #pragma unroll
-    for (int i = 0; i < K_INSTR; ++i) {
-      const int j = wave * K_INSTR + i;
-      const int d = j * 8 + lane / 8;                     // Ks row
-      const int c = (lane % 8) ^ k_swz(d);
-      const int key = min(kv0 + c * 8, Skv - 8);
-      dma_load16(kg + (int64_t)d * Skv + key, lk + j * 1024);
+      for (int i = 0; i < K_INSTR; ++i) {
+        const int j = wave * K_INSTR + i;
+        const int d = j * 8 + lane / 8;                     // Ks row
+        const int c = (lane % 8) ^ k_swz(d);
+        const int key = min(kv0 + c * 8, Skv - 8);
+        dma_load16(kg + (int64_t)d * Skv + key, lk + j * 1024);
+      }
     }
 #pragma unroll
     for (int i = 0; i < V_INSTR; ++i) {
@@ -128,13 +136,81 @@ __global__ void __launch_bounds__(64 * W) attention_dma_kernel(AttnParams p) {
     }
   };
 
+  // ---- KREG: this lane's K pieces of block `blk` (the DMA's positions:
+  // row d, 8 keys from key) into registers, then into stage s
+  const rsrc_t krs = make_rsrc(kg, KREG ? (uint32_t)(D * Skv * 2) : 0u);
+  // buffer loads of 16 and 4 bytes need 4-byte aligned addresses (only
+  // 2-byte alignment is required of k on this path)
+  const uint32_t kg_lo = (uint32_t)reinterpret_cast<uintptr_t>(kg);
+  const bool k4 = (Skv & 1) == 0 && (kg_lo & 3u) == 0;   // every row 4-byte aligned
+  u32x4_t kr[KREG ? K_INSTR : 1];
+  auto kload = [&](int blk) {
+    const int kv0 = blk * KB;
+#pragma unroll
+    for (int i = 0; i < K_INSTR; ++i) {
+      const int j = wave * K_INSTR + i;
+      const int d = j * 8 + lane / 8;
+      const int c = (lane % 8) ^ k_swz(d);
+      // keys key .. key+7.  A piece inside the row at a 4-byte aligned
+      // address is one 16-byte load; at a 2-byte aligned one, a 16-byte and
+      // a 4-byte load from two bytes earlier, shifted into place (when the
+      // piece neither starts the tensor nor ends its row, so both loads stay
+      // inside the descriptor's range).  Other pieces reaching into the row
+      // take eight 2-byte loads (elements past the row are masked keys, and
+      // past the tensor the range check returns zeros); a piece wholly past
+      // Skv is masked.
+      const int key = kv0 + c * 8;
+      const uint32_t off = (uint32_t)(d * Skv + key) * 2;
+      const bool al = ((kg_lo + off) & 3u) == 0;
+      if (k4) {                                           // wave-uniform
+        kr[i] = key + 8 <= Skv ? buf_load16(krs, off) : u32x4_t{0u, 0u, 0u, 0u};
+        if (key < Skv && key + 8 > Skv) {
+          uint32_t h[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) h[e] = buf_load2(krs, off + 2 * e);
+          kr[i] = u32x4_t{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
+                          h[6] | (h[7] << 16)};
+        }
+      } else if (key + 8 <= Skv && (al || (off >= 2 && key + 8 < Skv))) {
+        const uint32_t o4 = al ? off : off - 2;
+        const u32x4_t w = buf_load16(krs, o4);
+        const uint32_t x = buf_load4(krs, o4 + 16);
+        kr[i] = al ? w
+                   : u32x4_t{__builtin_amdgcn_alignbyte(w[1], w[0], 2),
+                             __builtin_amdgcn_alignbyte(w[2], w[1], 2),
+                             __builtin_amdgcn_alignbyte(w[3], w[2], 2),
+                             __builtin_amdgcn_alignbyte(x, w[3], 2)};
+      } else if (key < Skv) {
+        uint32_t h[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) h[e] = buf_load2(krs, off + 2 * e);
+        kr[i] = u32x4_t{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
+                        h[6] | (h[7] << 16)};
+      } else {
+        kr[i] = u32x4_t{0u, 0u, 0u, 0u};
+      }
+    }
+  };
+  auto kstore = [&](int s) {
+#pragma unroll
+    for (int i = 0; i < K_INSTR; ++i)
+      *reinterpret_cast<__attribute__((address_space(3))) u32x4_t*>(
+          stK(s) + (wave * K_INSTR + i) * 1024 + lane * 16) = kr[i];
+  };
+
   const int kv_end = p.causal ? min(Skv, q0 + BQ) : Skv;
   const int nblk = (kv_end + KB - 1) / KB;
   // the first NS-1 KV blocks start loading before Q, so their latency and
   // Q's overlap (the compiler's wait for Q then also covers these DMAs)
 #pragma unroll
   for (int s = 0; s < NS - 1; ++s)
-    if (s < nblk) issue(s, s);
+    if (s < nblk) {
+      if constexpr (KREG) {
+        kload(s);
+        kstore(s);
+      }
+      issue(s, s);
+    }
 
   // ---- Q^T operands: lane holds q[q0w + 16 qt + r][32 ds + 8 g .. +7] times
   // scale * log2(e), rounded to bf16, so scores come out in the log2 domain
@@ -287,9 +363,21 @@ __global__ void __launch_bounds__(64 * W) attention_dma_kernel(AttnParams p) {
         if (younger >= 2) LOOM_WAIT_VMCNT(2 * LPW);
         else if (younger == 1) LOOM_WAIT_VMCNT(LPW);
         else LOOM_WAIT_VMCNT(0);
+        // KREG: this wave's K stores of the previous iteration are in LDS
+        if constexpr (KREG) LOOM_WAIT_LGKM0();
         barrier_nofence();
-        if (it + NS - 1 < nblk) issue((s + NS - 1) % NS, it + NS - 1);
+        const bool ahead = it + NS - 1 < nblk;
+        if constexpr (KREG) {
+          if (ahead) kload(it + NS - 1);
+        }
+        if (ahead) issue((s + NS - 1) % NS, it + NS - 1);
         compute(s, it);
+        // KREG: the stage written here was last read before this
+        // iteration's barrier (block it - 1); the compiler waits for the
+        // loads (and, since it cannot tell them apart, everything older)
+        if constexpr (KREG) {
+          if (ahead) kstore((s + NS - 1) % NS);
+        }
       }
     }
   }
@@ -309,6 +397,21 @@ __global__ void __launch_bounds__(64 * W) attention_dma_kernel(AttnParams p) {
             u32x2_t{pack2<H>(o[0] * inv, o[1] * inv), pack2<H>(o[2] * inv, o[3] * inv)};
       }
     }
+  }
+}
+
+template <bool H, bool KREG>
+void launch_attention(const AttnParams& p, int64_t D, int64_t tile_m, hipStream_t st) {
+  const dim3 grid((unsigned)(p.BH * p.nqt)), b4(256), b8(512);
+  switch ((D == 128 ? 10 : 0) + (int)(tile_m / 64)) {
+    case 11: hipLaunchKernelGGL((attention_dma_kernel<128, 1, 4, H, KREG>), grid, b4, 0, st, p); break;
+    case 12: hipLaunchKernelGGL((attention_dma_kernel<128, 1, 8, H, KREG>), grid, b8, 0, st, p); break;
+    case 13: hipLaunchKernelGGL((attention_dma_kernel<128, 3, 4, H, KREG>), grid, b4, 0, st, p); break;
+    case 14: hipLaunchKernelGGL((attention_dma_kernel<128, 2, 8, H, KREG>), grid, b8, 0, st, p); break;
+    case 1: hipLaunchKernelGGL((attention_dma_kernel<64, 1, 4, H, KREG>), grid, b4, 0, st, p); break;
+    case 2: hipLaunchKernelGGL((attention_dma_kernel<64, 1, 8, H, KREG>), grid, b8, 0, st, p); break;
+    case 3: hipLaunchKernelGGL((attention_dma_kernel<64, 3, 4, H, KREG>), grid, b4, 0, st, p); break;
+    default: hipLaunchKernelGGL((attention_dma_kernel<64, 2, 8, H, KREG>), grid, b8, 0, st, p); break;
   }
 }
 
@@ -346,10 +449,16 @@ int attention_impl(const void* k, const void* v, const void* q, void* out, int64
   if (!(D == 64 || D == 128))
     return loom_fail(err, errlen, LOOM_EUNSUP, "attention: head_dim %lld not built (64, 128)",
                      (long long)D);
-  if (Skv % 8 != 0)
-    return loom_fail(err, errlen, LOOM_EUNSUP, "attention: Skv must be a multiple of 8");
-  if (!aligned16(k) || !aligned16(v) || !aligned16(q) || (reinterpret_cast<uintptr_t>(out) & 7u))
-    return loom_fail(err, errlen, LOOM_EINVAL, "attention: tensors must be 16-byte aligned");
+  // Skv not a multiple of 8 takes the register-staged K path (KREG), whose
+  // K buffer descriptor addresses one (b, h)'s D x Skv keys in 32 bits
+  const bool kreg = Skv % 8 != 0;
+  if (kreg && !loom_prod_le({D, Skv, 2}, 0x7fffffffll))
+    return loom_fail(err, errlen, LOOM_EINVAL, "attention: D*Skv too large");
+  if ((!kreg && !aligned16(k)) || (reinterpret_cast<uintptr_t>(k) & 1u) || !aligned16(v) ||
+      !aligned16(q) || (reinterpret_cast<uintptr_t>(out) & 7u))
+    return loom_fail(err, errlen, LOOM_EINVAL,
+                     "attention: v and q must be 16-byte aligned, out 8-byte, k 16-byte (2-byte "
+                     "when Skv is not a multiple of 8)");
   if (Sq > (1 << 30) || Skv > (1 << 30) || !loom_prod_le({BH, cdiv64(Sq, tile_m)}, 0x7fffffff) ||
       !loom_prod_le({BH, Sq, D}, (int64_t)1 << 50) || !loom_prod_le({BH, Skv, D}, (int64_t)1 << 50))
     return loom_fail(err, errlen, LOOM_EINVAL, "attention: problem too large");
@@ -366,19 +475,8 @@ int attention_impl(const void* k, const void* v, const void* q, void* out, int64
   p.c2 = scale * 1.4426950408889634f;
   if (loom_validate_only()) return loom_ok(err, errlen);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  {
-    const dim3 grid((unsigned)(p.BH * p.nqt)), b4(256), b8(512);
-    switch ((D == 128 ? 10 : 0) + (int)(tile_m / 64)) {
-      case 11: hipLaunchKernelGGL((attention_dma_kernel<128, 1, 4, H>), grid, b4, 0, st, p); break;
-      case 12: hipLaunchKernelGGL((attention_dma_kernel<128, 1, 8, H>), grid, b8, 0, st, p); break;
-      case 13: hipLaunchKernelGGL((attention_dma_kernel<128, 3, 4, H>), grid, b4, 0, st, p); break;
-      case 14: hipLaunchKernelGGL((attention_dma_kernel<128, 2, 8, H>), grid, b8, 0, st, p); break;
-      case 1: hipLaunchKernelGGL((attention_dma_kernel<64, 1, 4, H>), grid, b4, 0, st, p); break;
-      case 2: hipLaunchKernelGGL((attention_dma_kernel<64, 1, 8, H>), grid, b8, 0, st, p); break;
-      case 3: hipLaunchKernelGGL((attention_dma_kernel<64, 3, 4, H>), grid, b4, 0, st, p); break;
-      default: hipLaunchKernelGGL((attention_dma_kernel<64, 2, 8, H>), grid, b8, 0, st, p); break;
-    }
-  }
+  if (kreg) launch_attention<H, true>(p, D, tile_m, st);
+  else launch_attention<H, false>(p, D, tile_m, st);
   return loom_check_launch(err, errlen, "attention");
 }
 

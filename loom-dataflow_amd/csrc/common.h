@@ -261,6 +261,9 @@ LOOM_DEV u32x4_t buf_load16(rsrc_t r, uint32_t off) {
 LOOM_DEV u32x2_t buf_load8(rsrc_t r, uint32_t off) {
   return __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
 }
+LOOM_DEV uint32_t buf_load4(rsrc_t r, uint32_t off) {
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+}
 LOOM_DEV uint32_t buf_load2(rsrc_t r, uint32_t off) {
   return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
 }

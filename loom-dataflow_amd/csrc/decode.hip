@@ -154,6 +154,8 @@ __global__ void __launch_bounds__(256) decode_dma_kernel(DecodeParams p) {
 
   const int split = blockIdx.x, b = blockIdx.y;
   const int H = p.H, S = p.S;
+  // head group blockIdx.z: query heads h0 .. h0 + Hl - 1 (32 head slots)
+  const int h0 = (int)blockIdx.z * 32, Hl = min(32, H - h0);
   const int s0 = split * p.tile_s;
   const int s1 = min(S, s0 + p.tile_s);
   const int kbeg = s0 & ~7;                    // 16-byte aligned first key
@@ -184,7 +186,8 @@ __global__ void __launch_bounds__(256) decode_dma_kernel(DecodeParams p) {
       dma_load16(vg + (int64_t)key * D + c * 8, lv + j * 1024);
     }
   };
-  // q[b] (32 head slots, rows past H clamped to row H-1 and zeroed on read)
+  // q[b] (32 head slots of the group, rows past its heads clamped to its
+  // last head and zeroed on read)
   // arrives by LDS DMA ahead of the first stages: a plain load would make the
   // compiler wait for every copy in flight before its first use
   lds_char_t* sq = (lds_char_t*)(smem + NS * STAGE);
@@ -192,7 +195,7 @@ __global__ void __launch_bounds__(256) decode_dma_kernel(DecodeParams p) {
   for (int i = 0; i < Q_INSTR; ++i) {
     const int j = wave * Q_INSTR + i;
     const int e = j * 512 + lane * 8;                     // element of the [32][D] slots
-    const int hq = min(e / D, H - 1);
+    const int hq = h0 + min(e / D, Hl - 1);
     dma_load16(p.q + ((int64_t)b * H + hq) * D + e % D, lds_addr(sq) + j * 1024);
   }
 #pragma unroll
@@ -313,7 +316,7 @@ __global__ void __launch_bounds__(256) decode_dma_kernel(DecodeParams p) {
           for (int ds = 0; ds < DSTEPS; ++ds) {
             const u32x4_t raw = *reinterpret_cast<const __attribute__((address_space(3))) u32x4_t*>(
                 sq + (h * D + ds * 32 + g * 8) * 2);
-            qf[ds] = h < H ? raw : u32x4_t{0u, 0u, 0u, 0u};
+            qf[ds] = h < Hl ? raw : u32x4_t{0u, 0u, 0u, 0u};
           }
         }
         if (it + NS - 1 < nblk) issue((s + NS - 1) % NS, it + NS - 1);
@@ -341,7 +344,7 @@ __global__ void __launch_bounds__(256) decode_dma_kernel(DecodeParams p) {
   // 16-byte LDS reads and stores
   constexpr int DPT = D / 8;                   // d values per thread
   const int hh = tid >> 3, d0 = (tid & 7) * DPT;
-  if (hh < H) {
+  if (hh < Hl) {
     const float* w0 = mg + (2 * (hh >> 4)) * 16 * ROW + (hh & 15) * ROW;
     const float* w1 = w0 + 16 * ROW;
     // a half that saw no key of the split (l = 0) takes no part
@@ -351,7 +354,7 @@ __global__ void __launch_bounds__(256) decode_dma_kernel(DecodeParams p) {
     const float f1 = l1 > 0.f ? fast_exp2(w1[D] - M) : 0.f;
     const float L = l0 * f0 + l1 * f1;
     const float g0 = f0 / L, g1 = f1 / L;
-    const int64_t row = ((int64_t)split * p.B + b) * H + hh;
+    const int64_t row = ((int64_t)split * p.B + b) * H + h0 + hh;
     f32x4_t* dst = reinterpret_cast<f32x4_t*>(p.o + row * D + d0);
 #pragma unroll
     for (int u = 0; u < DPT / 4; ++u) {
@@ -382,13 +385,15 @@ __global__ void __launch_bounds__(64 * kWaves) decode_split_kernel(DecodeParams 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, g = lane >> 4;
   const int H = p.H, S = p.S;
+  // head group blockIdx.z: query heads h0 .. h0 + Hl - 1
+  const int h0 = (int)blockIdx.z * 32, Hl = min(32, H - h0);
   const int s0 = split * p.tile_s;
   const int s1 = min(S, s0 + p.tile_s);
   const int nblk = (s1 - s0 + kBlockKeys - 1) / kBlockKeys;
 
   const rsrc_t krs = make_rsrc(p.k + (int64_t)b * D * S, (uint32_t)(D * S * 2));
   const rsrc_t vrs = make_rsrc(p.v + (int64_t)b * S * D, (uint32_t)(S * D * 2));
-  const uint16_t* __restrict__ qb = p.q + (int64_t)b * H * D;
+  const uint16_t* __restrict__ qb = p.q + ((int64_t)b * H + h0) * D;
 
   // Q^T operands, shared by the waves through LDS: slot [ds][ht][lane]
   // holds q[h = r + 16 ht][32 ds + 8 g .. +7]
@@ -396,7 +401,7 @@ __global__ void __launch_bounds__(64 * kWaves) decode_split_kernel(DecodeParams 
   for (int e = threadIdx.x; e < DSTEPS * HT * 64; e += 64 * kWaves) {
     const int ln = e & 63, ht = (e >> 6) % HT, ds = (e >> 6) / HT;
     const int h = (ln & 15) + 16 * ht;
-    sm_q[ds][ht][ln] = h < H ? *reinterpret_cast<const u32x4_t*>(qb + (int64_t)h * D + ds * 32 +
+    sm_q[ds][ht][ln] = h < Hl ? *reinterpret_cast<const u32x4_t*>(qb + (int64_t)h * D + ds * 32 +
                                                                   (ln >> 4) * 8)
                              : u32x4_t{0u, 0u, 0u, 0u};
   }
@@ -580,8 +585,8 @@ __global__ void __launch_bounds__(64 * kWaves) decode_split_kernel(DecodeParams 
   __syncthreads();
 
   // ---- merge the waves: (lse_s, o_s) for every (head, d) of this split
-  const int64_t row0 = ((int64_t)split * p.B + b) * H;
-  for (int e = threadIdx.x; e < H * D; e += 64 * kWaves) {
+  const int64_t row0 = ((int64_t)split * p.B + b) * H + h0;
+  for (int e = threadIdx.x; e < Hl * D; e += 64 * kWaves) {
     const int h = e / D, d = e % D;
     float M = -INFINITY;
 #pragma unroll
@@ -601,7 +606,7 @@ __global__ void __launch_bounds__(64 * kWaves) decode_split_kernel(DecodeParams 
 
 template <int D, int HT, bool F16>
 void launch_split(const DecodeParams& p, bool aligned, hipStream_t st) {
-  const dim3 grid(p.ns, p.B), block(64 * kWaves);
+  const dim3 grid(p.ns, p.B, (p.H + 31) / 32), block(64 * kWaves);
   if (aligned)
     hipLaunchKernelGGL((decode_split_kernel<D, HT, true, F16>), grid, block, 0, st, p);
   else
@@ -635,8 +640,8 @@ int flash_decode_impl(const void* k, const void* v, const void* q, void* out,
   if (!(D == 64 || D == 128))
     return loom_fail(err, errlen, LOOM_EUNSUP, "flash_decode: head_dim %lld not built (64, 128)",
                      (long long)D);
-  if (H > 32)
-    return loom_fail(err, errlen, LOOM_EUNSUP, "flash_decode: at most 32 query heads (got %lld)",
+  if (H > 32 * 65535)
+    return loom_fail(err, errlen, LOOM_EINVAL, "flash_decode: too many query heads (got %lld)",
                      (long long)H);
   if (!loom_prod_le({S, D, 2}, 0x7fffffffll) || B > 65535)
     return loom_fail(err, errlen, LOOM_EINVAL, "flash_decode: S*D or B too large");
@@ -666,7 +671,7 @@ int flash_decode_impl(const void* k, const void* v, const void* q, void* out,
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (S % 8 == 0) {
     // LDS-DMA split kernel: K rows start on 16-byte boundaries
-    const dim3 grid((unsigned)ns, (unsigned)B), block(256);
+    const dim3 grid((unsigned)ns, (unsigned)B, (unsigned)cdiv64(H, 32)), block(256);
     if (D == 128)
       hipLaunchKernelGGL((decode_dma_kernel<128, F16>), grid, block, 0, st, p);
     else

@@ -189,8 +189,8 @@ def test_flash_decode_rejections(lh):
                     B, H, D, S, 0.1, 1, ts, 64, None)
     assert rc == 1 and "workspace" in msg
     rc, msg = _call(lh, "loom_hip_flash_decode", FAKE, FAKE, FAKE, FAKE, FAKE, need,
-                    B, 64, D, S, 0.1, 1, ts, 64, None)
-    assert rc == 2 and "heads" in msg
+                    B, H, 96, S, 0.1, 1, ts, 64, None)
+    assert rc == 2 and "head_dim" in msg
     rc, msg = _call(lh, "loom_hip_flash_decode", FAKE, FAKE, FAKE, FAKE, FAKE, need,
                     B, H, D, S, 0.1, 1, S + 8, 64, None)
     assert rc == 1
@@ -212,9 +212,9 @@ def test_flash_decode_noalloc_rejections(lh):
                     1, 256, 64, None)
     assert rc == 1 and "scratch" in msg, (rc, msg)
     # the workspace form's own checks run first too
-    rc, msg = _call(lh, "loom_hip_flash_decode_noalloc", FAKE, FAKE, FAKE, FAKE, B, 64, D, S, 0.1,
+    rc, msg = _call(lh, "loom_hip_flash_decode_noalloc", FAKE, FAKE, FAKE, FAKE, B, H, 96, S, 0.1,
                     1, 1024, 64, None)
-    assert rc == 2 and "heads" in msg, (rc, msg)
+    assert rc == 2 and "head_dim" in msg, (rc, msg)
     rc, msg = _call(lh, "loom_hip_flash_decode_noalloc", FAKE, FAKE, FAKE, FAKE, B, H, D, S, -1.0,
                     1, 1024, 64, None)
     assert rc == 1 and "scale" in msg, (rc, msg)

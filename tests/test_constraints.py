@@ -57,7 +57,8 @@ CASES = {
     "batch_matmul": (["tile_b", "tile_m", "tile_n", "tile_k"], [(16, 2048, 2048, 2048), (2, 96, 80, 64)]),
     "split_k_matmul_gather": (["tile_m", "tile_n", "tile_k"], [(512, 512, 16384), (48, 96, 1000)]),
     "attention": (["tile_b", "tile_m", "tile_n"], [(128, 4096, 4096, 128), (3, 1000, 1000, 64)]),
-    "flash_decode": (["tile_b", "tile_s", "tile_n"], [(32, 32, 128, 8192), (3, 5, 64, 1000)]),
+    "flash_decode": (["tile_b", "tile_s", "tile_n"], [(32, 32, 128, 8192), (3, 5, 64, 1000),
+                                                       (2, 64, 128, 2048)]),
     "helion_mamba2_chunk_scan_kernel": (["tile_m", "tile_n", "tile_k", "tile_c", "tile_b", "tile_h"],
                                         [(4, 16, 32, 1, 256, 64, 128), (2, 8, 32, 4, 192, 160, 128)]),
 }

@@ -393,6 +393,25 @@ def test_decode_partials_match_oracle(lh, golden):
     assert_close(o.cpu().numpy(), o_ref, **ATTN_TOL, what="o_s")
 
 
+@pytest.mark.parametrize("H,D,S,ts", [(40, 128, 2048, 512), (64, 64, 1024, 100),
+                                      (96, 128, 1001, 256), (33, 64, 1004, 128)])
+def test_decode_more_than_32_heads(lh, H, D, S, ts):
+    """More query heads than one workgroup's 32 slots: head groups of 32 on
+    the third grid axis, each streaming the split's K and V (LDS-DMA kernel
+    for S a multiple of 8, register kernel otherwise); output and both
+    gathered partials against the oracle."""
+    print(f"decode H{H} D{D} S{S} tile_s{ts}", flush=True)
+    rng = np.random.default_rng(H * 7 + S)
+    B = 2
+    k, v, q = rng_bf16(rng, (B, D, S)), rng_bf16(rng, (B, S, D)), rng_bf16(rng, (B, H, D))
+    ref, lse_r, o_r = oracle.flash_decode(k, v, q, 1 / math.sqrt(D), 1, ts, 64)
+    got, lse, o = lh.flash_decode(dev(k), dev(v), dev(q), tile_s=ts, tile_n=64,
+                                  return_partials=True)
+    assert_close(from_bf16(host(got)), from_bf16(ref), **ATTN_TOL, what=f"decode H{H} S{S}")
+    assert_close(lse.cpu().numpy(), lse_r, atol=1e-2, rtol=1e-3, what=f"decode H{H} lse_s")
+    assert_close(o.cpu().numpy(), o_r, **ATTN_TOL, what=f"decode H{H} o_s")
+
+
 @pytest.mark.parametrize("S,ts", [(1001, 256), (1004, 128)])
 def test_decode_register_path(lh, S, ts):
     """S not a multiple of 8: K rows do not start on 16-byte boundaries, so the

@@ -6,10 +6,9 @@ random legal binding, against the CPU oracle.
 Integer-valued GEMM inputs make matmul, batch_matmul and split-K exact (the
 oracle's fp32 sums are exact below 2^24), so those compare bit for bit;
 attention, decode and the Mamba-2 path use the floating-point bars of
-tests/test_gpu_parity.py.  Attention draws Skv as a multiple of 8 (what its
-kernel is built for) and every draw must run; elsewhere a shape the library
-does not build (LOOM_HIP_EUNSUP) must be refused with that code before
-anything launches, and no other error is accepted.
+tests/test_gpu_parity.py.  Every attention draw must launch; elsewhere a shape
+the library does not build (LOOM_HIP_EUNSUP) must be refused with that code
+before anything launches, and no other error is accepted.
 """
 import math
 
@@ -96,17 +95,11 @@ def test_split_k_random(lh, M, N, K, tk):
     assert np.array_equal(host(out), o_ref), (M, N, K, tk, "out")
 
 
-def _up8(n):
-    return 8 * -(-int(n) // 8)
-
-
-# The attention kernel streams K ([BH, D, Skv], keys contiguous) by 16-byte
-# LDS-DMA copies, so it is built for Skv a multiple of 8: the draws round Skv
-# up to one (Sq stays ragged where the mask allows it) and every draw must run;
-# test_attention_unbuilt_skv_refused checks the refusal of the others.
+# every draw must launch: ragged Skv (not a multiple of 8) takes the
+# register-staged K path, multiples of 8 the LDS-DMA one
 @pytest.mark.parametrize("BH,Sq,Skv,D,causal", [
-    (int(SHAPES.integers(1, 4)), _up8(sq) if c else int(sq),
-     _up8(sq) if c else _up8(SHAPES.integers(1, 700)), int(SHAPES.choice([64, 128])), bool(c))
+    (int(SHAPES.integers(1, 4)), int(sq), int(sq) if c else int(SHAPES.integers(1, 700)),
+     int(SHAPES.choice([64, 128])), bool(c))
     for sq, c in zip(SHAPES.integers(1, 700, 6), [1, 0, 1, 0, 1, 0])])
 def test_attention_random(lh, BH, Sq, Skv, D, causal):
     rng = np.random.default_rng(BH * 13 + Sq * 101 + Skv + D)
@@ -135,20 +128,54 @@ def test_decode_random(lh, B, H, D, S):
 
 
 @pytest.mark.parametrize("f16", [False, True])
-def test_attention_unbuilt_skv_refused(lh, f16):
-    """Skv not a multiple of 8 is refused with LOOM_HIP_EUNSUP before anything
-    launches (the output keeps its sentinel)."""
-    BH, Sq, Skv, D = 2, 100, 381, 128
-    dt = torch.float16 if f16 else torch.bfloat16
-    k = torch.zeros((BH, D, Skv), dtype=dt, device="cuda")
-    v = torch.zeros((BH, Skv, D), dtype=dt, device="cuda")
-    q = torch.zeros((BH, Sq, D), dtype=dt, device="cuda")
-    out = torch.full((BH, Sq, D), 7.0, dtype=dt, device="cuda")
-    with pytest.raises(RuntimeError) as ei:
-        lh.attention(k, v, q, out)
-    assert ei.value.code == 2 and "multiple of 8" in str(ei.value)
-    torch.cuda.synchronize()
-    assert bool((out == 7.0).all())
+@pytest.mark.parametrize("BH,Sq,Skv,D,causal,tile_m", [
+    (2, 100, 381, 128, False, 256), (1, 381, 381, 128, True, 128), (2, 77, 250, 64, False, 64),
+    (1, 250, 250, 64, True, 192), (3, 5, 5, 128, True, 64), (1, 1, 13, 64, False, 64),
+    (2, 333, 1003, 128, False, 256)])
+def test_attention_skv_not_multiple_of_8(lh, f16, BH, Sq, Skv, D, causal, tile_m):
+    """Skv not a multiple of 8 (odd and even, below one 8-key piece, causal
+    and not): K rows do not start on 16-byte boundaries and K is staged
+    through registers; against the oracle in the tensors' element type."""
+    tile_m = tile_m if tile_m <= Sq else Sq          # bounded by Sq (natural_ub)
+    print(f"attention ragged Skv BH{BH} Sq{Sq} Skv{Skv} D{D} causal={causal} "
+          f"tile_m={tile_m} f16={f16}", flush=True)
+    rng = np.random.default_rng(Skv * 31 + Sq + D + f16)
+    if f16:
+        k, v, q = _rnd16(rng, (BH, D, Skv)), _rnd16(rng, (BH, Skv, D)), _rnd16(rng, (BH, Sq, D))
+        got = _host16(lh.attention(_dev16(k), _dev16(v), _dev16(q), causal=causal, tile_m=tile_m))
+        with oracle.element_type("f16"):
+            ref = oracle.from_f16(oracle.attention(k, v, q, 1 / math.sqrt(D), causal, 1, 64, 64))
+        gotf = oracle.from_f16(got)
+    else:
+        k, v, q = rng_bf16(rng, (BH, D, Skv)), rng_bf16(rng, (BH, Skv, D)), rng_bf16(rng, (BH, Sq, D))
+        gotf = from_bf16(host(lh.attention(dev(k), dev(v), dev(q), causal=causal, tile_m=tile_m)))
+        ref = from_bf16(oracle.attention(k, v, q, 1 / math.sqrt(D), causal, 1, 64, 64))
+    assert_close(gotf, ref, **ATTN_TOL,
+                 what=f"attention Skv{Skv} Sq{Sq} D{D} causal={causal} f16={f16}")
+
+
+@pytest.mark.parametrize("Skv", [250, 381, 1000])
+def test_attention_k_two_byte_aligned(lh, Skv):
+    """k starting 2 bytes past a 4-byte boundary (a view at an odd element
+    offset): with Skv not a multiple of 8 the register-staged K loads shift
+    misaligned pieces into place; with Skv a multiple of 8 such a k is refused
+    (its rows would not start on 16-byte boundaries for the LDS DMA)."""
+    BH, Sq, D = 2, 123, 128
+    rng = np.random.default_rng(Skv + 5)
+    k, v, q = rng_bf16(rng, (BH, D, Skv)), rng_bf16(rng, (BH, Skv, D)), rng_bf16(rng, (BH, Sq, D))
+    flat = torch.empty(BH * D * Skv + 1, dtype=torch.bfloat16, device="cuda")
+    kd = flat[1:].view(BH, D, Skv)
+    kd.copy_(dev(k))
+    assert kd.data_ptr() % 4 == 2
+    print(f"attention k at 2 mod 4 Skv{Skv}", flush=True)
+    if Skv % 8 == 0:
+        with pytest.raises(RuntimeError) as ei:
+            lh.attention(kd, dev(v), dev(q))
+        assert ei.value.code == 1 and "aligned" in str(ei.value)
+        return
+    got = from_bf16(host(lh.attention(kd, dev(v), dev(q))))
+    ref = from_bf16(oracle.attention(k, v, q, 1 / math.sqrt(D), False, 1, 64, 64))
+    assert_close(got, ref, **ATTN_TOL, what=f"attention k at 2 mod 4, Skv{Skv}")
 
 
 def _mamba_case(rng):
@@ -245,7 +272,7 @@ def test_split_k_f16_random(lh, M, N, K, tk):
 
 
 # the first f16 draw is pinned to D = 64 (the other head size's f16 kernels)
-@pytest.mark.parametrize("BH,S,D,causal", [(int(SHAPES.integers(1, 4)), _up8(s),
+@pytest.mark.parametrize("BH,S,D,causal", [(int(SHAPES.integers(1, 4)), int(s),
                                             64 if i == 0 else d, bool(c))
                                            for i, (s, c, d) in enumerate(
                                                zip(SHAPES.integers(1, 600, 3), [1, 0, 1],
