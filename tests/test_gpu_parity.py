@@ -21,8 +21,7 @@ import torch
 
 import oracle
 from oracle import from_bf16, to_bf16
-from tests.conftest import (ATTN_TILES, GEMM_TILES, MAMBA_M_TILES, assert_close, assert_close_gpu,
-                            tile_for)
+from tests.conftest import ATTN_TILES, GEMM_TILES, MAMBA_M_TILES, assert_close, tile_for
 
 pytestmark = pytest.mark.gpu
 
@@ -154,23 +153,15 @@ def test_batch_matmul_golden(lh, golden):
 
 
 def test_batch_matmul_baseline(lh):
-    """B16 x 2048^3 (the bench config): every batch against the oracle on 64
-    sampled rows, every element against an fp32 product on the GPU, and a
-    second run bit-identical to the first."""
+    """B16 x 2048^3 (the bench config): every element of every batch against
+    the oracle, and a second run bit-identical to the first."""
     torch.manual_seed(0)
     a0 = (torch.randn(16, 2048, 2048, device="cuda") * 0.02).to(torch.bfloat16)
     a1 = (torch.randn(16, 2048, 2048, device="cuda") * 0.02).to(torch.bfloat16)
     dout = lh.batch_matmul(a0, a1, tile_m=256, tile_n=256)
     out = host(dout)
-    rows = np.random.default_rng(5).choice(2048, 64, replace=False)
-    rows.sort()
-    h0, h1 = host(a0), host(a1)
-    for b in range(16):
-        ref = oracle.matmul(np.ascontiguousarray(h0[b][rows]), h1[b])
-        assert_close(from_bf16(out[b][rows]), from_bf16(ref), **GEMM_TOL, what=f"bmm batch {b}")
-    full = torch.bmm(a0.float(), a1.float())            # fp32 operands, contiguous
-    assert_close_gpu(dout, full, **GEMM_TOL, what="bmm every element vs fp32")
-    del full
+    ref = oracle.batch_matmul(host(a0), host(a1), 1, 256, 256, 64)
+    assert_close(from_bf16(out), from_bf16(ref), **GEMM_TOL, what="bmm B16 2048^3 vs oracle")
     again = lh.batch_matmul(a0, a1, tile_m=256, tile_n=256)
     assert torch.equal(dout.view(torch.int16), again.view(torch.int16))
 
@@ -325,34 +316,22 @@ def test_attention_vs_oracle_mid(lh):
             assert_close(got, ref, **ATTN_TOL, what=f"attention S=1000 causal={causal} tile_m={tm}")
 
 
-@pytest.mark.parametrize("tile_m", [192, 256])
-def test_attention_baseline_heads(lh, tile_m):
-    """B4 x H32, S 4096, D 128, causal (the bench config): 3 heads vs the
-    oracle, all 128 heads against a plain fp32 softmax(q k * scale) v on the
-    GPU (the oracle's running sum starts at l = 1, but its first rescale
-    multiplies that by exp(-inf) = 0, so its result is the plain softmax),
-    and a second run bit-identical to the first."""
+def test_attention_baseline_heads(lh):
+    """B4 x H32, S 4096, D 128, causal (the bench config) with query tiles of
+    192 and 256: every element of all 128 heads against the oracle, and a
+    second run bit-identical to the first."""
     torch.manual_seed(1)
     BH, S, D = 128, 4096, 128
     k = torch.randn(BH, D, S, device="cuda").to(torch.bfloat16)
     v = torch.randn(BH, S, D, device="cuda").to(torch.bfloat16)
     q = torch.randn(BH, S, D, device="cuda").to(torch.bfloat16)
-    dout = lh.attention(k, v, q, causal=True, tile_m=tile_m, tile_n=64)
-    out = host(dout)
-    assert np.isfinite(from_bf16(out)).all()
-    for h in (0, 77, 127):
-        ref = oracle.attention(host(k[h:h + 1]), host(v[h:h + 1]), host(q[h:h + 1]),
-                               1 / math.sqrt(D), True, 1, 128, 64)
-        assert_close(from_bf16(out[h:h + 1]), from_bf16(ref), **ATTN_TOL, what=f"head {h}")
-    hidden = torch.triu(torch.ones(S, S, dtype=torch.bool, device="cuda"), diagonal=1)
-    for h0 in range(0, BH, 8):                            # 8 heads: 512 MB of fp32 scores
-        s = torch.bmm(q[h0:h0 + 8].float(), k[h0:h0 + 8].float()) * (1 / math.sqrt(D))
-        s.masked_fill_(hidden, float("-inf"))
-        ref = torch.bmm(torch.softmax(s, dim=-1), v[h0:h0 + 8].float())
-        assert_close_gpu(dout[h0:h0 + 8], ref, **ATTN_TOL, what=f"heads {h0}..{h0 + 7} vs fp32")
-    del s, ref
-    again = lh.attention(k, v, q, causal=True, tile_m=tile_m, tile_n=64)
-    assert torch.equal(dout.view(torch.int16), again.view(torch.int16))
+    ref = from_bf16(oracle.attention(host(k), host(v), host(q), 1 / math.sqrt(D), True, 1, 128, 64))
+    for tile_m in (192, 256):
+        dout = lh.attention(k, v, q, causal=True, tile_m=tile_m, tile_n=64)
+        assert_close(from_bf16(host(dout)), ref, **ATTN_TOL,
+                     what=f"flashattn B4 H32 S4096 causal tile_m {tile_m} vs oracle")
+        again = lh.attention(k, v, q, causal=True, tile_m=tile_m, tile_n=64)
+        assert torch.equal(dout.view(torch.int16), again.view(torch.int16))
 
 
 @pytest.mark.parametrize("causal,BH,Sq,Skv,D", [(True, 48, 2816, 2816, 128),
