@@ -129,6 +129,61 @@ __global__ void __launch_bounds__(64 * kWaves, kWaves == 8 ? 4 : 1)
   const uint16_t* __restrict__ pvh = reinterpret_cast<const uint16_t*>(p.prevT) + pv0;  // f16 form
   const int64_t sidx = ((int64_t)(b * H + h) * p.nc + c) * Q;
 
+  const float Dh = side_at<F16>(p.Dh, h);
+  const int nmt16 = (mend - m0 + 15) / 16;  // 16-row tiles of this workgroup
+  constexpr int MAXT = kQmax / 16 / kWaves;  // tiles per wave at most
+  constexpr int NSN = kNmax / 32;            // state-term steps at most
+  constexpr int NKS = kQmax / 32;            // intra-chunk steps at most
+  // snake deal of 16-row tiles: slot ti of wave w is tile 4 ti + (w or 3 - w)
+  auto tile_of = [&](int ti) {
+    return kWaves * ti + ((ti & 1) ? (kWaves - 1 - wave) : wave);
+  };
+  // C and cb rows come straight from global memory as MFMA operands.  A
+  // tile's C rows are loaded while the previous tile computes (two register
+  // sets); so are its cb rows with 4 waves, while with 8 waves (128 VGPRs)
+  // they are loaded at the tile's start, behind its state term's MFMAs.
+  // Buffer loads read rows past the chunk as zeros.
+  const rsrc_t rC = make_rsrc(Cg, (uint32_t)(Q * N * 2));
+  const rsrc_t rCB = make_rsrc(cbg, (uint32_t)(Q * Q * 2));
+  constexpr bool kCbAhead = kWaves == 4;
+  struct CRows {
+    u32x4_t c[NSN];
+  };
+  struct BRows {
+    u32x4_t cb[NKS];
+  };
+  // Every load is issued, unneeded ones with an offset past the
+  // descriptor's range (zeros, no memory access): the compiler can then
+  // count the loads younger than the ones it waits for, where a
+  // conditional load makes it wait for all of them, prefetch included.
+  constexpr uint32_t kNone = 0x7ffffff0u;
+  auto fetch_c = [&](int ti, CRows& rw) {
+    const int am = m0 + 16 * tile_of(ti) + rr;
+#pragma unroll
+    for (int ns = 0; ns < NSN; ++ns)
+      rw.c[ns] = buf_load16(rC, ns * 32 < N ? (uint32_t)(am * N + ns * 32 + g4 * 8) * 2 : kNone);
+  };
+  auto fetch_cb = [&](int ti, BRows& rw) {
+    const int mrow0 = m0 + 16 * tile_of(ti);
+    const int am = mrow0 + rr;
+    const int kend = min(mrow0 + 16, Q);
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks)
+      rw.cb[ks] = buf_load16(rCB, ks * 32 < kend ? (uint32_t)(am * Q + ks * 32 + g4 * 8) * 2 : kNone);
+  };
+
+  // The MFMAs compute out^T tiles (x^T / prevT^T as the row operand, W / C
+  // as the column operand): lane (rr, g4) of tile (ti, pt) accumulates
+  // out[m = mrow0 + rr][p = 16 pt + 4 g4 + i], four consecutive columns.
+  uint16_t* og = p.out + ((int64_t)(b * H + h) * L + (int64_t)c * Q) * P;
+  CRows cbuf[2];
+  BRows bbuf[kCbAhead ? 2 : 1];
+  // the first tile's C rows (and, with 4 waves, its cb rows) are loaded
+  // before the staging loads, so their latency overlaps the staging instead
+  // of following it (BASELINE shape 81.4 -> 78.1 us; the 8-wave form's cb
+  // rows as well would spill at 128 VGPRs)
+  fetch_c(0, cbuf[0]);
+  if constexpr (kCbAhead) fetch_cb(0, bbuf[0]);
   // ---- staging: every global load first, then conversions and LDS stores.
   // One 8x8 block of x per thread (k-chunk fastest; k rounded up to the
   // 32-deep MFMA step, rows past the chunk zero-filled); half an 8x8 block
@@ -215,57 +270,6 @@ __global__ void __launch_bounds__(64 * kWaves, kWaves == 8 ? 4 : 1)
   }
   __syncthreads();
 
-  const float Dh = side_at<F16>(p.Dh, h);
-  const int nmt16 = (mend - m0 + 15) / 16;  // 16-row tiles of this workgroup
-  constexpr int MAXT = kQmax / 16 / kWaves;  // tiles per wave at most
-  constexpr int NSN = kNmax / 32;            // state-term steps at most
-  constexpr int NKS = kQmax / 32;            // intra-chunk steps at most
-  // snake deal of 16-row tiles: slot ti of wave w is tile 4 ti + (w or 3 - w)
-  auto tile_of = [&](int ti) {
-    return kWaves * ti + ((ti & 1) ? (kWaves - 1 - wave) : wave);
-  };
-  // C and cb rows come straight from global memory as MFMA operands.  A
-  // tile's C rows are loaded while the previous tile computes (two register
-  // sets); so are its cb rows with 4 waves, while with 8 waves (128 VGPRs)
-  // they are loaded at the tile's start, behind its state term's MFMAs.
-  // Buffer loads read rows past the chunk as zeros.
-  const rsrc_t rC = make_rsrc(Cg, (uint32_t)(Q * N * 2));
-  const rsrc_t rCB = make_rsrc(cbg, (uint32_t)(Q * Q * 2));
-  constexpr bool kCbAhead = kWaves == 4;
-  struct CRows {
-    u32x4_t c[NSN];
-  };
-  struct BRows {
-    u32x4_t cb[NKS];
-  };
-  // Every load is issued, unneeded ones with an offset past the
-  // descriptor's range (zeros, no memory access): the compiler can then
-  // count the loads younger than the ones it waits for, where a
-  // conditional load makes it wait for all of them, prefetch included.
-  constexpr uint32_t kNone = 0x7ffffff0u;
-  auto fetch_c = [&](int ti, CRows& rw) {
-    const int am = m0 + 16 * tile_of(ti) + rr;
-#pragma unroll
-    for (int ns = 0; ns < NSN; ++ns)
-      rw.c[ns] = buf_load16(rC, ns * 32 < N ? (uint32_t)(am * N + ns * 32 + g4 * 8) * 2 : kNone);
-  };
-  auto fetch_cb = [&](int ti, BRows& rw) {
-    const int mrow0 = m0 + 16 * tile_of(ti);
-    const int am = mrow0 + rr;
-    const int kend = min(mrow0 + 16, Q);
-#pragma unroll
-    for (int ks = 0; ks < NKS; ++ks)
-      rw.cb[ks] = buf_load16(rCB, ks * 32 < kend ? (uint32_t)(am * Q + ks * 32 + g4 * 8) * 2 : kNone);
-  };
-
-  // The MFMAs compute out^T tiles (x^T / prevT^T as the row operand, W / C
-  // as the column operand): lane (rr, g4) of tile (ti, pt) accumulates
-  // out[m = mrow0 + rr][p = 16 pt + 4 g4 + i], four consecutive columns.
-  uint16_t* og = p.out + ((int64_t)(b * H + h) * L + (int64_t)c * Q) * P;
-  CRows cbuf[2];
-  BRows bbuf[kCbAhead ? 2 : 1];
-  fetch_c(0, cbuf[0]);
-  if constexpr (kCbAhead) fetch_cb(0, bbuf[0]);
 #pragma unroll
   for (int ti = 0; ti < MAXT; ++ti) {
     if (tile_of(ti) >= nmt16) continue;
