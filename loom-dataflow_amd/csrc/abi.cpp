@@ -568,10 +568,11 @@ int build_scope(const std::string& f, const int64_t* d, int nd, Scope& sc, std::
     sc.temp_iter.push_back(jop("Div", jc(d[2]), js("tile_k")));
   } else if (f == "attention") {
     if (!need(4)) return LOOM_HIP_EINVAL;
-    if (!(d[3] == 64 || d[3] == 128)) {
-      err = "constraint_scope: attention is built for head_dim 64 or 128";
+    if (d[3] % 8 || d[3] > 128) {
+      err = "constraint_scope: attention is built for head_dim a multiple of 8 up to 128";
       return LOOM_HIP_EUNSUP;
     }
+    const long long dk = d[3] <= 64 ? 64 : 128;   // the kernel's (padded) head dim
     sc.symbols.push_back(jsym("tile_b", d[0], 1));
     sc.symbols.push_back(jsym("tile_m", d[1], kTileAlign));
     sc.symbols.push_back(jsym("tile_n", d[2], 1));
@@ -579,16 +580,16 @@ int build_scope(const std::string& f, const int64_t* d, int nd, Scope& sc, std::
     tiled("tile_m", d[1]);
     ub("tile_n", d[2]);
     // four stages of 64-key K and V blocks
-    sc.footprint.push_back(jc(4 * 64 * d[3] * 2));
-    sc.footprint.push_back(jc(4 * 64 * d[3] * 2));
+    sc.footprint.push_back(jc(4 * 64 * dk * 2));
+    sc.footprint.push_back(jc(4 * 64 * dk * 2));
     sc.hard.push_back(jop("Le", jop("Add", sc.footprint[0], sc.footprint[1]), jc(kLdsBytes)));
     sc.temp_iter.push_back(jop("Div", jc(d[0]), js("tile_b")));
     sc.temp_iter.push_back(jop("Div", jc(d[1]), js("tile_m")));
     sc.seq_iter = jop("Div", jc(d[2]), js("tile_n"));
   } else if (f == "flash_decode") {
     if (!need(4)) return LOOM_HIP_EINVAL;
-    if (!(d[2] == 64 || d[2] == 128)) {
-      err = "constraint_scope: flash_decode is built for head_dim 64 or 128";
+    if (d[2] % 8 || d[2] > 128) {
+      err = "constraint_scope: flash_decode is built for head_dim a multiple of 8 up to 128";
       return LOOM_HIP_EUNSUP;
     }
     sc.symbols.push_back(jsym("tile_b", d[0], 1));

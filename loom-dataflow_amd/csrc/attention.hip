@@ -9,6 +9,10 @@
 //   acc' = acc*alpha + P.V (:97-113); out = acc / l (:116-121).
 //   `causal` (absent from the reference) makes key j visible to query i
 //   only when j <= i; fully hidden KV blocks are skipped.
+//   Any head dim that is a multiple of 8 up to 128 runs on the kernel built
+//   for 64 or 128: the K rows past it are copied from zeros, the Q elements
+//   past it are zero, so the scores are exact; the V columns past it only
+//   reach O columns that are never stored.
 //
 // gfx950 mapping (attention_dma_kernel below): a workgroup of W waves owns
 // 16 QT W query rows of one (b, h) and streams K and V through LDS in
@@ -26,6 +30,7 @@ struct AttnParams {
   const uint16_t* q;
   uint16_t* out;
   int BH, Sq, Skv, causal, nqt;
+  int D;     // head dim: a multiple of 8, at most the kernel's D
   float c2;  // scale * log2(e)
 };
 
@@ -95,10 +100,10 @@ __global__ void __launch_bounds__(64 * W) attention_dma_kernel(AttnParams p) {
   const int qtile = p.nqt - 1 - L / p.BH;       // heaviest tiles first
   const int bh = L % p.BH;
   const int q0 = qtile * BQ;
-  const int Sq = p.Sq, Skv = p.Skv;
-  const uint16_t* __restrict__ kg = p.k + (int64_t)bh * D * Skv;
-  const uint16_t* __restrict__ vg = p.v + (int64_t)bh * Skv * D;
-  const uint16_t* __restrict__ qg = p.q + (int64_t)bh * Sq * D;
+  const int Sq = p.Sq, Skv = p.Skv, Dr = p.D;
+  const uint16_t* __restrict__ kg = p.k + (int64_t)bh * Dr * Skv;
+  const uint16_t* __restrict__ vg = p.v + (int64_t)bh * Skv * Dr;
+  const uint16_t* __restrict__ qg = p.q + (int64_t)bh * Sq * Dr;
 
   auto stK = [&](int s) -> lds_char_t* {
     if (s == 0) return (lds_char_t*)sK0;
@@ -112,7 +117,9 @@ __global__ void __launch_bounds__(64 * W) attention_dma_kernel(AttnParams p) {
     if (s == 2) return (lds_char_t*)sV2;
     return (lds_char_t*)sV3;
   };
-  // ---- DMA of block `blk` into stage s (keys past Skv are clamped: masked later)
+  // ---- DMA of block `blk` into stage s (keys past Skv are clamped: masked
+  // later; Ks rows d >= Dr, eight to a copy, come from zeros; Vs chunks past
+  // Dr repeat the row's last chunk)
   auto issue = [&](int s, int blk) {
     const int kv0 = blk * KB;
     const uint32_t lk = lds_addr(stK(s)), lv = lds_addr(stV(s));
@@ -123,22 +130,25 @@ __global__ void __launch_bounds__(64 * W) attention_dma_kernel(AttnParams p) {
         const int d = j * 8 + lane / 8;                     // Ks row
         const int c = (lane % 8) ^ k_swz(d);
         const int key = min(kv0 + c * 8, Skv - 8);
-        dma_load16(kg + (int64_t)d * Skv + key, lk + j * 1024);
+        if (j * 8 < Dr)                                     // wave-uniform
+          dma_load16(kg + (int64_t)d * Skv + key, lk + j * 1024);
+        else
+          dma_load16(loom_zero_kb + lane * 4, lk + j * 1024);
       }
     }
 #pragma unroll
     for (int i = 0; i < V_INSTR; ++i) {
       const int j = wave * V_INSTR + i;
       const int kr = j * V_ROWS_PER_I + lane / (D / 8);   // Vs row (key)
-      const int c = (lane % (D / 8)) ^ v_swz<D>(kr);
+      const int c = min((lane % (D / 8)) ^ v_swz<D>(kr), Dr / 8 - 1);
       const int key = min(kv0 + kr, Skv - 1);
-      dma_load16(vg + (int64_t)key * D + c * 8, lv + j * 1024);
+      dma_load16(vg + (int64_t)key * Dr + c * 8, lv + j * 1024);
     }
   };
 
   // ---- KREG: this lane's K pieces of block `blk` (the DMA's positions:
   // row d, 8 keys from key) into registers, then into stage s
-  const rsrc_t krs = make_rsrc(kg, KREG ? (uint32_t)(D * Skv * 2) : 0u);
+  const rsrc_t krs = make_rsrc(kg, KREG ? (uint32_t)(Dr * Skv * 2) : 0u);
   // buffer loads of 16 and 4 bytes need 4-byte aligned addresses (only
   // 2-byte alignment is required of k on this path)
   const uint32_t kg_lo = (uint32_t)reinterpret_cast<uintptr_t>(kg);
@@ -151,6 +161,10 @@ __global__ void __launch_bounds__(64 * W) attention_dma_kernel(AttnParams p) {
       const int j = wave * K_INSTR + i;
       const int d = j * 8 + lane / 8;
       const int c = (lane % 8) ^ k_swz(d);
+      if (j * 8 >= Dr) {                                  // padding rows: zeros
+        kr[i] = u32x4_t{0u, 0u, 0u, 0u};
+        continue;
+      }
       // keys key .. key+7.  A piece inside the row at a 4-byte aligned
       // address is one 16-byte load; at a 2-byte aligned one, a 16-byte and
       // a 4-byte load from two bytes earlier, shifted into place (when the
@@ -214,6 +228,7 @@ __global__ void __launch_bounds__(64 * W) attention_dma_kernel(AttnParams p) {
 
   // ---- Q^T operands: lane holds q[q0w + 16 qt + r][32 ds + 8 g .. +7] times
   // scale * log2(e), rounded to bf16, so scores come out in the log2 domain
+  // (zero past Dr)
   const int q0w = q0 + 16 * QT * wave;
   u32x4_t qf[DSTEPS][QT];
 #pragma unroll
@@ -221,8 +236,9 @@ __global__ void __launch_bounds__(64 * W) attention_dma_kernel(AttnParams p) {
     const int qrow = min(q0w + 16 * qt + r, Sq - 1);
 #pragma unroll
     for (int ds = 0; ds < DSTEPS; ++ds) {
-      const u32x4_t raw =
-          *reinterpret_cast<const u32x4_t*>(qg + (int64_t)qrow * D + ds * 32 + g * 8);
+      const int d0 = ds * 32 + g * 8;
+      const u32x4_t raw = d0 < Dr ? *reinterpret_cast<const u32x4_t*>(qg + (int64_t)qrow * Dr + d0)
+                                  : u32x4_t{0u, 0u, 0u, 0u};
 #pragma unroll
       for (int e = 0; e < 4; ++e)
         qf[ds][qt][e] = pack2<H>(lo16<H>(raw[e]) * p.c2, hi16<H>(raw[e]) * p.c2);
@@ -389,12 +405,13 @@ __global__ void __launch_bounds__(64 * W) attention_dma_kernel(AttnParams p) {
     const float inv = 1.f / lacc[qt][0];
     const int qrow = q0w + 16 * qt + r;
     if (qrow < Sq) {
-      uint16_t* orow = p.out + ((int64_t)bh * Sq + qrow) * D;
+      uint16_t* orow = p.out + ((int64_t)bh * Sq + qrow) * Dr;
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
         const f32x4_t o = ot[dt][qt];
-        *reinterpret_cast<u32x2_t*>(orow + dt * 16 + 4 * g) =
-            u32x2_t{pack2<H>(o[0] * inv, o[1] * inv), pack2<H>(o[2] * inv, o[3] * inv)};
+        if (dt * 16 + 4 * g < Dr)
+          *reinterpret_cast<u32x2_t*>(orow + dt * 16 + 4 * g) =
+              u32x2_t{pack2<H>(o[0] * inv, o[1] * inv), pack2<H>(o[2] * inv, o[3] * inv)};
       }
     }
   }
@@ -446,8 +463,9 @@ int attention_impl(const void* k, const void* v, const void* q, void* out, int64
                      "itself",
                      (long long)tile_m);
   tile_m = wm;
-  if (!(D == 64 || D == 128))
-    return loom_fail(err, errlen, LOOM_EUNSUP, "attention: head_dim %lld not built (64, 128)",
+  if (D % 8 != 0 || D > 128)
+    return loom_fail(err, errlen, LOOM_EUNSUP,
+                     "attention: head_dim %lld not built (a multiple of 8 up to 128)",
                      (long long)D);
   // Skv not a multiple of 8 takes the register-staged K path (KREG), whose
   // K buffer descriptor addresses one (b, h)'s D x Skv keys in 32 bits
@@ -472,11 +490,14 @@ int attention_impl(const void* k, const void* v, const void* q, void* out, int64
   p.Skv = (int)Skv;
   p.causal = causal ? 1 : 0;
   p.nqt = (int)cdiv64(Sq, tile_m);
+  p.D = (int)D;
   p.c2 = scale * 1.4426950408889634f;
   if (loom_validate_only()) return loom_ok(err, errlen);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (kreg) launch_attention<H, true>(p, D, tile_m, st);
-  else launch_attention<H, false>(p, D, tile_m, st);
+  // the kernel built for 64 or 128 (the next one up) runs any narrower D
+  const int64_t Dk = D <= 64 ? 64 : 128;
+  if (kreg) launch_attention<H, true>(p, Dk, tile_m, st);
+  else launch_attention<H, false>(p, Dk, tile_m, st);
   return loom_check_launch(err, errlen, "attention");
 }
 

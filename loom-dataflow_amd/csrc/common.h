@@ -306,6 +306,11 @@ LOOM_DEV void dma_load16(const void* g, uint32_t lds) {
       : "memory", "m0");
 }
 
+// 1 KB of zeros in device memory: the source of the LDS-DMA copies of
+// padding rows (an operand narrower than the tile built for it), so those
+// rows hold zeros and every wave still issues the same copies per stage.
+static __device__ __align__(1024) uint32_t loom_zero_kb[256] = {};
+
 // LDS banks repeat every 256 bytes.  A transposed read (below) serves 32
 // lanes per pass; when each of its 16-lane groups reads rows r..r+3 of one
 // tile and the two groups rows r+4..r+7, the pass touches 32-byte pieces of 8

@@ -24,6 +24,10 @@
 // Softmax runs in the log2 domain in fp32.  The waves' partial states merge
 // through LDS into (lse_s, o_s), exactly the reference's gathered tensors;
 // decode_combine_kernel performs the split-0 combine.
+// Any head dim that is a multiple of 8 up to 128 runs on the kernels built
+// for 64 or 128: K rows and q elements past it are zeros (copied from zeros,
+// or read past the buffer range), so the scores are exact, and V columns
+// past it only reach O columns that are never stored.
 #include "common.h"
 
 #include <cmath>
@@ -42,6 +46,7 @@ struct DecodeParams {
   float* o;    // [ns, B, H, D]
   uint16_t* out;
   int B, H, S, tile_s, ns;
+  int D;       // head dim: a multiple of 8, at most the kernel's D
   float c2;    // scale * log2(e)
 };
 
@@ -51,9 +56,10 @@ struct DecodeParams {
 // and o loads are independent and issued together (in chunks of CH splits:
 // 8 when there are at most 8, else 16), so the combine costs about one
 // memory round trip.
-template <int D, bool F16, int CH>
+template <bool F16, int CH>
 __global__ void __launch_bounds__(256) decode_combine_kernel(DecodeParams p) {
-  constexpr int TPR = D / 2;   // threads per (b, head) row
+  const int D = p.D;
+  const int TPR = D / 2;       // threads per (b, head) row
   const int64_t BH = (int64_t)p.B * p.H;
   const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const int64_t bh = t / TPR;
@@ -160,12 +166,15 @@ __global__ void __launch_bounds__(256) decode_dma_kernel(DecodeParams p) {
   const int s1 = min(S, s0 + p.tile_s);
   const int kbeg = s0 & ~7;                    // 16-byte aligned first key
   const int nblk = (s1 - kbeg + KB - 1) / KB;
-  const uint16_t* __restrict__ kg = p.k + (int64_t)b * D * S;
-  const uint16_t* __restrict__ vg = p.v + (int64_t)b * S * D;
+  const int Dr = p.D;
+  const uint16_t* __restrict__ kg = p.k + (int64_t)b * Dr * S;
+  const uint16_t* __restrict__ vg = p.v + (int64_t)b * S * Dr;
 
   auto stK = [&](int s) { return (lds_char_t*)(smem + s * STAGE); };
   auto stV = [&](int s) { return (lds_char_t*)(smem + s * STAGE + K_BYTES); };
-  // ---- DMA of block `blk` into stage s (reads past S clamped; masked later)
+  // ---- DMA of block `blk` into stage s (reads past S clamped; masked
+  // later; Ks rows d >= Dr, eight to a copy, come from zeros; Vs chunks past
+  // Dr repeat the row's last chunk)
   auto issue = [&](int s, int blk) {
     const int kv0 = kbeg + blk * KB;
     const uint32_t lk = lds_addr(stK(s)), lv = lds_addr(stV(s));
@@ -175,19 +184,22 @@ __global__ void __launch_bounds__(256) decode_dma_kernel(DecodeParams p) {
       const int d = j * 8 + lane / 8;                   // Ks row
       const int c = (lane % 8) ^ dk_swz(d);
       const int key = min(kv0 + c * 8, S - 8);
-      dma_load16(kg + (int64_t)d * S + key, lk + j * 1024);
+      if (j * 8 < Dr)                                   // wave-uniform
+        dma_load16(kg + (int64_t)d * S + key, lk + j * 1024);
+      else
+        dma_load16(loom_zero_kb + lane * 4, lk + j * 1024);
     }
 #pragma unroll
     for (int i = 0; i < V_INSTR; ++i) {
       const int j = wave * V_INSTR + i;
       const int kr = j * V_ROWS_PER_I + lane / (D / 8); // Vs row (key)
-      const int c = (lane % (D / 8)) ^ dv_swz<D>(kr);
+      const int c = min((lane % (D / 8)) ^ dv_swz<D>(kr), Dr / 8 - 1);
       const int key = min(kv0 + kr, S - 1);
-      dma_load16(vg + (int64_t)key * D + c * 8, lv + j * 1024);
+      dma_load16(vg + (int64_t)key * Dr + c * 8, lv + j * 1024);
     }
   };
   // q[b] (32 head slots of the group, rows past its heads clamped to its
-  // last head and zeroed on read)
+  // last head and zeroed on read, as are the elements past Dr)
   // arrives by LDS DMA ahead of the first stages: a plain load would make the
   // compiler wait for every copy in flight before its first use
   lds_char_t* sq = (lds_char_t*)(smem + NS * STAGE);
@@ -196,7 +208,7 @@ __global__ void __launch_bounds__(256) decode_dma_kernel(DecodeParams p) {
     const int j = wave * Q_INSTR + i;
     const int e = j * 512 + lane * 8;                     // element of the [32][D] slots
     const int hq = h0 + min(e / D, Hl - 1);
-    dma_load16(p.q + ((int64_t)b * H + hq) * D + e % D, lds_addr(sq) + j * 1024);
+    dma_load16(p.q + ((int64_t)b * H + hq) * Dr + min(e % D, Dr - 8), lds_addr(sq) + j * 1024);
   }
 #pragma unroll
   for (int s = 0; s < NS - 1; ++s)
@@ -316,7 +328,7 @@ __global__ void __launch_bounds__(256) decode_dma_kernel(DecodeParams p) {
           for (int ds = 0; ds < DSTEPS; ++ds) {
             const u32x4_t raw = *reinterpret_cast<const __attribute__((address_space(3))) u32x4_t*>(
                 sq + (h * D + ds * 32 + g * 8) * 2);
-            qf[ds] = h < Hl ? raw : u32x4_t{0u, 0u, 0u, 0u};
+            qf[ds] = h < Hl && ds * 32 + g * 8 < Dr ? raw : u32x4_t{0u, 0u, 0u, 0u};
           }
         }
         if (it + NS - 1 < nblk) issue((s + NS - 1) % NS, it + NS - 1);
@@ -355,12 +367,12 @@ __global__ void __launch_bounds__(256) decode_dma_kernel(DecodeParams p) {
     const float L = l0 * f0 + l1 * f1;
     const float g0 = f0 / L, g1 = f1 / L;
     const int64_t row = ((int64_t)split * p.B + b) * H + h0 + hh;
-    f32x4_t* dst = reinterpret_cast<f32x4_t*>(p.o + row * D + d0);
+    f32x4_t* dst = reinterpret_cast<f32x4_t*>(p.o + row * Dr + d0);
 #pragma unroll
     for (int u = 0; u < DPT / 4; ++u) {
       const f32x4_t a = *reinterpret_cast<const f32x4_t*>(w0 + d0 + 4 * u);
       const f32x4_t c = *reinterpret_cast<const f32x4_t*>(w1 + d0 + 4 * u);
-      dst[u] = a * g0 + c * g1;
+      if (d0 + 4 * u < Dr) dst[u] = a * g0 + c * g1;
     }
     if (d0 == 0) p.lse[row] = (logf(L) + M * 0.69314718055994530942f);
   }
@@ -391,19 +403,21 @@ __global__ void __launch_bounds__(64 * kWaves) decode_split_kernel(DecodeParams 
   const int s1 = min(S, s0 + p.tile_s);
   const int nblk = (s1 - s0 + kBlockKeys - 1) / kBlockKeys;
 
-  const rsrc_t krs = make_rsrc(p.k + (int64_t)b * D * S, (uint32_t)(D * S * 2));
-  const rsrc_t vrs = make_rsrc(p.v + (int64_t)b * S * D, (uint32_t)(S * D * 2));
-  const uint16_t* __restrict__ qb = p.q + ((int64_t)b * H + h0) * D;
+  // K rows past Dr lie past the descriptor's range: they read as zeros
+  const int Dr = p.D;
+  const rsrc_t krs = make_rsrc(p.k + (int64_t)b * Dr * S, (uint32_t)(Dr * S * 2));
+  const rsrc_t vrs = make_rsrc(p.v + (int64_t)b * S * Dr, (uint32_t)(S * Dr * 2));
+  const uint16_t* __restrict__ qb = p.q + ((int64_t)b * H + h0) * Dr;
 
   // Q^T operands, shared by the waves through LDS: slot [ds][ht][lane]
   // holds q[h = r + 16 ht][32 ds + 8 g .. +7]
   __shared__ u32x4_t sm_q[DSTEPS][HT][64];
   for (int e = threadIdx.x; e < DSTEPS * HT * 64; e += 64 * kWaves) {
     const int ln = e & 63, ht = (e >> 6) % HT, ds = (e >> 6) / HT;
-    const int h = (ln & 15) + 16 * ht;
-    sm_q[ds][ht][ln] = h < Hl ? *reinterpret_cast<const u32x4_t*>(qb + (int64_t)h * D + ds * 32 +
-                                                                  (ln >> 4) * 8)
-                             : u32x4_t{0u, 0u, 0u, 0u};
+    const int h = (ln & 15) + 16 * ht, d0 = ds * 32 + (ln >> 4) * 8;
+    sm_q[ds][ht][ln] = h < Hl && d0 < Dr
+                           ? *reinterpret_cast<const u32x4_t*>(qb + (int64_t)h * Dr + d0)
+                           : u32x4_t{0u, 0u, 0u, 0u};
   }
   __syncthreads();
 
@@ -436,7 +450,7 @@ __global__ void __launch_bounds__(64 * kWaves) decode_split_kernel(DecodeParams 
 #pragma unroll
       for (int t = 0; t < 8; ++t) {
         const int key = base + 16 * g + 4 * (t & 3) + 2 * c + (t >> 2);
-        const uint32_t o = valid ? ((uint32_t)key * D + r * VEC) * 2 : kNone;
+        const uint32_t o = valid ? ((uint32_t)key * Dr + r * VEC) * 2 : kNone;
         if constexpr (VEC == 8) {
           buf[t] = buf_load16(vrs, o);
         } else {
@@ -586,8 +600,8 @@ __global__ void __launch_bounds__(64 * kWaves) decode_split_kernel(DecodeParams 
 
   // ---- merge the waves: (lse_s, o_s) for every (head, d) of this split
   const int64_t row0 = ((int64_t)split * p.B + b) * H + h0;
-  for (int e = threadIdx.x; e < Hl * D; e += 64 * kWaves) {
-    const int h = e / D, d = e % D;
+  for (int e = threadIdx.x; e < Hl * Dr; e += 64 * kWaves) {
+    const int h = e / Dr, d = e % Dr;
     float M = -INFINITY;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) M = fmaxf(M, sm_m[w][h]);
@@ -598,7 +612,7 @@ __global__ void __launch_bounds__(64 * kWaves) decode_split_kernel(DecodeParams 
       L += sm_l[w][h] * f;
       o += sm_acc[w][h * ACC_STRIDE + d] * f;
     }
-    p.o[(row0 + h) * D + d] = o / L;
+    p.o[(row0 + h) * Dr + d] = o / L;
     if (d == 0) p.lse[row0 + h] = logf(L) + M * 0.69314718055994530942f;
   }
 
@@ -637,8 +651,9 @@ int flash_decode_impl(const void* k, const void* v, const void* q, void* out,
   if (!(scale > 0.f) || !std::isfinite(scale))
     return loom_fail(err, errlen, LOOM_EINVAL,
                      "flash_decode: scale must be finite and positive (got %g)", (double)scale);
-  if (!(D == 64 || D == 128))
-    return loom_fail(err, errlen, LOOM_EUNSUP, "flash_decode: head_dim %lld not built (64, 128)",
+  if (D % 8 != 0 || D > 128)
+    return loom_fail(err, errlen, LOOM_EUNSUP,
+                     "flash_decode: head_dim %lld not built (a multiple of 8 up to 128)",
                      (long long)D);
   if (H > 32 * 65535)
     return loom_fail(err, errlen, LOOM_EINVAL, "flash_decode: too many query heads (got %lld)",
@@ -666,19 +681,22 @@ int flash_decode_impl(const void* k, const void* v, const void* q, void* out,
   p.S = (int)S;
   p.tile_s = (int)tile_s;
   p.ns = (int)ns;
+  p.D = (int)D;
   p.c2 = scale * 1.4426950408889634f;
   if (loom_validate_only()) return loom_ok(err, errlen);
   hipStream_t st = static_cast<hipStream_t>(stream);
+  // the kernels built for 64 or 128 (the next one up) run any narrower D
+  const bool d128 = D > 64;
   if (S % 8 == 0) {
     // LDS-DMA split kernel: K rows start on 16-byte boundaries
     const dim3 grid((unsigned)ns, (unsigned)B, (unsigned)cdiv64(H, 32)), block(256);
-    if (D == 128)
+    if (d128)
       hipLaunchKernelGGL((decode_dma_kernel<128, F16>), grid, block, 0, st, p);
     else
       hipLaunchKernelGGL((decode_dma_kernel<64, F16>), grid, block, 0, st, p);
   } else {
     const bool al = S % 4 == 0;
-    if (D == 128) {
+    if (d128) {
       if (H > 16) launch_split<128, 2, F16>(p, al, st); else launch_split<128, 1, F16>(p, al, st);
     } else {
       if (H > 16) launch_split<64, 2, F16>(p, al, st); else launch_split<64, 1, F16>(p, al, st);
@@ -687,13 +705,8 @@ int flash_decode_impl(const void* k, const void* v, const void* q, void* out,
   int rc = loom_check_launch(err, errlen, "flash_decode (split)");
   if (rc) return rc;
   const dim3 cgrid((unsigned)cdiv64(B * H * D / 2, 256)), cblock(256);
-  if (D == 128) {
-    if (p.ns <= 8) hipLaunchKernelGGL((decode_combine_kernel<128, F16, 8>), cgrid, cblock, 0, st, p);
-    else hipLaunchKernelGGL((decode_combine_kernel<128, F16, 16>), cgrid, cblock, 0, st, p);
-  } else {
-    if (p.ns <= 8) hipLaunchKernelGGL((decode_combine_kernel<64, F16, 8>), cgrid, cblock, 0, st, p);
-    else hipLaunchKernelGGL((decode_combine_kernel<64, F16, 16>), cgrid, cblock, 0, st, p);
-  }
+  if (p.ns <= 8) hipLaunchKernelGGL((decode_combine_kernel<F16, 8>), cgrid, cblock, 0, st, p);
+  else hipLaunchKernelGGL((decode_combine_kernel<F16, 16>), cgrid, cblock, 0, st, p);
   return loom_check_launch(err, errlen, "flash_decode (combine)");
 }
 

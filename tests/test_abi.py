@@ -173,9 +173,11 @@ def test_attention_rejections(lh):
     rc, msg = _call(lh, "loom_hip_attention", FAKE, FAKE, FAKE, FAKE, 4, 128, 64, 128, 0.1, 1,
                     1, 128, 64, None)
     assert rc == 1 and "causal" in msg
-    rc, msg = _call(lh, "loom_hip_attention", FAKE, FAKE, FAKE, FAKE, 4, 128, 128, 80, 0.1, 0,
-                    1, 128, 64, None)
-    assert rc == 2 and "head_dim" in msg
+    # any multiple of 8 up to 128 is built (on the 64 or 128 kernel); others are not
+    for bad in (100, 136, 256):
+        rc, msg = _call(lh, "loom_hip_attention", FAKE, FAKE, FAKE, FAKE, 4, 128, 128, bad, 0.1, 0,
+                        1, 128, 64, None)
+        assert rc == 2 and "head_dim" in msg, bad
     rc, msg = _call(lh, "loom_hip_attention", *base, 0.1, 0, 5, 128, 64, None)
     assert rc == 1  # tile_b > BH
 
@@ -188,9 +190,10 @@ def test_flash_decode_rejections(lh):
     rc, msg = _call(lh, "loom_hip_flash_decode", FAKE, FAKE, FAKE, FAKE, FAKE, need - 1,
                     B, H, D, S, 0.1, 1, ts, 64, None)
     assert rc == 1 and "workspace" in msg
-    rc, msg = _call(lh, "loom_hip_flash_decode", FAKE, FAKE, FAKE, FAKE, FAKE, need,
-                    B, H, 96, S, 0.1, 1, ts, 64, None)
-    assert rc == 2 and "head_dim" in msg
+    for bad in (100, 136):
+        rc, msg = _call(lh, "loom_hip_flash_decode", FAKE, FAKE, FAKE, FAKE, FAKE, need,
+                        B, H, bad, S, 0.1, 1, ts, 64, None)
+        assert rc == 2 and "head_dim" in msg, bad
     rc, msg = _call(lh, "loom_hip_flash_decode", FAKE, FAKE, FAKE, FAKE, FAKE, need,
                     B, H, D, S, 0.1, 1, S + 8, 64, None)
     assert rc == 1
@@ -212,7 +215,7 @@ def test_flash_decode_noalloc_rejections(lh):
                     1, 256, 64, None)
     assert rc == 1 and "scratch" in msg, (rc, msg)
     # the workspace form's own checks run first too
-    rc, msg = _call(lh, "loom_hip_flash_decode_noalloc", FAKE, FAKE, FAKE, FAKE, B, H, 96, S, 0.1,
+    rc, msg = _call(lh, "loom_hip_flash_decode_noalloc", FAKE, FAKE, FAKE, FAKE, B, H, 100, S, 0.1,
                     1, 1024, 64, None)
     assert rc == 2 and "head_dim" in msg, (rc, msg)
     rc, msg = _call(lh, "loom_hip_flash_decode_noalloc", FAKE, FAKE, FAKE, FAKE, B, H, D, S, -1.0,
