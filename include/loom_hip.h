@@ -112,8 +112,9 @@ int loom_hip_split_k_matmul_gather(const void* a, const void* b, void* out, void
  * tile_m (a multiple of 16 up to Sq, or Sq) runs as the smallest workgroup
  * query tile of 64, 128, 192, 256 covering it; tile_b (<= BH) and tile_n (<= Skv, the
  * online-softmax step) are validated, the kernel streams KV in 64-key LDS
- * blocks.  D a multiple of 8 up to 128 (built for 64 and 128; a narrower D
- * runs on the next one up with its padding rows zero); any Sq and Skv (Skv
+ * blocks.  D a multiple of 8 up to 256 (built for 64, 128 and 256; a
+ * narrower D runs on the next one up with its padding rows zero; above 128
+ * the query tiles are 64 or 128); any Sq and Skv (Skv
  * not a multiple of 8 stages K through registers instead of 16-byte LDS DMA,
  * and k then needs only 2-byte alignment). */
 int loom_hip_attention(const void* k, const void* v, const void* q, void* out, int64_t BH,
@@ -134,7 +135,8 @@ size_t loom_hip_flash_decode_workspace_bytes(int64_t B, int64_t H, int64_t D, in
  * [s*tile_s, (s+1)*tile_s); its (lse_s, o_s) land in the workspace, then a
  * second kernel performs the split-0 combine into out.  tile_b (<= B) and
  * tile_n (<= S) are validated and do not change the result.  D a multiple
- * of 8 up to 128 (built for 64 and 128, a narrower D runs on the next one up);
+ * of 8 up to 128, or up to 256 when S is a multiple of 8 (built for 64, 128
+ * and 256, a narrower D runs on the next one up);
  * any H (a workgroup serves up to 32 query heads, more heads take more
  * workgroups, each streaming the split's K and V).  scale must be finite and
  * positive (the running max is taken over raw scores before scaling). */

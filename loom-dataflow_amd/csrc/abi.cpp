@@ -568,28 +568,30 @@ int build_scope(const std::string& f, const int64_t* d, int nd, Scope& sc, std::
     sc.temp_iter.push_back(jop("Div", jc(d[2]), js("tile_k")));
   } else if (f == "attention") {
     if (!need(4)) return LOOM_HIP_EINVAL;
-    if (d[3] % 8 || d[3] > 128) {
-      err = "constraint_scope: attention is built for head_dim a multiple of 8 up to 128";
+    if (d[3] % 8 || d[3] > 256) {
+      err = "constraint_scope: attention is built for head_dim a multiple of 8 up to 256";
       return LOOM_HIP_EUNSUP;
     }
-    const long long dk = d[3] <= 64 ? 64 : 128;   // the kernel's (padded) head dim
+    // the kernel's (padded) head dim and its stages of 64-key K and V blocks
+    const long long dk = d[3] <= 64 ? 64 : d[3] <= 128 ? 128 : 256;
+    const long long nst = dk > 128 ? 2 : 4;
     sc.symbols.push_back(jsym("tile_b", d[0], 1));
     sc.symbols.push_back(jsym("tile_m", d[1], kTileAlign));
     sc.symbols.push_back(jsym("tile_n", d[2], 1));
     ub("tile_b", d[0]);
     tiled("tile_m", d[1]);
     ub("tile_n", d[2]);
-    // four stages of 64-key K and V blocks
-    sc.footprint.push_back(jc(4 * 64 * dk * 2));
-    sc.footprint.push_back(jc(4 * 64 * dk * 2));
+    sc.footprint.push_back(jc(nst * 64 * dk * 2));
+    sc.footprint.push_back(jc(nst * 64 * dk * 2));
     sc.hard.push_back(jop("Le", jop("Add", sc.footprint[0], sc.footprint[1]), jc(kLdsBytes)));
     sc.temp_iter.push_back(jop("Div", jc(d[0]), js("tile_b")));
     sc.temp_iter.push_back(jop("Div", jc(d[1]), js("tile_m")));
     sc.seq_iter = jop("Div", jc(d[2]), js("tile_n"));
   } else if (f == "flash_decode") {
     if (!need(4)) return LOOM_HIP_EINVAL;
-    if (d[2] % 8 || d[2] > 128) {
-      err = "constraint_scope: flash_decode is built for head_dim a multiple of 8 up to 128";
+    if (d[2] % 8 || d[2] > 256 || (d[2] > 128 && d[3] % 8)) {
+      err = "constraint_scope: flash_decode is built for head_dim a multiple of 8 up to 128, "
+            "or up to 256 when S is a multiple of 8";
       return LOOM_HIP_EUNSUP;
     }
     sc.symbols.push_back(jsym("tile_b", d[0], 1));
@@ -829,9 +831,10 @@ int loom_hip_preferred_block_sizes(const char* func, const int64_t* dims, int nd
     b["tile_k"] = std::min<long long>(d[2], ceil_div(ceil_div(d[2], S), step) * step);
   } else if (f == "attention") {
     b["tile_b"] = 1;
-    // 256 query rows, or the largest built tile within a shorter Sq (Sq
-    // itself below 64)
-    b["tile_m"] = d[1] >= 256 ? 256 : d[1] >= 192 ? 192 : d[1] >= 128 ? 128 : d[1] >= 64 ? 64 : d[1];
+    // 256 query rows (128 for head dims above 128), or the largest built
+    // tile within a shorter Sq (Sq itself below 64)
+    const long long top = d[3] > 128 ? 128 : 256;
+    b["tile_m"] = d[1] >= top ? top : d[1] >= 192 ? 192 : d[1] >= 128 ? 128 : d[1] >= 64 ? 64 : d[1];
     b["tile_n"] = std::min<long long>(64, d[2]);
   } else if (f == "flash_decode") {
     b["tile_b"] = 1;

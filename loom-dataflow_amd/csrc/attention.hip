@@ -9,10 +9,10 @@
 //   acc' = acc*alpha + P.V (:97-113); out = acc / l (:116-121).
 //   `causal` (absent from the reference) makes key j visible to query i
 //   only when j <= i; fully hidden KV blocks are skipped.
-//   Any head dim that is a multiple of 8 up to 128 runs on the kernel built
-//   for 64 or 128: the K rows past it are copied from zeros, the Q elements
-//   past it are zero, so the scores are exact; the V columns past it only
-//   reach O columns that are never stored.
+//   Any head dim that is a multiple of 8 up to 256 runs on the kernel built
+//   for 64, 128 or 256: the K rows past it are copied from zeros, the Q
+//   elements past it are zero, so the scores are exact; the V columns past it
+//   only reach O columns that are never stored.
 //
 // gfx950 mapping (attention_dma_kernel below): a workgroup of W waves owns
 // 16 QT W query rows of one (b, h) and streams K and V through LDS in
@@ -36,7 +36,8 @@ struct AttnParams {
 
 // ---------------------------------------------------------------------------
 // LDS-DMA variant: K and V blocks are copied global -> LDS unchanged
-// (global_load_lds_dwordx4, 4 stages of 64 keys), Ks [d][key] and Vs [key][d],
+// (global_load_lds_dwordx4, 4 stages of 64 keys, 2 at D 256), Ks [d][key] and
+// Vs [key][d],
 // and both operands that need k-contiguous data are built by
 // ds_read_b64_tr_b16:
 //   S^T[key, q]  = K^T . Q^T : row operand K^T from Ks (lane r gets key 16 jt + r,
@@ -60,10 +61,11 @@ struct AttnParams {
 // row bits 1 and 3 pick them (bit 0 only repeats the half's pattern).
 LOOM_DEV int k_swz(int d) { return (2 * (d & 3)) ^ (2 * ((d >> 3) & 1)); }
 // One pass of a V^T read covers 8 consecutive Vs rows, 32 bytes each.  D 128
-// (256-byte rows): all eight share a window position, row bits 0-2 pick the
-// pair.  D 64 (128-byte rows): rows r, r^2, r^4, r^6 share one, bits 1-2.
+// and 256 (rows of a multiple of 256 bytes): all eight share a window
+// position, row bits 0-2 pick the pair.  D 64 (128-byte rows): rows r, r^2,
+// r^4, r^6 share one, bits 1-2.
 template <int D>
-LOOM_DEV int v_swz(int k) { return D == 128 ? 2 * (k & 7) : 2 * ((k >> 1) & 3); }
+LOOM_DEV int v_swz(int k) { return D >= 128 ? 2 * (k & 7) : 2 * ((k >> 1) & 3); }
 
 // KREG (Skv not a multiple of 8): K rows [d][0..Skv) do not start on
 // 16-byte boundaries, so K cannot be copied by 16-byte LDS DMA.  Each lane
@@ -74,7 +76,8 @@ LOOM_DEV int v_swz(int k) { return D == 128 ? 2 * (k & 7) : 2 * ((k >> 1) & 3); 
 template <int D, int QT, int W, bool H, bool KREG>
 __global__ void __launch_bounds__(64 * W) attention_dma_kernel(AttnParams p) {
   constexpr int KB = 64;                        // keys per stage
-  constexpr int NS = 4;                         // stages
+  // stages: four of 32 KB (K and V) up to D 128; two of 64 KB at D 256
+  constexpr int NS = D > 128 ? 2 : 4;
   constexpr int BQ = 16 * QT * W;               // queries per workgroup
   constexpr int K_BYTES = D * KB * 2, V_BYTES = KB * D * 2;
   constexpr int K_INSTR = K_BYTES / 1024 / W;   // DMA instructions per wave per stage
@@ -85,10 +88,11 @@ __global__ void __launch_bounds__(64 * W) attention_dma_kernel(AttnParams p) {
   constexpr int V_ROWS_PER_I = 1024 / VROW;
   constexpr int DSTEPS = D / 32, DT = D / 16;
   static_assert(LPW * (NS - 2) <= 63, "vmcnt range");
+  constexpr int K_BYTES23 = NS > 2 ? K_BYTES : 16, V_BYTES23 = NS > 2 ? V_BYTES : 16;
   __shared__ __attribute__((aligned(1024))) char sK0[K_BYTES], sV0[V_BYTES];
   __shared__ __attribute__((aligned(1024))) char sK1[K_BYTES], sV1[V_BYTES];
-  __shared__ __attribute__((aligned(1024))) char sK2[K_BYTES], sV2[V_BYTES];
-  __shared__ __attribute__((aligned(1024))) char sK3[K_BYTES], sV3[V_BYTES];
+  __shared__ __attribute__((aligned(1024))) char sK2[K_BYTES23], sV2[V_BYTES23];
+  __shared__ __attribute__((aligned(1024))) char sK3[K_BYTES23], sV3[V_BYTES23];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -107,13 +111,13 @@ __global__ void __launch_bounds__(64 * W) attention_dma_kernel(AttnParams p) {
 
   auto stK = [&](int s) -> lds_char_t* {
     if (s == 0) return (lds_char_t*)sK0;
-    if (s == 1) return (lds_char_t*)sK1;
+    if (s == 1 || NS == 2) return (lds_char_t*)sK1;
     if (s == 2) return (lds_char_t*)sK2;
     return (lds_char_t*)sK3;
   };
   auto stV = [&](int s) -> lds_char_t* {
     if (s == 0) return (lds_char_t*)sV0;
-    if (s == 1) return (lds_char_t*)sV1;
+    if (s == 1 || NS == 2) return (lds_char_t*)sV1;
     if (s == 2) return (lds_char_t*)sV2;
     return (lds_char_t*)sV3;
   };
@@ -420,6 +424,11 @@ __global__ void __launch_bounds__(64 * W) attention_dma_kernel(AttnParams p) {
 template <bool H, bool KREG>
 void launch_attention(const AttnParams& p, int64_t D, int64_t tile_m, hipStream_t st) {
   const dim3 grid((unsigned)(p.BH * p.nqt)), b4(256), b8(512);
+  if (D == 256) {   // one 16-row query tile per wave: 64 or 128 queries
+    if (tile_m == 64) hipLaunchKernelGGL((attention_dma_kernel<256, 1, 4, H, KREG>), grid, b4, 0, st, p);
+    else hipLaunchKernelGGL((attention_dma_kernel<256, 1, 8, H, KREG>), grid, b8, 0, st, p);
+    return;
+  }
   switch ((D == 128 ? 10 : 0) + (int)(tile_m / 64)) {
     case 11: hipLaunchKernelGGL((attention_dma_kernel<128, 1, 4, H, KREG>), grid, b4, 0, st, p); break;
     case 12: hipLaunchKernelGGL((attention_dma_kernel<128, 1, 8, H, KREG>), grid, b8, 0, st, p); break;
@@ -449,10 +458,11 @@ int attention_impl(const void* k, const void* v, const void* q, void* out, int64
   if (causal && Sq != Skv)
     return loom_fail(err, errlen, LOOM_EINVAL, "attention: causal needs Sq == Skv");
   // tile_m is bounded by Sq (natural_ub) and runs on the smallest built
-  // query tile covering it (256 above); a query row's result does not depend
-  // on the workgroup that holds it
+  // query tile covering it (the largest above them: 256, or 128 for head dims
+  // above 128); a query row's result does not depend on the workgroup that
+  // holds it
   static const int64_t kQTiles[4] = {64, 128, 192, 256};
-  const int64_t wm = loom_fit_tile(tile_m, Sq, kQTiles, 4);
+  const int64_t wm = loom_fit_tile(tile_m, Sq, kQTiles, D > 128 ? 2 : 4);
   if (wm == 0)
     return loom_fail(err, errlen, LOOM_EINVAL,
                      "attention: tile_m=%lld exceeds its extent Sq=%lld (natural_ub)",
@@ -463,9 +473,9 @@ int attention_impl(const void* k, const void* v, const void* q, void* out, int64
                      "itself",
                      (long long)tile_m);
   tile_m = wm;
-  if (D % 8 != 0 || D > 128)
+  if (D % 8 != 0 || D > 256)
     return loom_fail(err, errlen, LOOM_EUNSUP,
-                     "attention: head_dim %lld not built (a multiple of 8 up to 128)",
+                     "attention: head_dim %lld not built (a multiple of 8 up to 256)",
                      (long long)D);
   // Skv not a multiple of 8 takes the register-staged K path (KREG), whose
   // K buffer descriptor addresses one (b, h)'s D x Skv keys in 32 bits
@@ -494,8 +504,8 @@ int attention_impl(const void* k, const void* v, const void* q, void* out, int64
   p.c2 = scale * 1.4426950408889634f;
   if (loom_validate_only()) return loom_ok(err, errlen);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  // the kernel built for 64 or 128 (the next one up) runs any narrower D
-  const int64_t Dk = D <= 64 ? 64 : 128;
+  // the kernel built for 64, 128 or 256 (the next one up) runs any narrower D
+  const int64_t Dk = D <= 64 ? 64 : D <= 128 ? 128 : 256;
   if (kreg) launch_attention<H, true>(p, Dk, tile_m, st);
   else launch_attention<H, false>(p, Dk, tile_m, st);
   return loom_check_launch(err, errlen, "attention");

@@ -25,7 +25,8 @@
 // through LDS into (lse_s, o_s), exactly the reference's gathered tensors;
 // decode_combine_kernel performs the split-0 combine.
 // Any head dim that is a multiple of 8 up to 128 runs on the kernels built
-// for 64 or 128: K rows and q elements past it are zeros (copied from zeros,
+// for 64 or 128, and up to 256 (S a multiple of 8) on the LDS-DMA kernel
+// built for 256: K rows and q elements past it are zeros (copied from zeros,
 // or read past the buffer range), so the scores are exact, and V columns
 // past it only reach O columns that are never stored.
 #include "common.h"
@@ -130,12 +131,12 @@ __global__ void __launch_bounds__(256) decode_combine_kernel(DecodeParams p) {
 // rows r, r^2, r^4, r^6.
 LOOM_DEV int dk_swz(int d) { return (2 * (d & 3)) ^ (2 * ((d >> 3) & 1)); }
 template <int D>
-LOOM_DEV int dv_swz(int k) { return D == 128 ? 2 * (k & 7) : 2 * ((k >> 1) & 3); }
+LOOM_DEV int dv_swz(int k) { return D >= 128 ? 2 * (k & 7) : 2 * ((k >> 1) & 3); }
 
 template <int D, bool F16>
 __global__ void __launch_bounds__(256) decode_dma_kernel(DecodeParams p) {
   constexpr int KB = 64;                       // keys per stage
-  constexpr int NS = 4;                        // stages
+  constexpr int NS = D > 128 ? 2 : 4;          // stages (64 KB each at D 256)
   constexpr int W = 4;
   constexpr int K_BYTES = D * KB * 2, V_BYTES = KB * D * 2;
   constexpr int K_INSTR = K_BYTES / 1024 / W, V_INSTR = V_BYTES / 1024 / W;
@@ -651,10 +652,15 @@ int flash_decode_impl(const void* k, const void* v, const void* q, void* out,
   if (!(scale > 0.f) || !std::isfinite(scale))
     return loom_fail(err, errlen, LOOM_EINVAL,
                      "flash_decode: scale must be finite and positive (got %g)", (double)scale);
-  if (D % 8 != 0 || D > 128)
+  if (D % 8 != 0 || D > 256)
     return loom_fail(err, errlen, LOOM_EUNSUP,
-                     "flash_decode: head_dim %lld not built (a multiple of 8 up to 128)",
+                     "flash_decode: head_dim %lld not built (a multiple of 8 up to 256)",
                      (long long)D);
+  if (D > 128 && S % 8 != 0)
+    return loom_fail(err, errlen, LOOM_EUNSUP,
+                     "flash_decode: head_dim %lld above 128 is built for S a multiple of 8 "
+                     "(got S=%lld)",
+                     (long long)D, (long long)S);
   if (H > 32 * 65535)
     return loom_fail(err, errlen, LOOM_EINVAL, "flash_decode: too many query heads (got %lld)",
                      (long long)H);
@@ -685,12 +691,14 @@ int flash_decode_impl(const void* k, const void* v, const void* q, void* out,
   p.c2 = scale * 1.4426950408889634f;
   if (loom_validate_only()) return loom_ok(err, errlen);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  // the kernels built for 64 or 128 (the next one up) run any narrower D
+  // the kernels built for 64, 128 or 256 (the next one up) run any narrower D
   const bool d128 = D > 64;
   if (S % 8 == 0) {
     // LDS-DMA split kernel: K rows start on 16-byte boundaries
     const dim3 grid((unsigned)ns, (unsigned)B, (unsigned)cdiv64(H, 32)), block(256);
-    if (d128)
+    if (D > 128)
+      hipLaunchKernelGGL((decode_dma_kernel<256, F16>), grid, block, 0, st, p);
+    else if (d128)
       hipLaunchKernelGGL((decode_dma_kernel<128, F16>), grid, block, 0, st, p);
     else
       hipLaunchKernelGGL((decode_dma_kernel<64, F16>), grid, block, 0, st, p);

@@ -173,8 +173,8 @@ def test_attention_rejections(lh):
     rc, msg = _call(lh, "loom_hip_attention", FAKE, FAKE, FAKE, FAKE, 4, 128, 64, 128, 0.1, 1,
                     1, 128, 64, None)
     assert rc == 1 and "causal" in msg
-    # any multiple of 8 up to 128 is built (on the 64 or 128 kernel); others are not
-    for bad in (100, 136, 256):
+    # any multiple of 8 up to 256 is built (on the 64, 128 or 256 kernel); others are not
+    for bad in (100, 264, 512):
         rc, msg = _call(lh, "loom_hip_attention", FAKE, FAKE, FAKE, FAKE, 4, 128, 128, bad, 0.1, 0,
                         1, 128, 64, None)
         assert rc == 2 and "head_dim" in msg, bad
@@ -190,10 +190,15 @@ def test_flash_decode_rejections(lh):
     rc, msg = _call(lh, "loom_hip_flash_decode", FAKE, FAKE, FAKE, FAKE, FAKE, need - 1,
                     B, H, D, S, 0.1, 1, ts, 64, None)
     assert rc == 1 and "workspace" in msg
-    for bad in (100, 136):
+    for bad in (100, 264):
         rc, msg = _call(lh, "loom_hip_flash_decode", FAKE, FAKE, FAKE, FAKE, FAKE, need,
                         B, H, bad, S, 0.1, 1, ts, 64, None)
         assert rc == 2 and "head_dim" in msg, bad
+    # above 128 the head dim needs S a multiple of 8 (the LDS-DMA kernel)
+    need2 = lh.flash_decode_workspace_bytes(B, H, 256, S - 1, ts)
+    rc, msg = _call(lh, "loom_hip_flash_decode", FAKE, FAKE, FAKE, FAKE, FAKE, need2,
+                    B, H, 256, S - 1, 0.1, 1, ts, 64, None)
+    assert rc == 2 and "multiple of 8" in msg, msg
     rc, msg = _call(lh, "loom_hip_flash_decode", FAKE, FAKE, FAKE, FAKE, FAKE, need,
                     B, H, D, S, 0.1, 1, S + 8, 64, None)
     assert rc == 1

@@ -57,9 +57,10 @@ CASES = {
     "batch_matmul": (["tile_b", "tile_m", "tile_n", "tile_k"], [(16, 2048, 2048, 2048), (2, 96, 80, 64)]),
     "split_k_matmul_gather": (["tile_m", "tile_n", "tile_k"], [(512, 512, 16384), (48, 96, 1000)]),
     "attention": (["tile_b", "tile_m", "tile_n"], [(128, 4096, 4096, 128), (3, 1000, 1000, 64),
-                                                   (2, 300, 300, 96)]),
+                                                   (2, 300, 300, 96), (2, 500, 500, 256)]),
     "flash_decode": (["tile_b", "tile_s", "tile_n"], [(32, 32, 128, 8192), (3, 5, 64, 1000),
-                                                       (2, 64, 128, 2048), (2, 8, 40, 1000)]),
+                                                       (2, 64, 128, 2048), (2, 8, 40, 1000),
+                                                       (2, 8, 256, 1000)]),
     "helion_mamba2_chunk_scan_kernel": (["tile_m", "tile_n", "tile_k", "tile_c", "tile_b", "tile_h"],
                                         [(4, 16, 32, 1, 256, 64, 128), (2, 8, 32, 4, 192, 160, 128)]),
 }
@@ -137,13 +138,17 @@ def test_scope_json_round_trips_into_block_sizes_json():
 
 
 def test_unsupported_shapes_and_functions():
-    for d in (100, 136):   # head_dim: a multiple of 8 up to 128
+    for d in (100, 264):   # head_dim: a multiple of 8 up to 256
         with pytest.raises(RuntimeError) as ei:
             loom_hip.constraint_scope("attention", (4, 128, 128, d))
         assert ei.value.code == 2
         with pytest.raises(RuntimeError) as ei:
             loom_hip.constraint_scope("flash_decode", (4, 8, d, 1024))
         assert ei.value.code == 2
+    with pytest.raises(RuntimeError) as ei:   # decode above 128 needs S % 8 == 0
+        loom_hip.constraint_scope("flash_decode", (4, 8, 136, 1001))
+    assert ei.value.code == 2
+    assert loom_hip.preferred_block_sizes("attention", (8, 4096, 4096, 256))["tile_m"] == 128
     with pytest.raises(RuntimeError) as ei:
         loom_hip.constraint_scope("conv2d", (1, 2, 3))
     assert ei.value.code == 2

@@ -1,10 +1,11 @@
-"""GPU parity at head dims other than the two built ones.
+"""GPU parity at head dims other than the built ones.
 
-attention and flash_decode are built for head_dim 64 and 128; any multiple of
-8 up to 128 runs on the next one up, with the K rows and q elements past the
-real head dim zero and the V columns past it reaching only O columns that are
-never stored.  Each case compares the whole output (and, for decode, the
-gathered split partials lse_s and o_s) with the CPU oracle, at the bars of
+attention and flash_decode are built for head_dim 64, 128 and 256 (decode
+above 128 for S a multiple of 8); any multiple of 8 up to 256 runs on the next
+one up, with the K rows and q elements past the real head dim zero and the V
+columns past it reaching only O columns that are never stored.  Each case
+compares the whole output (and, for decode, the gathered split partials
+lse_s and o_s) with the CPU oracle, at the bars of
 tests/test_gpu_parity.py, on both K staging paths (16-byte LDS DMA when the
 key count is a multiple of 8, registers otherwise) and in both 16-bit types.
 The out buffers are pre-filled with a sentinel so a store past the head dim
@@ -39,7 +40,8 @@ def _sentinel(shape, dtype):
 @pytest.mark.parametrize("BH,Sq,Skv,D,causal,tile_m", [
     (2, 200, 200, 8, True, 64), (1, 130, 517, 24, False, 128), (2, 300, 300, 40, True, 256),
     (1, 96, 1000, 56, False, 192), (2, 257, 257, 72, True, 256), (1, 64, 333, 96, False, 64),
-    (3, 190, 190, 96, True, 128), (1, 120, 640, 120, False, 256)])
+    (3, 190, 190, 96, True, 128), (1, 120, 640, 120, False, 256), (2, 300, 300, 256, True, 256),
+    (1, 200, 517, 256, False, 64), (2, 150, 640, 136, False, 128), (1, 333, 333, 200, True, 192)])
 def test_attention_head_dims(lh, BH, Sq, Skv, D, causal, tile_m):
     rng = np.random.default_rng(BH * 7 + Sq * 13 + Skv * 3 + D)
     k, v, q = rng_bf16(rng, (BH, D, Skv)), rng_bf16(rng, (BH, Skv, D)), rng_bf16(rng, (BH, Sq, D))
@@ -54,9 +56,10 @@ def test_attention_head_dims(lh, BH, Sq, Skv, D, causal, tile_m):
 
 
 def test_attention_head_dim_f16(lh):
-    """f16 at D 96 (the 128 kernel) and D 40 (the 64 kernel), one of them
-    with ragged Skv."""
-    for BH, Sq, Skv, D, causal in ((2, 160, 160, 96, True), (1, 70, 301, 40, False)):
+    """f16 at D 96 (the 128 kernel), D 40 (the 64 kernel, ragged Skv) and
+    D 256."""
+    for BH, Sq, Skv, D, causal in ((2, 160, 160, 96, True), (1, 70, 301, 40, False),
+                                   (2, 130, 130, 256, True)):
         rng = np.random.default_rng(Sq + D)
         k = to_f16(rng.standard_normal((BH, D, Skv)).astype(np.float32))
         v = to_f16(rng.standard_normal((BH, Skv, D)).astype(np.float32))
@@ -75,7 +78,8 @@ def test_attention_head_dim_f16(lh):
 
 @pytest.mark.parametrize("B,H,D,S,ts", [
     (2, 8, 8, 1024, 256), (3, 5, 40, 1000, 200), (2, 33, 72, 2048, 512), (1, 32, 96, 777, 128),
-    (4, 16, 96, 4096, 1024), (2, 3, 120, 1203, 300), (1, 40, 56, 640, 64)])
+    (4, 16, 96, 4096, 1024), (2, 3, 120, 1203, 300), (1, 40, 56, 640, 64), (2, 32, 256, 2048, 512),
+    (3, 37, 136, 1000, 200), (1, 8, 200, 640, 128)])
 def test_decode_head_dims(lh, B, H, D, S, ts):
     rng = np.random.default_rng(B * 5 + H * 11 + D * 3 + S)
     k, v, q = rng_bf16(rng, (B, D, S)), rng_bf16(rng, (B, S, D)), rng_bf16(rng, (B, H, D))
