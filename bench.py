@@ -361,7 +361,7 @@ def make_cases(torch, lh):
         return dict(fn=lambda i: lh.attention(*sets[i % n], causal=True, tile_m=256, tile_n=64),
                     flop=4 * BH * S * S * D // 2, bytes=nb, bound="mfma", sets=n,
                     desc="flashattn fwd B4 H32 S4096 D128 causal, tile_m 256", cpu=cpu,
-                    kernel="attention_dma_kernel<128, 2, 8, false>")
+                    kernel="attention_dma_kernel<128, 2, 8, false, false>")
     cases["flashattn"] = flashattn
 
     def decode():
