@@ -13,10 +13,10 @@
 // heads sharing the KV head give 32 FLOP per KV byte, which at 8 TB/s is
 // more arithmetic than the fp32 VALU peak, so S^T = K^T . Q^T and
 // O^T += V^T . P^T run on MFMA and the kernel stays bound by the stream.
-// One workgroup (4 waves) per (batch, split):
+// One workgroup (4 waves) per (batch, split, group of 32 query heads):
 //   - decode_dma_kernel (S a multiple of 8): K and V stream through
-//     a four-stage ring of LDS-DMA stages and reach the MFMAs by transposed
-//     LDS reads (described at the kernel);
+//     a ring of LDS-DMA stages (four, two at D 256) and reach the MFMAs by
+//     transposed LDS reads (described at the kernel);
 //   - decode_split_kernel (S not a multiple of 8): raw buffer loads straight into
 //     registers, MFMA operands built by register transposes (v_perm_b32),
 //     keys permuted inside a block and the permutation undone only where
@@ -101,12 +101,12 @@ __global__ void __launch_bounds__(256) decode_combine_kernel(DecodeParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// Split kernel, LDS-DMA form (the production path: S a multiple of 8,
-// H <= 32).  One workgroup of four waves per (batch, split).  K and V of the
-// split stream through LDS in 64-key stages copied by LDS DMA
-// (global_load_lds_dwordx4), four stages deep: up to 96 KB per workgroup in
-// flight with no registers held by loads, which is what streaming HBM at
-// full rate takes.  Ks is [d][key] and Vs [key][d], as the tensors lay them
+// Split kernel, LDS-DMA form (the production path: S a multiple of 8).  One
+// workgroup of four waves per (batch, split, group of up to 32 query heads).
+// K and V of the split stream through LDS in 64-key stages copied by LDS DMA
+// (global_load_lds_dwordx4), four stages deep up to D 128 (two 64 KB stages
+// at D 256): up to 96 KB per workgroup in flight with no registers held by
+// loads, which is what streaming HBM at full rate takes.  Ks is [d][key] and Vs [key][d], as the tensors lay them
 // out; the MFMA operands that need k-contiguous data come from
 // ds_read_b64_tr_b16:
 //   S^T[key, h]  = K^T . Q^T : row operand K^T from Ks (lane r: key, eight
