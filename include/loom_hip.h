@@ -135,8 +135,8 @@ size_t loom_hip_flash_decode_workspace_bytes(int64_t B, int64_t H, int64_t D, in
  * [s*tile_s, (s+1)*tile_s); its (lse_s, o_s) land in the workspace, then a
  * second kernel performs the split-0 combine into out.  tile_b (<= B) and
  * tile_n (<= S) are validated and do not change the result.  D a multiple
- * of 8 up to 128, or up to 256 when S is a multiple of 8 (built for 64, 128
- * and 256, a narrower D runs on the next one up);
+ * of 8 up to 256 (built for 64, 128 and 256, a narrower D runs on the next
+ * one up); any S;
  * any H (a workgroup serves up to 32 query heads, more heads take more
  * workgroups, each streaming the split's K and V).  scale must be finite and
  * positive (the running max is taken over raw scores before scaling). */

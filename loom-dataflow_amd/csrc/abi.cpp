@@ -589,9 +589,8 @@ int build_scope(const std::string& f, const int64_t* d, int nd, Scope& sc, std::
     sc.seq_iter = jop("Div", jc(d[2]), js("tile_n"));
   } else if (f == "flash_decode") {
     if (!need(4)) return LOOM_HIP_EINVAL;
-    if (d[2] % 8 || d[2] > 256 || (d[2] > 128 && d[3] % 8)) {
-      err = "constraint_scope: flash_decode is built for head_dim a multiple of 8 up to 128, "
-            "or up to 256 when S is a multiple of 8";
+    if (d[2] % 8 || d[2] > 256) {
+      err = "constraint_scope: flash_decode is built for head_dim a multiple of 8 up to 256";
       return LOOM_HIP_EUNSUP;
     }
     sc.symbols.push_back(jsym("tile_b", d[0], 1));

@@ -151,10 +151,9 @@ __global__ void __launch_bounds__(64 * W) attention_dma_kernel(AttnParams p) {
   };
 
   // ---- KREG: this lane's K pieces of block `blk` (the DMA's positions:
-  // row d, 8 keys from key) into registers, then into stage s
+  // row d, 8 keys from kv0 + 8 c) into registers (row_piece8), then into
+  // stage s; k needs only 2-byte alignment
   const rsrc_t krs = make_rsrc(kg, KREG ? (uint32_t)(Dr * Skv * 2) : 0u);
-  // buffer loads of 16 and 4 bytes need 4-byte aligned addresses (only
-  // 2-byte alignment is required of k on this path)
   const uint32_t kg_lo = (uint32_t)reinterpret_cast<uintptr_t>(kg);
   const bool k4 = (Skv & 1) == 0 && (kg_lo & 3u) == 0;   // every row 4-byte aligned
   u32x4_t kr[KREG ? K_INSTR : 1];
@@ -165,48 +164,8 @@ __global__ void __launch_bounds__(64 * W) attention_dma_kernel(AttnParams p) {
       const int j = wave * K_INSTR + i;
       const int d = j * 8 + lane / 8;
       const int c = (lane % 8) ^ k_swz(d);
-      if (j * 8 >= Dr) {                                  // padding rows: zeros
-        kr[i] = u32x4_t{0u, 0u, 0u, 0u};
-        continue;
-      }
-      // keys key .. key+7.  A piece inside the row at a 4-byte aligned
-      // address is one 16-byte load; at a 2-byte aligned one, a 16-byte and
-      // a 4-byte load from two bytes earlier, shifted into place (when the
-      // piece neither starts the tensor nor ends its row, so both loads stay
-      // inside the descriptor's range).  Other pieces reaching into the row
-      // take eight 2-byte loads (elements past the row are masked keys, and
-      // past the tensor the range check returns zeros); a piece wholly past
-      // Skv is masked.
-      const int key = kv0 + c * 8;
-      const uint32_t off = (uint32_t)(d * Skv + key) * 2;
-      const bool al = ((kg_lo + off) & 3u) == 0;
-      if (k4) {                                           // wave-uniform
-        kr[i] = key + 8 <= Skv ? buf_load16(krs, off) : u32x4_t{0u, 0u, 0u, 0u};
-        if (key < Skv && key + 8 > Skv) {
-          uint32_t h[8];
-#pragma unroll
-          for (int e = 0; e < 8; ++e) h[e] = buf_load2(krs, off + 2 * e);
-          kr[i] = u32x4_t{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
-                          h[6] | (h[7] << 16)};
-        }
-      } else if (key + 8 <= Skv && (al || (off >= 2 && key + 8 < Skv))) {
-        const uint32_t o4 = al ? off : off - 2;
-        const u32x4_t w = buf_load16(krs, o4);
-        const uint32_t x = buf_load4(krs, o4 + 16);
-        kr[i] = al ? w
-                   : u32x4_t{__builtin_amdgcn_alignbyte(w[1], w[0], 2),
-                             __builtin_amdgcn_alignbyte(w[2], w[1], 2),
-                             __builtin_amdgcn_alignbyte(w[3], w[2], 2),
-                             __builtin_amdgcn_alignbyte(x, w[3], 2)};
-      } else if (key < Skv) {
-        uint32_t h[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) h[e] = buf_load2(krs, off + 2 * e);
-        kr[i] = u32x4_t{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
-                        h[6] | (h[7] << 16)};
-      } else {
-        kr[i] = u32x4_t{0u, 0u, 0u, 0u};
-      }
+      kr[i] = j * 8 < Dr ? row_piece8(krs, kg_lo, Skv, d, kv0 + c * 8, k4)   // padding rows: zeros
+                         : u32x4_t{0u, 0u, 0u, 0u};
     }
   };
   auto kstore = [&](int s) {

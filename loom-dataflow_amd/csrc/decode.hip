@@ -14,10 +14,11 @@
 // more arithmetic than the fp32 VALU peak, so S^T = K^T . Q^T and
 // O^T += V^T . P^T run on MFMA and the kernel stays bound by the stream.
 // One workgroup (4 waves) per (batch, split, group of 32 query heads):
-//   - decode_dma_kernel (S a multiple of 8): K and V stream through
-//     a ring of LDS-DMA stages (four, two at D 256) and reach the MFMAs by
-//     transposed LDS reads (described at the kernel);
-//   - decode_split_kernel (S not a multiple of 8): raw buffer loads straight into
+//   - decode_dma_kernel (S a multiple of 8; with K staged through registers
+//     for S = 2 mod 4 and above D 128): K and V stream through a ring of
+//     LDS-DMA stages (four, two at D 256) and reach the MFMAs by transposed
+//     LDS reads (described at the kernel);
+//   - decode_split_kernel (other S, D up to 128): raw buffer loads straight into
 //     registers, MFMA operands built by register transposes (v_perm_b32),
 //     keys permuted inside a block and the permutation undone only where
 //     results are addressed (softmax and P.V do not depend on key order).
@@ -25,8 +26,7 @@
 // through LDS into (lse_s, o_s), exactly the reference's gathered tensors;
 // decode_combine_kernel performs the split-0 combine.
 // Any head dim that is a multiple of 8 up to 128 runs on the kernels built
-// for 64 or 128, and up to 256 (S a multiple of 8) on the LDS-DMA kernel
-// built for 256: K rows and q elements past it are zeros (copied from zeros,
+// for 64 or 128, and up to 256 on the LDS-DMA kernel built for 256: K rows and q elements past it are zeros (copied from zeros,
 // or read past the buffer range), so the scores are exact, and V columns
 // past it only reach O columns that are never stored.
 #include "common.h"
@@ -133,7 +133,12 @@ LOOM_DEV int dk_swz(int d) { return (2 * (d & 3)) ^ (2 * ((d >> 3) & 1)); }
 template <int D>
 LOOM_DEV int dv_swz(int k) { return D >= 128 ? 2 * (k & 7) : 2 * ((k >> 1) & 3); }
 
-template <int D, bool F16>
+// KREG (S not a multiple of 8): K rows [d][0..S) do not start on 16-byte
+// boundaries, so K cannot be copied by 16-byte LDS DMA.  Each lane then
+// loads its 16-byte pieces of a K block into registers (row_piece8), issued
+// before the block NS-1 stages ahead of the one being computed and written to
+// the DMA's LDS positions after that computation; V keeps its DMA.
+template <int D, bool F16, bool KREG>
 __global__ void __launch_bounds__(256) decode_dma_kernel(DecodeParams p) {
   constexpr int KB = 64;                       // keys per stage
   constexpr int NS = D > 128 ? 2 : 4;          // stages (64 KB each at D 256)
@@ -179,16 +184,18 @@ __global__ void __launch_bounds__(256) decode_dma_kernel(DecodeParams p) {
   auto issue = [&](int s, int blk) {
     const int kv0 = kbeg + blk * KB;
     const uint32_t lk = lds_addr(stK(s)), lv = lds_addr(stV(s));
+    if constexpr (!KREG) {
 #pragma unroll
-    for (int i = 0; i < K_INSTR; ++i) {
-      const int j = wave * K_INSTR + i;
-      const int d = j * 8 + lane / 8;                   // Ks row
-      const int c = (lane % 8) ^ dk_swz(d);
-      const int key = min(kv0 + c * 8, S - 8);
-      if (j * 8 < Dr)                                   // wave-uniform
-        dma_load16(kg + (int64_t)d * S + key, lk + j * 1024);
-      else
-        dma_load16(loom_zero_kb + lane * 4, lk + j * 1024);
+      for (int i = 0; i < K_INSTR; ++i) {
+        const int j = wave * K_INSTR + i;
+        const int d = j * 8 + lane / 8;                 // Ks row
+        const int c = (lane % 8) ^ dk_swz(d);
+        const int key = min(kv0 + c * 8, S - 8);
+        if (j * 8 < Dr)                                 // wave-uniform
+          dma_load16(kg + (int64_t)d * S + key, lk + j * 1024);
+        else
+          dma_load16(loom_zero_kb + lane * 4, lk + j * 1024);
+      }
     }
 #pragma unroll
     for (int i = 0; i < V_INSTR; ++i) {
@@ -199,6 +206,31 @@ __global__ void __launch_bounds__(256) decode_dma_kernel(DecodeParams p) {
       dma_load16(vg + (int64_t)key * Dr + c * 8, lv + j * 1024);
     }
   };
+  // ---- KREG: this lane's K pieces of block `blk` (the DMA's positions: row
+  // d, 8 keys from kv0 + 8 c) into registers, then into stage s.  Pieces
+  // past S read as zeros (their keys are masked); k needs 2-byte alignment.
+  const rsrc_t krs = make_rsrc(kg, KREG ? (uint32_t)(Dr * S * 2) : 0u);
+  const uint32_t kg_lo = (uint32_t)reinterpret_cast<uintptr_t>(kg);
+  const bool k4 = (S & 1) == 0 && (kg_lo & 3u) == 0;     // every row 4-byte aligned
+  u32x4_t kr[KREG ? K_INSTR : 1];
+  auto kload = [&](int blk) {
+    const int kv0 = kbeg + blk * KB;
+#pragma unroll
+    for (int i = 0; i < K_INSTR; ++i) {
+      const int j = wave * K_INSTR + i;
+      const int d = j * 8 + lane / 8;
+      const int c = (lane % 8) ^ dk_swz(d);
+      kr[i] = j * 8 < Dr ? row_piece8(krs, kg_lo, S, d, kv0 + c * 8, k4)   // padding rows: zeros
+                         : u32x4_t{0u, 0u, 0u, 0u};
+    }
+  };
+  auto kstore = [&](int s) {
+#pragma unroll
+    for (int i = 0; i < K_INSTR; ++i)
+      *reinterpret_cast<__attribute__((address_space(3))) u32x4_t*>(
+          stK(s) + (wave * K_INSTR + i) * 1024 + lane * 16) = kr[i];
+  };
+
   // q[b] (32 head slots of the group, rows past its heads clamped to its
   // last head and zeroed on read, as are the elements past Dr)
   // arrives by LDS DMA ahead of the first stages: a plain load would make the
@@ -213,7 +245,13 @@ __global__ void __launch_bounds__(256) decode_dma_kernel(DecodeParams p) {
   }
 #pragma unroll
   for (int s = 0; s < NS - 1; ++s)
-    if (s < nblk) issue(s, s);
+    if (s < nblk) {
+      if constexpr (KREG) {
+        kload(s);
+        kstore(s);
+      }
+      issue(s, s);
+    }
 
   // Q^T operand of this wave's head tile, q[b][16 ht + r][32 ds + 8 g ..],
   // read from LDS once the first stage has landed
@@ -322,6 +360,8 @@ __global__ void __launch_bounds__(256) decode_dma_kernel(DecodeParams p) {
         if (younger >= 2) LOOM_WAIT_VMCNT(2 * LPW);
         else if (younger == 1) LOOM_WAIT_VMCNT(LPW);
         else LOOM_WAIT_VMCNT(0);
+        // KREG: this wave's K stores of the previous iteration are in LDS
+        if constexpr (KREG) LOOM_WAIT_LGKM0();
         barrier_nofence();
         if (it == 0) {
           // q's copies were issued before stage 0's, so they have landed too
@@ -332,8 +372,18 @@ __global__ void __launch_bounds__(256) decode_dma_kernel(DecodeParams p) {
             qf[ds] = h < Hl && ds * 32 + g * 8 < Dr ? raw : u32x4_t{0u, 0u, 0u, 0u};
           }
         }
-        if (it + NS - 1 < nblk) issue((s + NS - 1) % NS, it + NS - 1);
+        const bool ahead = it + NS - 1 < nblk;
+        if constexpr (KREG) {
+          if (ahead) kload(it + NS - 1);
+        }
+        if (ahead) issue((s + NS - 1) % NS, it + NS - 1);
         compute(s, it);
+        // KREG: the stage written here was last read before this
+        // iteration's barrier (block it - 1); the compiler waits for the
+        // loads (and, since it cannot tell them apart, everything older)
+        if constexpr (KREG) {
+          if (ahead) kstore((s + NS - 1) % NS);
+        }
       }
     }
   }
@@ -656,11 +706,6 @@ int flash_decode_impl(const void* k, const void* v, const void* q, void* out,
     return loom_fail(err, errlen, LOOM_EUNSUP,
                      "flash_decode: head_dim %lld not built (a multiple of 8 up to 256)",
                      (long long)D);
-  if (D > 128 && S % 8 != 0)
-    return loom_fail(err, errlen, LOOM_EUNSUP,
-                     "flash_decode: head_dim %lld above 128 is built for S a multiple of 8 "
-                     "(got S=%lld)",
-                     (long long)D, (long long)S);
   if (H > 32 * 65535)
     return loom_fail(err, errlen, LOOM_EINVAL, "flash_decode: too many query heads (got %lld)",
                      (long long)H);
@@ -693,15 +738,24 @@ int flash_decode_impl(const void* k, const void* v, const void* q, void* out,
   hipStream_t st = static_cast<hipStream_t>(stream);
   // the kernels built for 64, 128 or 256 (the next one up) run any narrower D
   const bool d128 = D > 64;
-  if (S % 8 == 0) {
-    // LDS-DMA split kernel: K rows start on 16-byte boundaries
+  // S not a multiple of 8: the register kernel where it is faster (S odd,
+  // or a multiple of 4: B32 H32 D128 S 8191 59 against 65 us, S 8188 35
+  // against 46 us), the LDS-DMA kernel with K staged through registers
+  // (KREG) for S = 2 mod 4 (S 8190: 47 against 59 us) and above D 128,
+  // where the register kernel is not built
+  const bool kreg = S % 8 != 0;
+  if (!kreg || D > 128 || S % 4 == 2) {
     const dim3 grid((unsigned)ns, (unsigned)B, (unsigned)cdiv64(H, 32)), block(256);
-    if (D > 128)
-      hipLaunchKernelGGL((decode_dma_kernel<256, F16>), grid, block, 0, st, p);
-    else if (d128)
-      hipLaunchKernelGGL((decode_dma_kernel<128, F16>), grid, block, 0, st, p);
-    else
-      hipLaunchKernelGGL((decode_dma_kernel<64, F16>), grid, block, 0, st, p);
+    if (D > 128) {
+      if (kreg) hipLaunchKernelGGL((decode_dma_kernel<256, F16, true>), grid, block, 0, st, p);
+      else hipLaunchKernelGGL((decode_dma_kernel<256, F16, false>), grid, block, 0, st, p);
+    } else if (d128) {
+      if (kreg) hipLaunchKernelGGL((decode_dma_kernel<128, F16, true>), grid, block, 0, st, p);
+      else hipLaunchKernelGGL((decode_dma_kernel<128, F16, false>), grid, block, 0, st, p);
+    } else {
+      if (kreg) hipLaunchKernelGGL((decode_dma_kernel<64, F16, true>), grid, block, 0, st, p);
+      else hipLaunchKernelGGL((decode_dma_kernel<64, F16, false>), grid, block, 0, st, p);
+    }
   } else {
     const bool al = S % 4 == 0;
     if (d128) {

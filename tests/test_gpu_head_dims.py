@@ -1,13 +1,14 @@
 """GPU parity at head dims other than the built ones.
 
-attention and flash_decode are built for head_dim 64, 128 and 256 (decode
-above 128 for S a multiple of 8); any multiple of 8 up to 256 runs on the next
-one up, with the K rows and q elements past the real head dim zero and the V
+attention and flash_decode are built for head_dim 64, 128 and 256; any
+multiple of 8 up to 256 runs on the next one up, with the K rows and q elements past the real head dim zero and the V
 columns past it reaching only O columns that are never stored.  Each case
 compares the whole output (and, for decode, the gathered split partials
 lse_s and o_s) with the CPU oracle, at the bars of
-tests/test_gpu_parity.py, on both K staging paths (16-byte LDS DMA when the
-key count is a multiple of 8, registers otherwise) and in both 16-bit types.
+tests/test_gpu_parity.py, on every K staging path (16-byte LDS DMA when the
+key count is a multiple of 8, registers into LDS otherwise -- decode's
+LDS-DMA kernel does that for S = 2 mod 4 and above D 128, its register
+kernel for the other S) and in both 16-bit types.
 The out buffers are pre-filled with a sentinel so a store past the head dim
 into a neighbouring row would show.
 """
@@ -79,7 +80,8 @@ def test_attention_head_dim_f16(lh):
 @pytest.mark.parametrize("B,H,D,S,ts", [
     (2, 8, 8, 1024, 256), (3, 5, 40, 1000, 200), (2, 33, 72, 2048, 512), (1, 32, 96, 777, 128),
     (4, 16, 96, 4096, 1024), (2, 3, 120, 1203, 300), (1, 40, 56, 640, 64), (2, 32, 256, 2048, 512),
-    (3, 37, 136, 1000, 200), (1, 8, 200, 640, 128)])
+    (3, 37, 136, 1000, 200), (1, 8, 200, 640, 128), (2, 20, 256, 1001, 256), (1, 33, 200, 1002, 128),
+    (2, 32, 128, 2006, 512), (3, 7, 64, 998, 100), (2, 32, 128, 4099, 1024), (1, 17, 256, 1203, 300)])
 def test_decode_head_dims(lh, B, H, D, S, ts):
     rng = np.random.default_rng(B * 5 + H * 11 + D * 3 + S)
     k, v, q = rng_bf16(rng, (B, D, S)), rng_bf16(rng, (B, S, D)), rng_bf16(rng, (B, H, D))
@@ -97,8 +99,9 @@ def test_decode_head_dims(lh, B, H, D, S, ts):
 
 def test_decode_head_dim_noalloc_and_f16(lh):
     """The allocation-free entry point at D 72 (bit-identical to the
-    workspace form) and the f16 entry point at D 48 with S not a multiple
-    of 8."""
+    workspace form) and the f16 entry point with S not a multiple of 8 on
+    each ragged path: D 48 S 1001 (register kernel), D 128 S 1002 and D 256
+    S 777 (K staged through registers into the LDS-DMA kernel)."""
     rng = np.random.default_rng(4242)
     B, H, D, S = 2, 32, 72, 3000
     k, v, q = rng_bf16(rng, (B, D, S)), rng_bf16(rng, (B, S, D)), rng_bf16(rng, (B, H, D))
@@ -108,7 +111,11 @@ def test_decode_head_dim_noalloc_and_f16(lh):
     lh.flash_decode_noalloc(dev(k), dev(v), dev(q), out, tile_s=1000)
     assert torch.equal(out, ref)
 
-    B, H, D, S = 2, 12, 48, 1001
+    for B, H, D, S in ((2, 12, 48, 1001), (2, 32, 128, 1002), (1, 9, 256, 777)):
+        _decode_f16(lh, rng, B, H, D, S)
+
+
+def _decode_f16(lh, rng, B, H, D, S):
     k = to_f16(rng.standard_normal((B, D, S)).astype(np.float32))
     v = to_f16(rng.standard_normal((B, S, D)).astype(np.float32))
     q = to_f16(rng.standard_normal((B, H, D)).astype(np.float32))
