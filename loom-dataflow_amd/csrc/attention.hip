@@ -69,10 +69,11 @@ LOOM_DEV int v_swz(int k) { return D >= 128 ? 2 * (k & 7) : 2 * ((k >> 1) & 3); 
 
 // KREG (Skv not a multiple of 8): K rows [d][0..Skv) do not start on
 // 16-byte boundaries, so K cannot be copied by 16-byte LDS DMA.  Each lane
-// then loads its 16-byte piece of a K block into registers (one 16-byte
-// buffer load when Skv is even, eight 2-byte loads when it is odd), issued
-// before the block NS-1 stages ahead of the one being computed and written
-// to the same LDS position after that computation; V keeps its DMA.
+// then loads its 16-byte pieces of a K block into registers (row_piece8: one
+// 16-byte buffer load at any 2-byte aligned offset, 2-byte loads where a
+// piece reaches past its row), issued before the block NS-1 stages ahead of
+// the one being computed and written to the same LDS position after that
+// computation; V keeps its DMA.
 template <int D, int QT, int W, bool H, bool KREG>
 __global__ void __launch_bounds__(64 * W) attention_dma_kernel(AttnParams p) {
   constexpr int KB = 64;                        // keys per stage
@@ -154,8 +155,6 @@ __global__ void __launch_bounds__(64 * W) attention_dma_kernel(AttnParams p) {
   // row d, 8 keys from kv0 + 8 c) into registers (row_piece8), then into
   // stage s; k needs only 2-byte alignment
   const rsrc_t krs = make_rsrc(kg, KREG ? (uint32_t)(Dr * Skv * 2) : 0u);
-  const uint32_t kg_lo = (uint32_t)reinterpret_cast<uintptr_t>(kg);
-  const bool k4 = (Skv & 1) == 0 && (kg_lo & 3u) == 0;   // every row 4-byte aligned
   u32x4_t kr[KREG ? K_INSTR : 1];
   auto kload = [&](int blk) {
     const int kv0 = blk * KB;
@@ -164,7 +163,7 @@ __global__ void __launch_bounds__(64 * W) attention_dma_kernel(AttnParams p) {
       const int j = wave * K_INSTR + i;
       const int d = j * 8 + lane / 8;
       const int c = (lane % 8) ^ k_swz(d);
-      kr[i] = j * 8 < Dr ? row_piece8(krs, kg_lo, Skv, d, kv0 + c * 8, k4)   // padding rows: zeros
+      kr[i] = j * 8 < Dr ? row_piece8(krs, Skv, d, kv0 + c * 8)   // padding rows: zeros
                          : u32x4_t{0u, 0u, 0u, 0u};
     }
   };

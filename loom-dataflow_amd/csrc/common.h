@@ -270,46 +270,24 @@ LOOM_DEV uint32_t buf_load2(rsrc_t r, uint32_t off) {
 
 // Elements key .. key+7 of row d of a [rows][n] tensor of 16-bit values
 // whose rows need not start on 16-byte boundaries (n not a multiple of 8),
-// through the buffer descriptor r over the whole tensor (base address low
-// bits base_lo; n * rows * 2 < 2^31).  Buffer loads of 16 and 4 bytes need
-// 4-byte aligned addresses, 2-byte loads only 2-byte aligned ones.  all4
-// (wave-uniform) says every row starts 4-byte aligned (n even, base 4-byte
-// aligned): a piece inside the row is then one 16-byte load.  Otherwise a
-// piece at a 4-byte aligned address is one 16-byte load, at a 2-byte aligned
-// one a 16-byte and a 4-byte load from two bytes earlier shifted into place
-// (when the piece neither starts the tensor nor ends its row, so both loads
-// stay inside the descriptor's range).  A piece reaching past the row's end
-// takes eight 2-byte loads (the elements past the row are the next row's,
-// past the tensor the range check returns zeros); a piece wholly past the
-// row is zero.
-LOOM_DEV u32x4_t row_piece8(rsrc_t r, uint32_t base_lo, int n, int d, int key, bool all4) {
+// through the buffer descriptor r over the whole tensor (n * rows * 2 <
+// 2^31).  A piece inside its row is one 16-byte load at whatever 2-byte
+// aligned offset it starts: ROCm's driver runs every GPU process in the
+// unaligned access mode (SH_MEM_CONFIG.alignment_mode UNALIGNED), where
+// dword and wider loads take any byte address.  A load reaching past the
+// buffer's range returns zeros whole, so a piece that reaches past its row's
+// end (past the tensor for the last row) takes one 2-byte load per element
+// (the elements past the row are the next row's, past the tensor zeros); a
+// piece wholly past the row is zero.
+LOOM_DEV u32x4_t row_piece8(rsrc_t r, int n, int d, int key) {
   const uint32_t off = (uint32_t)(d * n + key) * 2;
-  const u32x4_t zero = u32x4_t{0u, 0u, 0u, 0u};
-  auto halves = [&]() {
-    uint32_t h[8];
+  if (key + 8 <= n) return buf_load16(r, off);
+  if (key >= n) return u32x4_t{0u, 0u, 0u, 0u};
+  uint32_t h[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) h[e] = buf_load2(r, off + 2 * e);
-    return u32x4_t{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
-                   h[6] | (h[7] << 16)};
-  };
-  if (all4) {
-    u32x4_t v = key + 8 <= n ? buf_load16(r, off) : zero;
-    if (key < n && key + 8 > n) v = halves();
-    return v;
-  }
-  const bool al = ((base_lo + off) & 3u) == 0;
-  if (key + 8 <= n && (al || (off >= 2 && key + 8 < n))) {
-    const uint32_t o4 = al ? off : off - 2;
-    const u32x4_t w = buf_load16(r, o4);
-    const uint32_t x = buf_load4(r, o4 + 16);
-    return al ? w
-              : u32x4_t{__builtin_amdgcn_alignbyte(w[1], w[0], 2),
-                        __builtin_amdgcn_alignbyte(w[2], w[1], 2),
-                        __builtin_amdgcn_alignbyte(w[3], w[2], 2),
-                        __builtin_amdgcn_alignbyte(x, w[3], 2)};
-  }
-  if (key < n) return halves();
-  return zero;
+  for (int e = 0; e < 8; ++e) h[e] = buf_load2(r, off + 2 * e);
+  return u32x4_t{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
+                 h[6] | (h[7] << 16)};
 }
 
 LOOM_DEV float wave_max(float v) {

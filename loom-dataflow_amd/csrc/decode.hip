@@ -14,10 +14,10 @@
 // more arithmetic than the fp32 VALU peak, so S^T = K^T . Q^T and
 // O^T += V^T . P^T run on MFMA and the kernel stays bound by the stream.
 // One workgroup (4 waves) per (batch, split, group of 32 query heads):
-//   - decode_dma_kernel (S a multiple of 8; with K staged through registers
-//     for S = 2 mod 4 and above D 128): K and V stream through a ring of
-//     LDS-DMA stages (four, two at D 256) and reach the MFMAs by transposed
-//     LDS reads (described at the kernel);
+//   - decode_dma_kernel (S a multiple of 8, or any S above D 128 with K
+//     staged through registers): K and V stream through a ring of LDS-DMA
+//     stages (four, two at D 256) and reach the MFMAs by transposed LDS
+//     reads (described at the kernel);
 //   - decode_split_kernel (other S, D up to 128): raw buffer loads straight into
 //     registers, MFMA operands built by register transposes (v_perm_b32),
 //     keys permuted inside a block and the permutation undone only where
@@ -26,9 +26,10 @@
 // through LDS into (lse_s, o_s), exactly the reference's gathered tensors;
 // decode_combine_kernel performs the split-0 combine.
 // Any head dim that is a multiple of 8 up to 128 runs on the kernels built
-// for 64 or 128, and up to 256 on the LDS-DMA kernel built for 256: K rows and q elements past it are zeros (copied from zeros,
-// or read past the buffer range), so the scores are exact, and V columns
-// past it only reach O columns that are never stored.
+// for 64 or 128, and up to 256 on the LDS-DMA kernel built for 256: K rows
+// and q elements past it are zeros (copied from zeros, or read past the
+// buffer range), so the scores are exact, and V columns past it only reach O
+// columns that are never stored.
 #include "common.h"
 
 #include <cmath>
@@ -210,8 +211,6 @@ __global__ void __launch_bounds__(256) decode_dma_kernel(DecodeParams p) {
   // d, 8 keys from kv0 + 8 c) into registers, then into stage s.  Pieces
   // past S read as zeros (their keys are masked); k needs 2-byte alignment.
   const rsrc_t krs = make_rsrc(kg, KREG ? (uint32_t)(Dr * S * 2) : 0u);
-  const uint32_t kg_lo = (uint32_t)reinterpret_cast<uintptr_t>(kg);
-  const bool k4 = (S & 1) == 0 && (kg_lo & 3u) == 0;     // every row 4-byte aligned
   u32x4_t kr[KREG ? K_INSTR : 1];
   auto kload = [&](int blk) {
     const int kv0 = kbeg + blk * KB;
@@ -220,7 +219,7 @@ __global__ void __launch_bounds__(256) decode_dma_kernel(DecodeParams p) {
       const int j = wave * K_INSTR + i;
       const int d = j * 8 + lane / 8;
       const int c = (lane % 8) ^ dk_swz(d);
-      kr[i] = j * 8 < Dr ? row_piece8(krs, kg_lo, S, d, kv0 + c * 8, k4)   // padding rows: zeros
+      kr[i] = j * 8 < Dr ? row_piece8(krs, S, d, kv0 + c * 8)   // padding rows: zeros
                          : u32x4_t{0u, 0u, 0u, 0u};
     }
   };
@@ -429,7 +428,16 @@ __global__ void __launch_bounds__(256) decode_dma_kernel(DecodeParams p) {
   }
 }
 
-template <int D, int HT, bool ALIGNED, bool F16>
+// K rows start at 2-byte granularity here (S not a multiple of 8), and each
+// lane's four keys of a row are one 8-byte buffer load at a 2-, 4- or 8-byte
+// aligned offset.  That relies on the unaligned access mode ROCm's driver
+// sets for every GPU process (SH_MEM_CONFIG.alignment_mode UNALIGNED: dword
+// and wider loads take any byte address); the parity tests at odd S and odd
+// tile_s pin it.  A load reaching past the buffer's range returns zeros
+// whole, valid bytes included, so rows that can hold K's last keys keep one
+// 2-byte load per key (tests/test_gpu_head_dims.py puts the deciding keys
+// there).
+template <int D, int HT, bool F16>
 __global__ void __launch_bounds__(64 * kWaves) decode_split_kernel(DecodeParams p) {
   constexpr int VEC = D / 16;     // d values per lane per V row, also # of d tiles
   constexpr int DSTEPS = D / 32;  // 32-deep MFMA steps over d
@@ -485,10 +493,13 @@ __global__ void __launch_bounds__(64 * kWaves) decode_split_kernel(DecodeParams 
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const uint32_t o = valid ? off + (uint32_t)(e * S) * 2 : kNone;
-        if constexpr (ALIGNED) {
+        if (e < 7) {
           const u32x2_t w = buf_load8(krs, o);
           buf[e] = u32x4_t{w[0], w[1], 0u, 0u};
         } else {
+          // rows 8 m + 7 hold the last row of K (D is a multiple of 8),
+          // whose pieces can reach past the tensor's end: a load that does
+          // returns zeros whole, so these take one 2-byte load per key
           uint32_t h[4];
 #pragma unroll
           for (int x = 0; x < 4; ++x) h[x] = buf_load2(krs, o + 2 * x);
@@ -670,12 +681,9 @@ __global__ void __launch_bounds__(64 * kWaves) decode_split_kernel(DecodeParams 
 }
 
 template <int D, int HT, bool F16>
-void launch_split(const DecodeParams& p, bool aligned, hipStream_t st) {
+void launch_split(const DecodeParams& p, hipStream_t st) {
   const dim3 grid(p.ns, p.B, (p.H + 31) / 32), block(64 * kWaves);
-  if (aligned)
-    hipLaunchKernelGGL((decode_split_kernel<D, HT, true, F16>), grid, block, 0, st, p);
-  else
-    hipLaunchKernelGGL((decode_split_kernel<D, HT, false, F16>), grid, block, 0, st, p);
+  hipLaunchKernelGGL((decode_split_kernel<D, HT, F16>), grid, block, 0, st, p);
 }
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -738,13 +746,12 @@ int flash_decode_impl(const void* k, const void* v, const void* q, void* out,
   hipStream_t st = static_cast<hipStream_t>(stream);
   // the kernels built for 64, 128 or 256 (the next one up) run any narrower D
   const bool d128 = D > 64;
-  // S not a multiple of 8: the register kernel where it is faster (S odd,
-  // or a multiple of 4: B32 H32 D128 S 8191 59 against 65 us, S 8188 35
-  // against 46 us), the LDS-DMA kernel with K staged through registers
-  // (KREG) for S = 2 mod 4 (S 8190: 47 against 59 us) and above D 128,
-  // where the register kernel is not built
+  // S not a multiple of 8: the register kernel up to D 128 (B32 H32 D128
+  // S 8190: 35 us against 47 with K staged through registers into the
+  // LDS-DMA kernel), that KREG form above D 128, where the register kernel
+  // is not built
   const bool kreg = S % 8 != 0;
-  if (!kreg || D > 128 || S % 4 == 2) {
+  if (!kreg || D > 128) {
     const dim3 grid((unsigned)ns, (unsigned)B, (unsigned)cdiv64(H, 32)), block(256);
     if (D > 128) {
       if (kreg) hipLaunchKernelGGL((decode_dma_kernel<256, F16, true>), grid, block, 0, st, p);
@@ -757,11 +764,10 @@ int flash_decode_impl(const void* k, const void* v, const void* q, void* out,
       else hipLaunchKernelGGL((decode_dma_kernel<64, F16, false>), grid, block, 0, st, p);
     }
   } else {
-    const bool al = S % 4 == 0;
     if (d128) {
-      if (H > 16) launch_split<128, 2, F16>(p, al, st); else launch_split<128, 1, F16>(p, al, st);
+      if (H > 16) launch_split<128, 2, F16>(p, st); else launch_split<128, 1, F16>(p, st);
     } else {
-      if (H > 16) launch_split<64, 2, F16>(p, al, st); else launch_split<64, 1, F16>(p, al, st);
+      if (H > 16) launch_split<64, 2, F16>(p, st); else launch_split<64, 1, F16>(p, st);
     }
   }
   int rc = loom_check_launch(err, errlen, "flash_decode (split)");

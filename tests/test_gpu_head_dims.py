@@ -19,7 +19,7 @@ import pytest
 import torch
 
 import oracle
-from oracle import from_bf16, from_f16, to_f16
+from oracle import from_bf16, from_f16, to_bf16, to_f16
 from tests.conftest import assert_close
 from tests.test_gpu_parity import ATTN_TOL, dev, host, rng_bf16
 
@@ -127,3 +127,27 @@ def _decode_f16(lh, rng, B, H, D, S):
         ref, _, _ = oracle.flash_decode(k, v, q, 1 / math.sqrt(D), 1, 256, 64)
     got = from_f16(out.view(torch.int16).cpu().numpy().view(np.uint16))
     assert_close(got, from_f16(ref), **ATTN_TOL, what=f"decode f16 D{D}")
+
+
+@pytest.mark.parametrize("D,S,ts", [(128, 1001, 256), (128, 1002, 1002), (64, 999, 100),
+                                     (128, 1004, 101), (256, 1001, 512), (96, 1003, 333)])
+def test_decode_keys_at_the_tensor_end(lh, D, S, ts):
+    """The last keys of K's last row (d = D - 1 of the last batch) decide the
+    output: they carry a large value that q's last element multiplies, so a
+    load of them that straddled the end of the tensor and came back zero
+    would shift the softmax to other keys.  Odd S, S = 2 mod 4 and S = 0 mod
+    4 with an odd tile_s put 8-byte pieces across the end; D 96 pads."""
+    rng = np.random.default_rng(D * 7 + S)
+    B, H = 2, 8
+    kf = rng.standard_normal((B, D, S)).astype(np.float32) * 0.1
+    kf[:, D - 1, S - 3:] = 12.0
+    qf = rng.standard_normal((B, H, D)).astype(np.float32) * 0.1
+    qf[:, :, D - 1] = 4.0
+    k, q = to_bf16(kf), to_bf16(qf)
+    v = rng_bf16(rng, (B, S, D))
+    scale = 1 / math.sqrt(D)
+    print(f"decode tensor end B{B} H{H} D{D} S{S} tile_s {ts}", flush=True)
+    got = lh.flash_decode(dev(k), dev(v), dev(q), scale=scale, tile_s=ts)
+    ref, _, _ = oracle.flash_decode(k, v, q, scale, 1, ts, min(64, ts))
+    assert_close(from_bf16(host(got)), from_bf16(ref), **ATTN_TOL,
+                 what=f"decode tensor end D{D} S{S} ts{ts}")
