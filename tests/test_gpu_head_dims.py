@@ -151,3 +151,42 @@ def test_decode_keys_at_the_tensor_end(lh, D, S, ts):
     ref, _, _ = oracle.flash_decode(k, v, q, scale, 1, ts, min(64, ts))
     assert_close(from_bf16(host(got)), from_bf16(ref), **ATTN_TOL,
                  what=f"decode tensor end D{D} S{S} ts{ts}")
+
+
+DRAWS = np.random.default_rng(20261203)
+
+
+@pytest.mark.parametrize("B,H,D,S,ts", [
+    (int(DRAWS.integers(1, 4)), int(DRAWS.integers(1, 70)), int(8 * DRAWS.integers(1, 33)),
+     int(s), int(DRAWS.integers(1, s + 1))) for s in DRAWS.integers(1, 3000, 10)])
+def test_decode_random_head_dims(lh, B, H, D, S, ts):
+    """Seeded draws over the whole built space: D any multiple of 8 up to
+    256, any S (every split path), any H (head groups past 32), any tile_s;
+    output and partials against the oracle."""
+    rng = np.random.default_rng(B + H * 3 + D * 5 + S * 7 + ts)
+    k, v, q = rng_bf16(rng, (B, D, S)), rng_bf16(rng, (B, S, D)), rng_bf16(rng, (B, H, D))
+    scale = 1 / math.sqrt(D)
+    print(f"decode random B{B} H{H} D{D} S{S} tile_s {ts}", flush=True)
+    got, lse, o = lh.flash_decode(dev(k), dev(v), dev(q), scale=scale, tile_s=ts,
+                                  tile_n=min(ts, 64), return_partials=True)
+    ref, ref_lse, ref_o = oracle.flash_decode(k, v, q, scale, 1, ts, min(64, ts))
+    what = f"decode random B{B} H{H} D{D} S{S} tile_s {ts}"
+    assert_close(from_bf16(host(got)), from_bf16(ref), **ATTN_TOL, what=what)
+    assert_close(lse.cpu().numpy(), ref_lse, atol=1e-2, rtol=1e-3, what=what + " lse_s")
+    assert_close(o.cpu().numpy(), ref_o, **ATTN_TOL, what=what + " o_s")
+
+
+@pytest.mark.parametrize("BH,Sq,Skv,D,causal", [
+    (int(DRAWS.integers(1, 4)), int(sq), int(sq) if c else int(DRAWS.integers(1, 900)),
+     int(8 * DRAWS.integers(1, 33)), bool(c))
+    for sq, c in zip(DRAWS.integers(1, 900, 8), [1, 0, 1, 0, 1, 0, 1, 0])])
+def test_attention_random_head_dims(lh, BH, Sq, Skv, D, causal):
+    """Seeded draws: D any multiple of 8 up to 256, any Sq and Skv (both K
+    paths), causal and not, against the oracle."""
+    rng = np.random.default_rng(BH + Sq * 3 + Skv * 5 + D * 7)
+    k, v, q = rng_bf16(rng, (BH, D, Skv)), rng_bf16(rng, (BH, Skv, D)), rng_bf16(rng, (BH, Sq, D))
+    print(f"attention random BH{BH} Sq{Sq} Skv{Skv} D{D} causal={causal}", flush=True)
+    got = lh.attention(dev(k), dev(v), dev(q), causal=causal)
+    ref = from_bf16(oracle.attention(k, v, q, 1 / math.sqrt(D), causal, 1, 64, 64))
+    assert_close(from_bf16(host(got)), ref, **ATTN_TOL,
+                 what=f"attention random BH{BH} Sq{Sq} Skv{Skv} D{D} causal={causal}")
