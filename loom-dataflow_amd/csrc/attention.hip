@@ -31,6 +31,7 @@ struct AttnParams {
   uint16_t* out;
   int BH, Sq, Skv, causal, nqt;
   int D;     // head dim: a multiple of 8, at most the kernel's D
+  int koff32;  // D * Skv * 2 < 2^32: K's per-lane DMA offsets fit 32 bits
   float c2;  // scale * log2(e)
 };
 
@@ -124,10 +125,40 @@ __global__ void __launch_bounds__(64 * W) attention_dma_kernel(AttnParams p) {
   };
   // ---- DMA of block `blk` into stage s (keys past Skv are clamped: masked
   // later; Ks rows d >= Dr, eight to a copy, come from zeros; Vs chunks past
-  // Dr repeat the row's last chunk)
+  // Dr repeat the row's last chunk).  A whole block inside [0, Skv) takes
+  // each copy as the block's scalar base plus this lane's byte offset, both
+  // computed once (no VALU per copy); the last, partial block clamps every
+  // lane's key (and K offsets past 32 bits always do).
+  uint32_t koff[K_INSTR], voff[V_INSTR];
+#pragma unroll
+  for (int i = 0; i < K_INSTR; ++i) {
+    const int j = wave * K_INSTR + i, d = j * 8 + lane / 8;
+    koff[i] = (uint32_t)(d * Skv + ((lane % 8) ^ k_swz(d)) * 8) * 2;
+  }
+#pragma unroll
+  for (int i = 0; i < V_INSTR; ++i) {
+    const int j = wave * V_INSTR + i, kr = j * V_ROWS_PER_I + lane / (D / 8);
+    voff[i] = (uint32_t)(kr * Dr + min((lane % (D / 8)) ^ v_swz<D>(kr), Dr / 8 - 1) * 8) * 2;
+  }
   auto issue = [&](int s, int blk) {
     const int kv0 = blk * KB;
     const uint32_t lk = lds_addr(stK(s)), lv = lds_addr(stV(s));
+    if (kv0 + KB <= Skv && (KREG || p.koff32)) {               // wave-uniform
+      if constexpr (!KREG) {
+#pragma unroll
+        for (int i = 0; i < K_INSTR; ++i) {
+          const int j = wave * K_INSTR + i;
+          if (j * 8 < Dr)
+            dma_load16_s(koff[i], kg + kv0, lk + j * 1024);
+          else
+            dma_load16(loom_zero_kb + lane * 4, lk + j * 1024);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < V_INSTR; ++i)
+        dma_load16_s(voff[i], vg + (int64_t)kv0 * Dr, lv + (wave * V_INSTR + i) * 1024);
+      return;
+    }
     if constexpr (!KREG) {
 #pragma unroll
       for (int i = 0; i < K_INSTR; ++i) {
@@ -209,12 +240,16 @@ __global__ void __launch_bounds__(64 * W) attention_dma_kernel(AttnParams p) {
 
   // running base m (log2 domain) per query row; O^T and the row sums l (an
   // MFMA of P^T against ones: every row of that tile holds l) share it
+  // negm[qt] holds -m in all four lanes of a quad: the accumulator every
+  // score tile starts from, kept across blocks and rebuilt only when m moves
   float m_run[QT];
+  f32x4_t negm[QT];
   f32x4_t ot[DT][QT], lacc[QT];
   const u32x4_t ones = u32x4_t{kOnePair<H>, kOnePair<H>, kOnePair<H>, kOnePair<H>};
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
     m_run[qt] = 0.f;
+    negm[qt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     lacc[qt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) ot[dt][qt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
@@ -235,8 +270,7 @@ __global__ void __launch_bounds__(64 * W) attention_dma_kernel(AttnParams p) {
 #pragma unroll
       for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int qt = 0; qt < QT; ++qt)
-          st[j][qt] = f32x4_t{-m_run[qt], -m_run[qt], -m_run[qt], -m_run[qt]};
+        for (int qt = 0; qt < QT; ++qt) st[j][qt] = negm[qt];
 #pragma unroll
       for (int ds = 0; ds < DSTEPS; ++ds) {
 #pragma unroll
@@ -298,6 +332,7 @@ __global__ void __launch_bounds__(64 * W) attention_dma_kernel(AttnParams p) {
             for (int dt = 0; dt < DT; ++dt) ot[dt][qt] *= alpha;
           }
           m_run[qt] += shift;
+          negm[qt] = f32x4_t{-m_run[qt], -m_run[qt], -m_run[qt], -m_run[qt]};
 #pragma unroll
           for (int j = 0; j < 2; ++j) st[j][qt] -= shift;
         }
@@ -459,6 +494,7 @@ int attention_impl(const void* k, const void* v, const void* q, void* out, int64
   p.causal = causal ? 1 : 0;
   p.nqt = (int)cdiv64(Sq, tile_m);
   p.D = (int)D;
+  p.koff32 = loom_prod_le({D, Skv, 2}, 0xffffffffll) ? 1 : 0;
   p.c2 = scale * 1.4426950408889634f;
   if (loom_validate_only()) return loom_ok(err, errlen);
   hipStream_t st = static_cast<hipStream_t>(stream);
