@@ -34,6 +34,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
                        [--no-ceilings] [--kernels all|none|mm,bmm,...]
        python bench.py --profile-workload all|mm,bmm,...   (for rocprofv3 --pmc)
        python bench.py --library-baselines   (PyTorch / hipBLASLt / SDPA on the same shapes)
+       python bench.py --reference-signatures   (each example at the reference's f16 shapes)
 """
 import argparse
 import json
@@ -79,6 +80,9 @@ def parse():
                          "torch.matmul / torch.bmm (hipBLASLt) for mm, bmm and the split-K "
                          "shape, scaled_dot_product_attention for flashattn (causal) and "
                          "mqa_decode (enable_gqa, one KV head); one JSON line")
+    ap.add_argument("--reference-signatures", action="store_true",
+                    help="only time each example at the reference's own f16 signature "
+                         "(and emitted bindings); one JSON line")
     return ap.parse_args()
 
 
@@ -126,6 +130,72 @@ def library_baselines(torch, iters=30):
     out["mqa_decode"] = {"library": "scaled_dot_product_attention, flash backend, enable_gqa",
                          "ms": round(ms, 5), "gbs": round(2 * Bd * Sd * D * 2 / ms / 1e6, 1)}
     out["mamba_chunk_scan"] = out["mamba_prologue"] = None   # no library implementation here
+    return out
+
+
+def reference_signatures(torch, lh, iters=20):
+    """Each example at the reference's own f16 signature (SURVEY A.1's left
+    column: examples/*/IR/00_from_helion_frontend.mlir), split-K and mqa at
+    the bindings the reference emitted (tile_k512 tile_m64 tile_n32;
+    tile_s512 tile_n512), timed as the kernel table's ms_graph (replayed
+    calls, checked bit-identical to an eager call).  One set of inputs per
+    case, so operands that fit stay cache resident."""
+    h = torch.float16
+    g = torch.Generator(device="cuda")
+    g.manual_seed(11)
+
+    def rn(*shape, std=1.0):
+        return (torch.randn(*shape, generator=g, device="cuda") * std).to(h)
+
+    def run(name, fn, work, unit):
+        case = {"fn": fn}
+        settle(torch, fn, 50)
+        ms = graph_ms(torch, case, iters) or time_back_to_back(torch, fn, iters)
+        rate = work / ms / 1e9 if unit == "TFLOP/s" else work / ms / 1e6
+        return {name: {"ms": round(ms, 5), "tflops" if unit == "TFLOP/s" else "gbs": round(rate, 1)}}
+
+    out = {}
+    x, y = rn(2048, 256), rn(256, 256)
+    mo = torch.empty(2048, 256, dtype=h, device="cuda")
+    out.update(run("mm 2048x256 . 256x256", lambda i: lh.matmul(x, y, mo), 2 * 2048 * 256 * 256,
+                   "TFLOP/s"))
+    a, b = rn(8, 4096, 512, std=0.05), rn(8, 512, 4096, std=0.05)
+    bo = torch.empty(8, 4096, 4096, dtype=h, device="cuda")
+    out.update(run("bmm 8x4096x512 . 8x512x4096", lambda i: lh.batch_matmul(a, b, bo),
+                   2 * 8 * 4096 * 4096 * 512, "TFLOP/s"))
+    del a, b, bo
+    sa, sb = rn(512, 4096, std=0.05), rn(4096, 512, std=0.05)
+    so = torch.empty(512, 512, dtype=h, device="cuda")
+    sg = torch.empty(8, 512, 512, dtype=torch.float32, device="cuda")
+    out.update(run("split-K 512x4096 . 4096x512, tile_k512 tile_m64 tile_n32",
+                   lambda i: lh.split_k_matmul_gather(sa, sb, so, sg, tile_m=64, tile_n=32,
+                                                      tile_k=512),
+                   2 * (512 * 4096 * 2) + 2 * (8 * 512 * 512 * 4) + 512 * 512 * 2, "GB/s"))
+    k, v, q = rn(32, 128, 4096), rn(32, 4096, 128), rn(32, 4096, 128)
+    ao = torch.empty(32, 4096, 128, dtype=h, device="cuda")
+    out.update(run("flashattn BH32 S4096 D128, non-causal",
+                   lambda i: lh.attention(k, v, q, ao, scale=0.08837890625, causal=False),
+                   4 * 32 * 4096 * 4096 * 128, "TFLOP/s"))
+    del k, v, q, ao
+    kd, vd, qd = rn(16, 128, 8192), rn(16, 8192, 128), rn(16, 32, 128)
+    do = torch.empty(16, 32, 128, dtype=h, device="cuda")
+    ws = lh.flash_decode_workspace(16, 32, 128, 8192, 512, "cuda")
+    out.update(run("mqa B16 H32 D128 S8192, tile_s512 tile_n512",
+                   lambda i: lh.flash_decode(kd, vd, qd, do, ws, scale=0.08837890625, tile_s=512,
+                                             tile_n=512),
+                   2 * 16 * 8192 * 128 * 2 + 16 * 32 * 128 * 4, "GB/s"))
+    b_, H, G, nc, Q, P, N = 2, 32, 4, 8, 192, 160, 128
+    L = nc * Q
+    cb, xm, C = rn(b_, nc, G, Q, Q, std=0.1), rn(b_, H, L, P), rn(b_, G, L, N, std=0.1)
+    dt = (torch.rand(b_, H, nc, Q, generator=g, device="cuda") * 0.1).to(h)
+    dA = (-(torch.rand(b_, H, nc, Q, generator=g, device="cuda") * 0.05).cumsum(-1)).to(h)
+    Dh, pv = rn(H), rn(b_, nc, H, N, P, std=0.1)
+    mo2 = torch.empty(b_, H, L, P, dtype=h, device="cuda")
+    byts = 2 * sum(t.numel() for t in (cb, xm, dt, dA, C, pv, mo2))
+    out.update(run("mamba chunk scan b2 L1536 h32 P160 N128 g4 Q192",
+                   lambda i: lh.helion_mamba2_chunk_scan_kernel(cb, xm, dt, dA, C, Dh, pv, mo2,
+                                                                tile_m=192, tile_n=64),
+                   byts, "GB/s"))
     return out
 
 
@@ -593,6 +663,11 @@ def main():
     torch.cuda.set_device(0)
     print(f"# device: {torch.cuda.get_device_name(0)}; {lh.__version__}", file=sys.stderr,
           flush=True)
+
+    if args.reference_signatures:
+        print(json.dumps({"reference_signatures": reference_signatures(torch, lh),
+                          "dtype": "f16", "device": torch.cuda.get_device_name(0)}), flush=True)
+        return
 
     if args.library_baselines:
         print(json.dumps({"library_baselines": library_baselines(torch),
