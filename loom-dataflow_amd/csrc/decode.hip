@@ -14,11 +14,12 @@
 // more arithmetic than the fp32 VALU peak, so S^T = K^T . Q^T and
 // O^T += V^T . P^T run on MFMA and the kernel stays bound by the stream.
 // One workgroup (4 waves) per (batch, split, group of 32 query heads):
-//   - decode_dma_kernel (S a multiple of 8, or any S above D 128 with K
-//     staged through registers): K and V stream through a ring of LDS-DMA
-//     stages (four, two at D 256) and reach the MFMAs by transposed LDS
-//     reads (described at the kernel);
-//   - decode_split_kernel (other S, D up to 128): raw buffer loads straight into
+//   - decode_dma_kernel (S a multiple of 8, or any S above D 128 or 32
+//     heads with K staged through registers; 4 waves for up to 32 heads, 8
+//     for 64): K and V stream through a ring of LDS-DMA stages (four, two at
+//     D 256) and reach the MFMAs by transposed LDS reads (described at the
+//     kernel);
+//   - decode_split_kernel (other S, up to 32 heads and D 128): raw buffer loads straight into
 //     registers, MFMA operands built by register transposes (v_perm_b32),
 //     keys permuted inside a block and the permutation undone only where
 //     results are addressed (softmax and P.V do not depend on key order).
@@ -116,8 +117,9 @@ __global__ void __launch_bounds__(256) decode_combine_kernel(DecodeParams p) {
 //                              4 g + 0..3 and 16 + 4 g + 0..3 of a 32-key half),
 //                              the keys P^T holds in lane group g.
 // Wave w takes the 32-key half kh = w & 1 of every stage for the heads of
-// tile ht = w >> 1 (16 heads; 32 head slots in all, slots past H are zero
-// queries and never stored), with an online softmax of its own in the log2
+// tile ht = w >> 1 (16 heads; 8 W head slots in all -- 32 with four waves,
+// 64 with eight, which serve more heads per pass over K and V -- slots past
+// H are zero queries and never stored), with an online softmax of its own in the log2
 // domain whose base only moves when a score rises 8 above it (P <= 2^8; the
 // row sum is an MFMA of the same bf16 P against ones, so numerator and
 // denominator see identical weights).  At the end the two halves of each
@@ -139,11 +141,11 @@ LOOM_DEV int dv_swz(int k) { return D >= 128 ? 2 * (k & 7) : 2 * ((k >> 1) & 3);
 // loads its 16-byte pieces of a K block into registers (row_piece8), issued
 // before the block NS-1 stages ahead of the one being computed and written to
 // the DMA's LDS positions after that computation; V keeps its DMA.
-template <int D, bool F16, bool KREG>
-__global__ void __launch_bounds__(256) decode_dma_kernel(DecodeParams p) {
+template <int D, bool F16, bool KREG, int W>
+__global__ void __launch_bounds__(64 * W) decode_dma_kernel(DecodeParams p) {
   constexpr int KB = 64;                       // keys per stage
   constexpr int NS = D > 128 ? 2 : 4;          // stages (64 KB each at D 256)
-  constexpr int W = 4;
+  constexpr int HS = 8 * W;                    // head slots (16 per pair of waves)
   constexpr int K_BYTES = D * KB * 2, V_BYTES = KB * D * 2;
   constexpr int K_INSTR = K_BYTES / 1024 / W, V_INSTR = V_BYTES / 1024 / W;
   constexpr int LPW = K_INSTR + V_INSTR;       // DMA instructions per wave per stage
@@ -153,8 +155,10 @@ __global__ void __launch_bounds__(256) decode_dma_kernel(DecodeParams p) {
   constexpr int STAGE = K_BYTES + V_BYTES;
   constexpr int ROW = D + 4;                   // merge row: D o values, m, l (16-byte rows)
   constexpr int MERGE = W * 16 * ROW * 4;      // per wave: 16 heads
-  static_assert(MERGE <= NS * STAGE, "merge area fits the stage ring");
-  constexpr int Q_BYTES = 32 * D * 2;          // 32 head slots of q
+  constexpr int Q_BYTES = HS * D * 2;          // the head slots of q
+  // the merge reuses the stage ring and, past it, the q slots (read into
+  // registers at the first block)
+  static_assert(MERGE <= NS * STAGE + Q_BYTES, "merge area fits the LDS");
   constexpr int Q_INSTR = Q_BYTES / 1024 / W;
   __shared__ __attribute__((aligned(1024))) char smem[NS * STAGE + Q_BYTES];
 
@@ -167,8 +171,8 @@ __global__ void __launch_bounds__(256) decode_dma_kernel(DecodeParams p) {
 
   const int split = blockIdx.x, b = blockIdx.y;
   const int H = p.H, S = p.S;
-  // head group blockIdx.z: query heads h0 .. h0 + Hl - 1 (32 head slots)
-  const int h0 = (int)blockIdx.z * 32, Hl = min(32, H - h0);
+  // head group blockIdx.z: query heads h0 .. h0 + Hl - 1 (HS head slots)
+  const int h0 = (int)blockIdx.z * HS, Hl = min(HS, H - h0);
   const int s0 = split * p.tile_s;
   const int s1 = min(S, s0 + p.tile_s);
   const int kbeg = s0 & ~7;                    // 16-byte aligned first key
@@ -230,15 +234,15 @@ __global__ void __launch_bounds__(256) decode_dma_kernel(DecodeParams p) {
           stK(s) + (wave * K_INSTR + i) * 1024 + lane * 16) = kr[i];
   };
 
-  // q[b] (32 head slots of the group, rows past its heads clamped to its
-  // last head and zeroed on read, as are the elements past Dr)
+  // q[b] (the group's head slots, rows past its heads clamped to its last
+  // head and zeroed on read, as are the elements past Dr)
   // arrives by LDS DMA ahead of the first stages: a plain load would make the
   // compiler wait for every copy in flight before its first use
   lds_char_t* sq = (lds_char_t*)(smem + NS * STAGE);
 #pragma unroll
   for (int i = 0; i < Q_INSTR; ++i) {
     const int j = wave * Q_INSTR + i;
-    const int e = j * 512 + lane * 8;                     // element of the [32][D] slots
+    const int e = j * 512 + lane * 8;                     // element of the [HS][D] slots
     const int hq = h0 + min(e / D, Hl - 1);
     dma_load16(p.q + ((int64_t)b * H + hq) * Dr + min(e % D, Dr - 8), lds_addr(sq) + j * 1024);
   }
@@ -686,6 +690,19 @@ void launch_split(const DecodeParams& p, hipStream_t st) {
   hipLaunchKernelGGL((decode_split_kernel<D, HT, F16>), grid, block, 0, st, p);
 }
 
+template <int D, bool F16>
+void launch_dma(const DecodeParams& p, bool kreg, bool wide, hipStream_t st) {
+  const int hs = wide ? 64 : 32;
+  const dim3 grid((unsigned)p.ns, (unsigned)p.B, (unsigned)((p.H + hs - 1) / hs));
+  if (wide) {
+    if (kreg) hipLaunchKernelGGL((decode_dma_kernel<D, F16, true, 8>), grid, dim3(512), 0, st, p);
+    else hipLaunchKernelGGL((decode_dma_kernel<D, F16, false, 8>), grid, dim3(512), 0, st, p);
+  } else {
+    if (kreg) hipLaunchKernelGGL((decode_dma_kernel<D, F16, true, 4>), grid, dim3(256), 0, st, p);
+    else hipLaunchKernelGGL((decode_dma_kernel<D, F16, false, 4>), grid, dim3(256), 0, st, p);
+  }
+}
+
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 
@@ -746,23 +763,20 @@ int flash_decode_impl(const void* k, const void* v, const void* q, void* out,
   hipStream_t st = static_cast<hipStream_t>(stream);
   // the kernels built for 64, 128 or 256 (the next one up) run any narrower D
   const bool d128 = D > 64;
-  // S not a multiple of 8: the register kernel up to D 128 (B32 H32 D128
-  // S 8190: 35 us against 47 with K staged through registers into the
-  // LDS-DMA kernel), that KREG form above D 128, where the register kernel
-  // is not built
+  // More than 32 query heads: 8-wave workgroups of 64 heads, so K and V are
+  // streamed once per 64 heads, not per 32 (B32 H48 D128 S8192: 33.2 us
+  // against 52.2).  S not a multiple of 8: the register kernel up to 32
+  // heads and D 128 (B32 H32 D128 S8190: 35 us against 47 with K staged
+  // through registers into the LDS-DMA kernel); that KREG form for more
+  // heads (H48 S8191: 38.9 us against the register kernel's 60.1, which
+  // takes 32 heads per pass) and above D 128, where the register kernel is
+  // not built
   const bool kreg = S % 8 != 0;
-  if (!kreg || D > 128) {
-    const dim3 grid((unsigned)ns, (unsigned)B, (unsigned)cdiv64(H, 32)), block(256);
-    if (D > 128) {
-      if (kreg) hipLaunchKernelGGL((decode_dma_kernel<256, F16, true>), grid, block, 0, st, p);
-      else hipLaunchKernelGGL((decode_dma_kernel<256, F16, false>), grid, block, 0, st, p);
-    } else if (d128) {
-      if (kreg) hipLaunchKernelGGL((decode_dma_kernel<128, F16, true>), grid, block, 0, st, p);
-      else hipLaunchKernelGGL((decode_dma_kernel<128, F16, false>), grid, block, 0, st, p);
-    } else {
-      if (kreg) hipLaunchKernelGGL((decode_dma_kernel<64, F16, true>), grid, block, 0, st, p);
-      else hipLaunchKernelGGL((decode_dma_kernel<64, F16, false>), grid, block, 0, st, p);
-    }
+  const bool wide = H > 32;
+  if (!kreg || D > 128 || wide) {
+    if (D > 128) launch_dma<256, F16>(p, kreg, wide, st);
+    else if (d128) launch_dma<128, F16>(p, kreg, wide, st);
+    else launch_dma<64, F16>(p, kreg, wide, st);
   } else {
     if (d128) {
       if (H > 16) launch_split<128, 2, F16>(p, st); else launch_split<128, 1, F16>(p, st);
