@@ -133,7 +133,8 @@ __global__ void __launch_bounds__(64 * W) attention_dma_kernel(AttnParams p) {
 #pragma unroll
   for (int i = 0; i < K_INSTR; ++i) {
     const int j = wave * K_INSTR + i, d = j * 8 + lane / 8;
-    koff[i] = (uint32_t)(d * Skv + ((lane % 8) ^ k_swz(d)) * 8) * 2;
+    // unsigned: it wraps (and goes unused, koff32 == 0) when D * Skv * 2 >= 2^32
+    koff[i] = ((uint32_t)d * (uint32_t)Skv + (uint32_t)(((lane % 8) ^ k_swz(d)) * 8)) * 2u;
   }
 #pragma unroll
   for (int i = 0; i < V_INSTR; ++i) {
