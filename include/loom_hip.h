@@ -424,6 +424,15 @@ int loom_hip_dispatch(const char* variant, void* const* tensors, int ntensors,
                       const int64_t* dims, int ndims, float scale, int causal, void* workspace,
                       size_t workspace_bytes, void* stream, char* err, size_t errlen);
 
+/* Bytes of the workspace loom_hip_dispatch needs for `variant` at `dims`
+ * (the extents loom_hip_dispatch takes): split-K's fp32 partials (as
+ * loom_hip_split_k_workspace_bytes at the name's tile_k), decode's
+ * (lse_s, o_s) (as loom_hip_flash_decode_workspace_bytes at its tile_s), 0
+ * for the other functions.  The generic form of the two per-function
+ * queries, for a caller that holds only the materialized name. */
+int loom_hip_workspace_bytes(const char* variant, const int64_t* dims, int ndims,
+                             size_t* bytes, char* err, size_t errlen);
+
 /* loom_hip_dispatch for variants whose 16-bit tensors are f16 (the
  * reference's own element type): launches the *_f16 entry points. */
 int loom_hip_dispatch_f16(const char* variant, void* const* tensors, int ntensors,

@@ -950,6 +950,42 @@ int loom_hip_parse_variant(const char* variant, char* func, size_t funclen, int6
   return LOOM_HIP_OK;
 }
 
+int loom_hip_workspace_bytes(const char* variant, const int64_t* dims, int ndims,
+                             size_t* bytes, char* err, size_t errlen) {
+  if (!variant || !bytes || (ndims > 0 && !dims))
+    return fail(err, errlen, LOOM_HIP_EINVAL, "workspace_bytes: null argument");
+  std::string f, perr;
+  int64_t t[LOOM_HIP_NTILES];
+  int rc = parse_variant(variant, f, t, perr);
+  if (rc) return fail(err, errlen, rc, "workspace_bytes: %s", perr.c_str());
+  if (!known_function(f))
+    return fail(err, errlen, LOOM_HIP_EUNSUP,
+                "workspace_bytes: no gfx950 kernel for function '%s'", f.c_str());
+  const int nd = f == "split_k_matmul_gather" || f == "matmul" ? 3
+                 : f == "helion_mamba2_chunk_scan_kernel" ? 7 : 4;
+  if (ndims != nd)
+    return fail(err, errlen, LOOM_HIP_EINVAL, "workspace_bytes: %s takes %d extents (got %d)",
+                f.c_str(), nd, ndims);
+  for (int i = 0; i < nd; ++i)
+    if (dims[i] <= 0)
+      return fail(err, errlen, LOOM_HIP_EINVAL, "workspace_bytes: extents must be positive");
+  size_t n = 0;
+  if (f == "split_k_matmul_gather") {
+    if ((rc = need_tiles(f, t, {3}, err, errlen))) return rc;
+    n = loom_hip_split_k_workspace_bytes(dims[0], dims[1], dims[2], t[LOOM_HIP_TILE_K]);
+  } else if (f == "flash_decode") {
+    if ((rc = need_tiles(f, t, {4}, err, errlen))) return rc;
+    n = loom_hip_flash_decode_workspace_bytes(dims[0], dims[1], dims[2], dims[3],
+                                              t[LOOM_HIP_TILE_S]);
+  }
+  if (n == SIZE_MAX)
+    return fail(err, errlen, LOOM_HIP_EINVAL, "workspace_bytes: %s workspace too large",
+                f.c_str());
+  *bytes = n;
+  if (err && errlen) err[0] = '\0';
+  return LOOM_HIP_OK;
+}
+
 int loom_hip_dispatch(const char* variant, void* const* tensors, int ntensors,
                       const int64_t* dims, int ndims, float scale, int causal,
                       void* workspace, size_t workspace_bytes, void* stream, char* err,

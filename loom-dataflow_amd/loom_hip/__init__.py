@@ -83,6 +83,9 @@ _lib.loom_hip_dispatch_f16.argtypes = _lib.loom_hip_dispatch.argtypes
 _lib.loom_hip_dispatch_f16.restype = ctypes.c_int
 _lib.loom_hip_check_variant.argtypes = [ctypes.c_char_p, ctypes.POINTER(_i64), ctypes.c_int, *_ERR]
 _lib.loom_hip_check_variant.restype = ctypes.c_int
+_lib.loom_hip_workspace_bytes.argtypes = [ctypes.c_char_p, ctypes.POINTER(_i64), ctypes.c_int,
+                                          ctypes.POINTER(_sz), *_ERR]
+_lib.loom_hip_workspace_bytes.restype = ctypes.c_int
 for _fn in ("loom_hip_constraint_scope", "loom_hip_preferred_block_sizes", "loom_hip_hw_spec"):
     getattr(_lib, _fn).argtypes = [ctypes.c_char_p, ctypes.POINTER(_i64), ctypes.c_int,
                                    ctypes.c_char_p, _sz, *_ERR]
@@ -136,6 +139,7 @@ EXPORTED = tuple(_SIGS) + tuple(_CIFACE) + ("loom_hip_peak_hbm_read", "loom_hip_
                            "loom_hip_flash_decode_workspace_bytes", "loom_hip_version",
                            "loom_hip_materialize_variants", "loom_hip_parse_variant",
                            "loom_hip_dispatch", "loom_hip_dispatch_f16", "loom_hip_check_variant",
+                           "loom_hip_workspace_bytes",
                            "loom_hip_constraint_scope", "loom_hip_preferred_block_sizes", "loom_hip_hw_spec")
 
 #: block-size symbols in the slot order of loom_hip_parse_variant's tiles[]
@@ -537,6 +541,16 @@ def parse_variant(name: str):
     return func.value.decode(), {s: int(t) for s, t in zip(TILE_SYMBOLS, tiles) if t >= 0}
 
 
+def workspace_bytes(variant: str, dims) -> int:
+    """Bytes of the workspace ``dispatch`` needs for a materialized variant at
+    these extents (loom_hip_workspace_bytes): split-K's partials, decode's
+    (lse_s, o_s), 0 for the other functions."""
+    d = (_i64 * max(len(dims), 1))(*[int(x) for x in dims])
+    out = _sz(0)
+    _call("loom_hip_workspace_bytes", variant.encode(), d, len(dims), ctypes.byref(out))
+    return int(out.value)
+
+
 def dispatch(variant: str, *tensors, workspace=None, scale=None, causal=False):
     """Runs the kernel a materialized variant name selects on ``tensors``
     (the function's memref arguments in IR order, outputs included) through
@@ -552,12 +566,9 @@ def dispatch(variant: str, *tensors, workspace=None, scale=None, causal=False):
     ptrs = _check_call(func, tensors, dims, e)
     dev = tensors[0].device
     need = 0
-    if func == "split_k_matmul_gather" and "tile_k" in tiles:
-        M, N, K = dims
-        need = split_k_workspace_bytes(M, N, K, tiles["tile_k"])
-    if func == "flash_decode" and "tile_s" in tiles:
-        B, H, D, S = dims
-        need = flash_decode_workspace_bytes(B, H, D, S, tiles["tile_s"])
+    if (func == "split_k_matmul_gather" and "tile_k" in tiles) or \
+            (func == "flash_decode" and "tile_s" in tiles):
+        need = workspace_bytes(variant, dims)
     if workspace is None and need:
         workspace = torch.empty(max(need, 4), dtype=torch.uint8, device=dev)
     ws_ptr, ws_bytes = None, 0

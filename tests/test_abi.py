@@ -7,6 +7,7 @@
 - workspace-size helpers match the layouts the header documents.
 """
 import ctypes
+import json
 import os
 import re
 
@@ -129,7 +130,6 @@ def test_reference_emitted_variants_accepted(lh):
     __tile_b1__tile_n512__tile_s512 on B16 H32 D128 S8192.  The other
     examples' emitted names carry placeholder sizes beyond their extents
     (materialize.cpp:56-65) and are rejected as such."""
-    import json
     with open(os.path.join(os.path.dirname(__file__), "golden", "variant_names.json")) as f:
         names = json.load(f)
     for ex, dims in (("split_k_mm_gather", [512, 512, 4096]), ("mqa_decode", [16, 32, 128, 8192])):
@@ -256,3 +256,29 @@ def test_ssd_rejections(lh):
     # (a launch here, without a GPU, would fail with code 3 instead)
     rc, msg = _call(lh, "loom_hip_ssd_prologue", *([FAKE] * 8), 1, 2, 4, 1, 144, 64, 128, None)
     assert rc == 2 and "LDS stage" in msg, (rc, msg)
+
+
+def test_workspace_bytes_by_variant(lh):
+    """loom_hip_workspace_bytes: the per-function workspace sizes, reached by
+    a materialized name (the reference's own split-K and mqa variants
+    included), 0 for functions without a workspace, and its rejections."""
+    with open(os.path.join(os.path.dirname(__file__), "golden", "variant_names.json")) as f:
+        emitted = json.load(f)
+    sk = emitted["split_k_mm_gather"]["variants"][0]
+    assert lh.workspace_bytes(sk, (512, 512, 4096)) == lh.split_k_workspace_bytes(512, 512, 4096, 512)
+    mqa = emitted["mqa_decode"]["variants"][0]
+    assert lh.workspace_bytes(mqa, (16, 32, 128, 8192)) == \
+        lh.flash_decode_workspace_bytes(16, 32, 128, 8192, 512)
+    assert lh.workspace_bytes("flash_decode__tile_b1__tile_n64__tile_s1000", (2, 40, 96, 3001)) == \
+        lh.flash_decode_workspace_bytes(2, 40, 96, 3001, 1000)
+    assert lh.workspace_bytes("matmul__tile_k64__tile_m64__tile_n64", (64, 64, 64)) == 0
+    assert lh.workspace_bytes("attention__tile_b1__tile_m64__tile_n64", (2, 64, 64, 128)) == 0
+    assert lh.workspace_bytes("helion_mamba2_chunk_scan_kernel__tile_b1__tile_c1__tile_h1__tile_k64"
+                              "__tile_m64__tile_n64", (1, 2, 4, 1, 64, 64, 128)) == 0
+    for name, dims, code in (("conv2d__tile_m64", (1, 2, 3), 2),                       # no kernel
+                             ("split_k_matmul_gather__tile_m64__tile_n64", (8, 8, 8), 1),  # tile_k
+                             ("flash_decode__tile_s64", (1, 2, 64), 1),                # 3 extents
+                             ("flash_decode__tile_s64", (1, 2, 64, 0), 1)):             # not positive
+        with pytest.raises(lh.LoomHipError) as ei:
+            lh.workspace_bytes(name, dims)
+        assert ei.value.code == code, name
