@@ -95,6 +95,27 @@ def test_attention_and_decode(lh):
                     lambda: lh.flash_decode_noalloc(k, v, q, out2, tile_s=512, tile_n=128), [out2])
 
 
+def test_attention_and_decode_other_paths(lh):
+    """The kernels picked away from the common shapes: attention at head dim
+    256 and at head dim 96 with a key count not a multiple of 8 (K staged
+    through registers), decode with 64 heads per workgroup (H 48), with
+    ragged S on the LDS-DMA kernel (H 48, S 1001) and on the register kernel
+    (H 8, S 1001), and at head dim 200."""
+    torch.manual_seed(14)
+    for BH, Sq, Skv, D, causal in ((2, 300, 300, 256, True), (2, 190, 517, 96, False)):
+        k, v, q = _bf(BH, D, Skv), _bf(BH, Skv, D), _bf(BH, Sq, D)
+        out = torch.empty(BH, Sq, D, dtype=torch.bfloat16, device="cuda")
+        _replay_matches(f"attention D{D} Skv{Skv}",
+                        lambda: lh.attention(k, v, q, out, causal=causal, tile_m=128), [out])
+    for B, H, D, S, ts in ((2, 48, 128, 4096, 512), (2, 48, 128, 1001, 256),
+                           (2, 8, 64, 1001, 128), (3, 16, 200, 777, 256)):
+        k, v, q = _bf(B, D, S), _bf(B, S, D), _bf(B, H, D)
+        out = torch.empty(B, H, D, dtype=torch.bfloat16, device="cuda")
+        ws = lh.flash_decode_workspace(B, H, D, S, ts, "cuda")
+        _replay_matches(f"flash_decode B{B} H{H} D{D} S{S}",
+                        lambda: lh.flash_decode(k, v, q, out, ws, tile_s=ts), [out])
+
+
 def test_mamba(lh):
     torch.manual_seed(13)
     b, H, nc, Q, P, N = 2, 8, 4, 256, 64, 128
