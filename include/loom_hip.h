@@ -176,7 +176,8 @@ int loom_hip_flash_decode_noalloc(const void* k, const void* v, const void* q, v
  * P, or P) as the smallest of 16, 32, 64 columns covering it (64 above);
  * tile_k (1 <= tile_k <= max(8192, Q), 8192 being the example's loom.sym
  * upper_bound) is the reference's k step and does not change the result.
- * Q <= 256, N <= 128, Q, N, P multiples of 8. */
+ * Q <= 512, N <= 256, Q, N, P multiples of 8 (above Q 256 or N 128 a
+ * 4-wave build with one workgroup per CU runs it). */
 int loom_hip_helion_mamba2_chunk_scan_kernel(
     const void* cb, const void* x, const void* dt, const void* dA_cumsum, const void* C,
     const void* D, const void* prev_states_T, void* out, int64_t batch, int64_t nchunks,
@@ -230,10 +231,9 @@ int loom_hip_helion_mamba2_chunk_scan_kernel_f16(
  * softplus; the same memory as chunk_scan's dt [b,H,c,Q]), A [H] fp32,
  * B and C [b,G,L,N] bf16, L = nchunks * chunk_size, head h reads group
  * h / (H / G).  chunk_size, headdim and dstate are multiples of 16,
- * chunk_size <= 256 (a multiple of 32 from 128 up), headdim <= 256,
- * dstate <= 128 (a multiple of 32 above 32; of 64 above 64 when
- * headdim <= 128), and ceil32(chunk_size) * headdim * 2 <= 64 KiB.  The
- * dt, dA_cumsum and prev_states_T of these stages are fp32 in both forms. */
+ * chunk_size <= 512, headdim <= 256, dstate <= 256 (a multiple of 32 above
+ * 32).  The dt, dA_cumsum and prev_states_T of these stages are fp32 in
+ * both forms. */
 
 /* dA_cumsum[b,h,c,q] = sum_{q' <= q} dt[b,h,c*Q+q'] * A[h] (fp32; a wave
  * prefix scan, so the summation order differs from a serial loop). */

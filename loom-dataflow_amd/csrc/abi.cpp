@@ -604,8 +604,8 @@ int build_scope(const std::string& f, const int64_t* d, int nd, Scope& sc, std::
     sc.seq_iter = jop("Div", js("tile_s"), js("tile_n"));
   } else if (f == "helion_mamba2_chunk_scan_kernel") {
     if (!need(7)) return LOOM_HIP_EINVAL;
-    if (d[4] > 256 || d[6] > 128 || d[4] % 8 || d[5] % 8 || d[6] % 8 || d[2] % d[3]) {
-      err = "constraint_scope: chunk scan is built for chunk_size <= 256, dstate <= 128, "
+    if (d[4] > 512 || d[6] > 256 || d[4] % 8 || d[5] % 8 || d[6] % 8 || d[2] % d[3]) {
+      err = "constraint_scope: chunk scan is built for chunk_size <= 512, dstate <= 256, "
             "multiples of 8, and nheads a multiple of ngroups";
       return LOOM_HIP_EUNSUP;
     }

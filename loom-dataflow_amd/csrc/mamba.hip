@@ -42,8 +42,12 @@
 
 namespace {
 
-constexpr int kQmax = 256;   // chunk length
-constexpr int kNmax = 128;   // state size
+constexpr int kQmax = 256;   // chunk length of the default build
+constexpr int kNmax = 128;   // state size of the default build
+// The long-chunk build (4 waves, one workgroup per CU: 134 KB of LDS at
+// tile_n 64) takes chunks up to 512 and states up to 256 wide.
+constexpr int kQbig = 512, kNbig = 256;
+constexpr int kMTileMax = 256;   // rows of the largest built m-tile
 // upper_bound of the example's tile_k symbol
 // (examples/mamba_chunk_scan/IR/00_from_helion_frontend.mlir:3)
 constexpr int64_t kMambaTileKBound = 8192;
@@ -76,19 +80,20 @@ LOOM_DEV float side_at(const void* __restrict__ t, int64_t i) {
 
 // PT: p tiles of 16 per workgroup (tile_n = 16 PT); F16: f16 elements;
 // kWaves: 4 or 8 waves (the 8-wave form is held to 128 VGPRs: four waves per
-// SIMD)
-template <int PT, bool F16, int kWaves>
+// SIMD); QM, NM: the longest chunk and the widest state it is built for
+template <int PT, bool F16, int kWaves, int QM = kQmax, int NM = kNmax>
 __global__ void __launch_bounds__(64 * kWaves, kWaves == 8 ? 4 : 1)
     mamba_chunk_scan_kernel(MambaParams p) {
+  static_assert(QM % 128 == 0 && NM % 128 == 0, "xT and pT rows: whole 256-byte bank windows");
   constexpr int TN = 16 * PT;
-  constexpr int XROW = kQmax / 8;   // 16-byte chunks per xT row
-  constexpr int PROW = kNmax / 8;   // 16-byte chunks per pT row
+  constexpr int XROW = QM / 8;   // 16-byte chunks per xT row
+  constexpr int PROW = NM / 8;   // 16-byte chunks per pT row
   // LDS sized to the workgroup's TN columns: narrower tiles leave room for
   // more workgroups per CU (tile_n 16: 226.6 -> 179.2 us at the BASELINE
   // shape, against the 64-column size for every tile)
   __shared__ u32x4_t xT[TN * XROW];           // [p][k]
   __shared__ u32x4_t pT[2][TN * PROW];        // hi, lo: [p][n]
-  __shared__ __attribute__((aligned(16))) float s_dA[kQmax], s_dt[kQmax], s_U[kQmax];
+  __shared__ __attribute__((aligned(16))) float s_dA[QM], s_dt[QM], s_U[QM];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -131,9 +136,9 @@ __global__ void __launch_bounds__(64 * kWaves, kWaves == 8 ? 4 : 1)
 
   const float Dh = side_at<F16>(p.Dh, h);
   const int nmt16 = (mend - m0 + 15) / 16;  // 16-row tiles of this workgroup
-  constexpr int MAXT = kQmax / 16 / kWaves;  // tiles per wave at most
-  constexpr int NSN = kNmax / 32;            // state-term steps at most
-  constexpr int NKS = kQmax / 32;            // intra-chunk steps at most
+  constexpr int MAXT = kMTileMax / 16 / kWaves;  // tiles per wave at most
+  constexpr int NSN = NM / 32;                   // state-term steps at most
+  constexpr int NKS = QM / 32;                   // intra-chunk steps at most
   // snake deal of 16-row tiles: slot ti of wave w is tile 4 ti + (w or 3 - w)
   auto tile_of = [&](int ti) {
     return kWaves * ti + ((ti & 1) ? (kWaves - 1 - wave) : wave);
@@ -145,7 +150,7 @@ __global__ void __launch_bounds__(64 * kWaves, kWaves == 8 ? 4 : 1)
   // Buffer loads read rows past the chunk as zeros.
   const rsrc_t rC = make_rsrc(Cg, (uint32_t)(Q * N * 2));
   const rsrc_t rCB = make_rsrc(cbg, (uint32_t)(Q * Q * 2));
-  constexpr bool kCbAhead = kWaves == 4;
+  constexpr bool kCbAhead = kWaves == 4 && QM == kQmax;   // 64 more VGPRs in the long build
   struct CRows {
     u32x4_t c[NSN];
   };
@@ -189,85 +194,98 @@ __global__ void __launch_bounds__(64 * kWaves, kWaves == 8 ? 4 : 1)
   // 32-deep MFMA step, rows past the chunk zero-filled); half an 8x8 block
   // of prevT (rows n = 8 p_nc + 0..7, columns p = 8 p_pc + 4 p_h + 0..3) for
   // each of the first 2*nch*pch threads, from thread 256 on with 8 waves so
-  // no thread stages both; one dA and dt value per thread.
+  // no thread stages both; one dA and dt value per thread.  The long build
+  // has more blocks and keys than threads and stages them in rounds (x
+  // block tid + 256 r, and so on); the default build fits one round.
   const int kch = ((mend + 31) / 32) * 4, pch = TN / 8;
   const int nch = ((N + 31) / 32) * 4;
-  constexpr int pbase = kWaves == 8 ? 256 : 0;   // kch * pch <= 256, 2 nch pch <= 256
-  const int tp = tid - pbase;
-  const bool do_x = tid < kch * pch, do_p = tp >= 0 && tp < 2 * nch * pch;
-  const int x_kc = tid % kch, x_pc = tid / kch;
-  const int p_h = tp & 1, p_nc = (tp >> 1) % nch, p_pc = (tp >> 1) / nch;
-  u32x4_t xr[8];
-  f32x4_t pr[8];
-  float dA_v = 0.f, dt_v = 0.f, dA_e = 0.f;
-  if (tid < Q) {
-    dA_v = side_at<F16>(p.dA, sidx + tid);
-    dt_v = side_at<F16>(p.dt, sidx + tid);
-    dA_e = side_at<F16>(p.dA, sidx + min(tid | 31, Q - 1));  // last key of tid's 32-key block
-  }
-  if (do_x) {
-    const int pg = p0 + x_pc * 8;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int k = x_kc * 8 + e;
-      xr[e] = (k < Q && pg < P) ? *reinterpret_cast<const u32x4_t*>(xg + (int64_t)k * P + pg)
-                                : u32x4_t{0u, 0u, 0u, 0u};
+  constexpr int pbase = kWaves == 8 ? 256 : 0;
+  constexpr int NT = 64 * kWaves, XT = kWaves == 8 ? 256 : NT, PTH = NT - pbase;
+  constexpr int RX = ((QM / 8) * (2 * PT) + XT - 1) / XT;    // kch * pch <= QM/8 * TN/8
+  constexpr int RP = (2 * (NM / 8) * (2 * PT) + PTH - 1) / PTH;
+  constexpr int RQ = (QM + NT - 1) / NT;
+  constexpr int ROUNDS = RX > RP ? (RX > RQ ? RX : RQ) : (RP > RQ ? RP : RQ);
+  static_assert(QM != kQmax || NM != kNmax || ROUNDS == 1, "the default build stages in one round");
+  auto stage = [&](int rd) {
+    const int xi = tid + rd * XT, tp = tid - pbase + rd * PTH, qi = tid + rd * NT;
+    const bool do_x = (ROUNDS == 1 || tid < XT) && xi < kch * pch;
+    const bool do_p = tp >= rd * PTH && tp < 2 * nch * pch;
+    const int x_kc = xi % kch, x_pc = xi / kch;
+    const int p_h = tp & 1, p_nc = (tp >> 1) % nch, p_pc = (tp >> 1) / nch;
+    u32x4_t xr[8];
+    f32x4_t pr[8];
+    float dA_v = 0.f, dt_v = 0.f, dA_e = 0.f;
+    if (qi < Q) {
+      dA_v = side_at<F16>(p.dA, sidx + qi);
+      dt_v = side_at<F16>(p.dt, sidx + qi);
+      dA_e = side_at<F16>(p.dA, sidx + min(qi | 31, Q - 1));  // last key of qi's 32-key block
     }
-  }
-  if (do_p) {
-    const int pg = p0 + p_pc * 8 + 4 * p_h;   // P % 8 == 0: pg < P covers pg + 3
+    if (do_x) {
+      const int pg = p0 + x_pc * 8;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int n = p_nc * 8 + e;
-      if (n < N && pg < P) {
-        if constexpr (F16) {
-          const u32x2_t w = *reinterpret_cast<const u32x2_t*>(pvh + (int64_t)n * P + pg);
-          pr[e] = f32x4_t{lo16<true>(w[0]), hi16<true>(w[0]), lo16<true>(w[1]), hi16<true>(w[1])};
+      for (int e = 0; e < 8; ++e) {
+        const int k = x_kc * 8 + e;
+        xr[e] = (k < Q && pg < P) ? *reinterpret_cast<const u32x4_t*>(xg + (int64_t)k * P + pg)
+                                  : u32x4_t{0u, 0u, 0u, 0u};
+      }
+    }
+    if (do_p) {
+      const int pg = p0 + p_pc * 8 + 4 * p_h;   // P % 8 == 0: pg < P covers pg + 3
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int n = p_nc * 8 + e;
+        if (n < N && pg < P) {
+          if constexpr (F16) {
+            const u32x2_t w = *reinterpret_cast<const u32x2_t*>(pvh + (int64_t)n * P + pg);
+            pr[e] = f32x4_t{lo16<true>(w[0]), hi16<true>(w[0]), lo16<true>(w[1]), hi16<true>(w[1])};
+          } else {
+            pr[e] = *reinterpret_cast<const f32x4_t*>(pvg + (int64_t)n * P + pg);
+          }
         } else {
-          pr[e] = *reinterpret_cast<const f32x4_t*>(pvg + (int64_t)n * P + pg);
+          pr[e] = f32x4_t{0.f, 0.f, 0.f, 0.f};
         }
-      } else {
-        pr[e] = f32x4_t{0.f, 0.f, 0.f, 0.f};
       }
     }
-  }
-  if (tid < Q) {
-    constexpr float kLog2e = 1.4426950408889634f;
-    s_dA[tid] = dA_v * kLog2e;  // log2 domain
-    s_dt[tid] = dt_v;
-    // U[k] = exp2(dA[k_e] - dA[k]) dt[k], k_e = last key of k's 32-key block:
-    // the k-dependent factor of W on blocks that lie wholly below a row
-    s_U[tid] = fast_exp2((dA_e - dA_v) * kLog2e) * dt_v;
-  }
-  if (do_x) {
-    u32x4_t tr[8];
-    transpose8x8(xr, tr);
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int row = x_pc * 8 + u;
-      xT[row * XROW + (x_kc ^ (row & 15))] = tr[u];
+    if (qi < Q) {
+      constexpr float kLog2e = 1.4426950408889634f;
+      s_dA[qi] = dA_v * kLog2e;  // log2 domain
+      s_dt[qi] = dt_v;
+      // U[k] = exp2(dA[k_e] - dA[k]) dt[k], k_e = last key of k's 32-key block:
+      // the k-dependent factor of W on blocks that lie wholly below a row
+      s_U[qi] = fast_exp2((dA_e - dA_v) * kLog2e) * dt_v;
     }
-  }
-  if (do_p) {
-    // prevT split into bf16 hi + lo (the state term keeps ~16 mantissa bits),
-    // packed straight into the transposed layout: dword j of pT row p holds
-    // n = 8 p_nc + 2j, 2j + 1.  An f16 prevT is exact in f16, so its lo half
-    // is zero and never used.
+    if (do_x) {
+      u32x4_t tr[8];
+      transpose8x8(xr, tr);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int pp = p_pc * 8 + 4 * p_h + i;
-      u32x4_t hi, lo;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float a = pr[2 * j][i], c = pr[2 * j + 1][i];
-        const uint32_t hw = pack2<F16>(a, c);
-        hi[j] = hw;
-        lo[j] = pack2<F16>(a - lo16<F16>(hw), c - hi16<F16>(hw));
+      for (int u = 0; u < 8; ++u) {
+        const int row = x_pc * 8 + u;
+        xT[row * XROW + (x_kc ^ (row & 15))] = tr[u];
       }
-      pT[0][pp * PROW + (p_nc ^ (pp & 15))] = hi;
-      if constexpr (!F16) pT[1][pp * PROW + (p_nc ^ (pp & 15))] = lo;
     }
-  }
+    if (do_p) {
+      // prevT split into bf16 hi + lo (the state term keeps ~16 mantissa bits),
+      // packed straight into the transposed layout: dword j of pT row p holds
+      // n = 8 p_nc + 2j, 2j + 1.  An f16 prevT is exact in f16, so its lo half
+      // is zero and never used.
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int pp = p_pc * 8 + 4 * p_h + i;
+        u32x4_t hi, lo;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float a = pr[2 * j][i], c = pr[2 * j + 1][i];
+          const uint32_t hw = pack2<F16>(a, c);
+          hi[j] = hw;
+          lo[j] = pack2<F16>(a - lo16<F16>(hw), c - hi16<F16>(hw));
+        }
+        pT[0][pp * PROW + (p_nc ^ (pp & 15))] = hi;
+        if constexpr (!F16) pT[1][pp * PROW + (p_nc ^ (pp & 15))] = lo;
+      }
+    }
+  };
+  stage(0);
+  for (int rd = 1; rd < ROUNDS; ++rd) stage(rd);
   __syncthreads();
 
 #pragma unroll
@@ -378,8 +396,12 @@ __global__ void __launch_bounds__(64 * kWaves, kWaves == 8 ? 4 : 1)
 template <int PT, bool F16>
 void launch_mamba(const MambaParams& p, hipStream_t st) {
   const int64_t nblocks = (int64_t)p.Bb * p.nc * p.H * p.nmt * p.npt;
+  // chunks longer than 256 or states wider than 128: the long build, 4 waves
+  if (p.Q > kQmax || p.N > kNmax)
+    hipLaunchKernelGGL((mamba_chunk_scan_kernel<PT, F16, 4, kQbig, kNbig>), dim3((unsigned)nblocks),
+                       dim3(256), 0, st, p);
   // 8 waves when the m-tile holds 8 or more 16-row tiles (tile_m >= 128)
-  if (p.tile_m >= 128)
+  else if (p.tile_m >= 128)
     hipLaunchKernelGGL((mamba_chunk_scan_kernel<PT, F16, 8>), dim3((unsigned)nblocks), dim3(512), 0,
                        st, p);
   else
@@ -433,11 +455,11 @@ int chunk_scan_impl(
                      fn, (long long)tile_m, (long long)tile_n);
   tile_m = wm;
   tile_n = wn;
-  if (chunk_size > kQmax || dstate > kNmax || chunk_size % 8 || dstate % 8 || headdim % 8)
+  if (chunk_size > kQbig || dstate > kNbig || chunk_size % 8 || dstate % 8 || headdim % 8)
     return loom_fail(err, errlen, LOOM_EUNSUP,
                      "%s: built for chunk_size <= %d, dstate <= %d, both and headdim multiples "
                      "of 8",
-                     fn, kQmax, kNmax);
+                     fn, kQbig, kNbig);
   if (!aligned16(cb) || !aligned16(x) || !aligned16(C) || !aligned16(prev_states_T) ||
       !aligned16(out))
     return loom_fail(err, errlen, LOOM_EINVAL, "%s: tensors must be 16-byte aligned", fn);

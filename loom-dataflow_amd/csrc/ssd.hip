@@ -78,7 +78,8 @@ __global__ void __launch_bounds__(64) ssd_cumsum_kernel(const float* __restrict_
 // cb = C B^T, lower triangle
 // ---------------------------------------------------------------------------
 constexpr int kCbTiles = 4;  // 16x16 output tiles per wave (one row band)
-template <bool F16>
+// NKS: 32-wide n steps held in registers (4: dstate <= 128, 8: <= 256)
+template <bool F16, int NKS>
 __global__ void __launch_bounds__(64) ssd_cb_kernel(const uint16_t* __restrict__ Bm,
                                                     const uint16_t* __restrict__ Cm,
                                                     uint16_t* __restrict__ cb, int nc, int G,
@@ -99,9 +100,9 @@ __global__ void __launch_bounds__(64) ssd_cb_kernel(const uint16_t* __restrict__
   // per wave.  C^T operand: lane holds C[i0 + r][32 ks + 8 gq .. + 7], B
   // operand of tile j: B[16 (jt0 + j) + r][same n] (zero past N; tiles
   // above the diagonal are not loaded)
-  u32x4_t cf[4], bf[kCbTiles][4];
+  u32x4_t cf[NKS], bf[kCbTiles][NKS];
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
+  for (int ks = 0; ks < NKS; ++ks) {
     const int n = 32 * ks + 8 * gq;
     const bool live = ks < nks && n < N && jt0 <= it;
     cf[ks] = live ? *reinterpret_cast<const u32x4_t*>(Cc + (int64_t)(i0 + r) * N + n)
@@ -120,7 +121,7 @@ __global__ void __launch_bounds__(64) ssd_cb_kernel(const uint16_t* __restrict__
     f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
     if (jt <= it) {
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks)
+      for (int ks = 0; ks < NKS; ++ks)
         if (ks < nks) acc = mfma16t<F16>(bf[j][ks], cf[ks], acc);  // D[j][i] = sum_n B[j][n] C[i][n]
       // lane holds cb[i0 + r][16 jt + 4 gq + e]; the diagonal tile keeps j <= i
       if (jt == it) {
@@ -137,7 +138,7 @@ __global__ void __launch_bounds__(64) ssd_cb_kernel(const uint16_t* __restrict__
 // ---------------------------------------------------------------------------
 // chunk states + state passing -> prev_states_T
 // ---------------------------------------------------------------------------
-constexpr int kSsdQmax = 256, kSsdPmax = 256, kSsdNB = 64, kSsdWaves = 8;
+constexpr int kSsdQmax = 512, kSsdPmax = 256, kSsdNmax = 256, kSsdNB = 64, kSsdWaves = 8;
 constexpr int kSsdStageMax = 36 * 1024;      // bytes per pipeline stage
 constexpr int kSsdRing = 136 * 1024;         // LDS for the stage ring (four 34 KB stages)
 constexpr int kSsdNSMax = 8;                 // stages at most
@@ -575,11 +576,12 @@ int check_ssd(const char* fn, int64_t batch, int64_t nchunks, int64_t nheads, in
   if (chunk_size % 16 || headdim % 16 || dstate % 16)
     return loom_fail(err, errlen, LOOM_EUNSUP,
                      "%s: chunk_size, headdim and dstate must be multiples of 16", fn);
-  if (chunk_size > kSsdQmax || headdim > kSsdPmax || dstate > 128 || (dstate > 32 && dstate % 32))
+  if (chunk_size > kSsdQmax || headdim > kSsdPmax || dstate > kSsdNmax ||
+      (dstate > 32 && dstate % 32))
     return loom_fail(err, errlen, LOOM_EUNSUP,
-                     "%s: built for chunk_size <= %d, headdim <= %d, dstate <= 128 "
+                     "%s: built for chunk_size <= %d, headdim <= %d, dstate <= %d "
                      "(a multiple of 32 above 32)",
-                     fn, kSsdQmax, kSsdPmax);
+                     fn, kSsdQmax, kSsdPmax, kSsdNmax);
   if (!loom_prod_le({batch, nheads, nchunks, chunk_size, headdim}, ((int64_t)1 << 40) - 1) ||
       !loom_prod_le({batch, nchunks, nheads, dstate, headdim}, (int64_t)1 << 40) ||
       !loom_prod_le({batch, ngroups, nchunks, chunk_size, dstate}, (int64_t)1 << 40))
@@ -627,13 +629,16 @@ int bmm_chunk_impl(const void* B, const void* C, void* cb, int64_t batch, int64_
   if (!aligned16(B) || !aligned16(C) || (reinterpret_cast<uintptr_t>(cb) & 7u))
     return loom_fail(err, errlen, LOOM_EINVAL, "ssd_bmm_chunk: B, C 16-byte and cb 8-byte aligned");
   if (loom_validate_only()) return loom_ok(err, errlen);
-  hipLaunchKernelGGL(ssd_cb_kernel<F16>,
-                     dim3((unsigned)(batch * nchunks * ngroups), (unsigned)(chunk_size / 16),
-                          (unsigned)((chunk_size / 16 + kCbTiles - 1) / kCbTiles)),
-                     dim3(64), 0, static_cast<hipStream_t>(stream),
-                     static_cast<const uint16_t*>(B), static_cast<const uint16_t*>(C),
-                     static_cast<uint16_t*>(cb), (int)nchunks, (int)ngroups,
-                     (int)(nchunks * chunk_size), (int)chunk_size, (int)dstate);
+  const dim3 grid((unsigned)(batch * nchunks * ngroups), (unsigned)(chunk_size / 16),
+                  (unsigned)((chunk_size / 16 + kCbTiles - 1) / kCbTiles));
+  auto launch = [&](auto kern) {
+    hipLaunchKernelGGL(kern, grid, dim3(64), 0, static_cast<hipStream_t>(stream),
+                       static_cast<const uint16_t*>(B), static_cast<const uint16_t*>(C),
+                       static_cast<uint16_t*>(cb), (int)nchunks, (int)ngroups,
+                       (int)(nchunks * chunk_size), (int)chunk_size, (int)dstate);
+  };
+  if (dstate <= 128) launch(ssd_cb_kernel<F16, 4>);
+  else launch(ssd_cb_kernel<F16, 8>);
   return loom_check_launch(err, errlen, "ssd_bmm_chunk");
 }
 
@@ -651,7 +656,9 @@ int state_passing_impl(const void* x, const void* dt, const void* dA_cumsum,
   if (!aligned16(x) || !aligned16(B) || !aligned16(prev_states_T))
     return loom_fail(err, errlen, LOOM_EINVAL, "ssd_chunk_state_passing: tensors must be 16-byte aligned");
   // n block: 64 wide while the P x 64 block fits four tiles per wave, else 32
-  const int nb = (int)std::min<int64_t>(dstate, headdim <= 128 ? kSsdNB : 32);
+  // (and 32 when 64 does not divide dstate; dstate itself up to 32)
+  const int nb_cap = headdim <= 128 ? kSsdNB : 32;
+  const int nb = dstate <= nb_cap ? (int)dstate : (dstate % nb_cap == 0 ? nb_cap : 32);
   const int ptiles = (int)(headdim / 16), tiles = ptiles * (nb / 16);
   // kernel mode (see ssd_state_kernel) and tiles per wave
   const int mode = kSsdWaves % ptiles ? 0 : (2 * ptiles == kSsdWaves ? 2 : 1);
@@ -669,7 +676,9 @@ int state_passing_impl(const void* x, const void* dt, const void* dA_cumsum,
   p.H = (int)nheads; p.G = (int)ngroups; p.nc = (int)nchunks; p.Q = (int)chunk_size;
   p.P = (int)headdim; p.N = (int)dstate; p.nb = nb;
   // unit (when the WIDE form does not apply): the largest of 128, 64 and 32
-  // keys dividing Q whose stage fits
+  // keys dividing Q whose stage fits, else the largest other multiple of 16
+  // (a unit that is not a multiple of 32 keys is zero-weighted up to the
+  // next one)
   // (each unit costs a barrier and a wait, and the copies in flight per
   // workgroup, not the ring depth, bound the stream: 128-key units measured
   // faster than 64-key units with twice the stages); a Q that is not a
@@ -705,7 +714,7 @@ int state_passing_impl(const void* x, const void* dt, const void* dA_cumsum,
     static_assert(2 * (256 * 64 * 2 * 2 + 3072) <= kSsdRing, "two 256-key stages fit the ring");
     best = 0;
   }
-  for (int qs : {128, 64, 32}) {
+  for (int qs : {128, 64, 32, 112, 96, 80, 48, 16}) {
     if (best >= 0) break;
     if (p.Q % qs) continue;
     SsdStateParams q = p;

@@ -242,8 +242,10 @@ def test_ssd_rejections(lh):
     assert rc == 1 and "ngroups" in msg
     rc, msg = _call(lh, "loom_hip_ssd_prologue", *([FAKE] * 8), 1, 2, 4, 1, 8, 64, 128, None)
     assert rc == 2 and "multiples of 16" in msg
-    rc, msg = _call(lh, "loom_hip_ssd_prologue", *([FAKE] * 8), 1, 2, 4, 1, 512, 64, 128, None)
-    assert rc == 2 and "chunk_size <= 256" in msg
+    rc, msg = _call(lh, "loom_hip_ssd_prologue", *([FAKE] * 8), 1, 2, 4, 1, 640, 64, 128, None)
+    assert rc == 2 and "chunk_size <= 512" in msg
+    rc, msg = _call(lh, "loom_hip_ssd_prologue", *([FAKE] * 8), 1, 2, 4, 1, 256, 64, 288, None)
+    assert rc == 2 and "dstate <= 256" in msg
     rc, msg = _call(lh, "loom_hip_ssd_prologue", *([FAKE] * 8), 1, 2, 4, 1, 256, 64, 48, None)
     assert rc == 2 and "multiple of 32" in msg
     rc, msg = _call(lh, "loom_hip_ssd_chunk_state_passing", None, *([FAKE] * 4),
@@ -251,11 +253,9 @@ def test_ssd_rejections(lh):
     assert rc == 1 and "null" in msg
     rc, msg = _call(lh, "loom_hip_ssd_chunk_cumsum", FAKE, FAKE, FAKE, 1, 2, 4, 1024, None)
     assert rc == 2 and "512" in msg
-    # chunk_size 144 passes the shared checks but fits no LDS plan of the state
-    # kernel: the prologue rejects it before launching its first two stages
-    # (a launch here, without a GPU, would fail with code 3 instead)
-    rc, msg = _call(lh, "loom_hip_ssd_prologue", *([FAKE] * 8), 1, 2, 4, 1, 144, 64, 128, None)
-    assert rc == 2 and "LDS stage" in msg, (rc, msg)
+    # headdim above 256: refused before any of the three stages launches
+    rc, msg = _call(lh, "loom_hip_ssd_prologue", *([FAKE] * 8), 1, 2, 4, 1, 256, 272, 128, None)
+    assert rc == 2 and "headdim <= 256" in msg, (rc, msg)
 
 
 def test_workspace_bytes_by_variant(lh):
