@@ -62,7 +62,8 @@ CASES = {
                                                        (2, 64, 128, 2048), (2, 8, 40, 1000),
                                                        (2, 8, 256, 1000)]),
     "helion_mamba2_chunk_scan_kernel": (["tile_m", "tile_n", "tile_k", "tile_c", "tile_b", "tile_h"],
-                                        [(4, 16, 32, 1, 256, 64, 128), (2, 8, 32, 4, 192, 160, 128)]),
+                                        [(4, 16, 32, 1, 256, 64, 128), (2, 8, 32, 4, 192, 160, 128),
+                                         (1, 2, 4, 1, 512, 64, 256), (1, 2, 3, 1, 264, 40, 136)]),
 }
 GRID = [1, 16, 48, 64, 96, 128, 192, 256, 1024]
 SMALL = [1, 2]
@@ -146,6 +147,12 @@ def test_unsupported_shapes_and_functions():
             loom_hip.constraint_scope("flash_decode", (4, 8, d, 1024))
         assert ei.value.code == 2
     loom_hip.constraint_scope("flash_decode", (4, 8, 136, 1001))   # any S at any built D
+    # chunk scan: chunk_size up to 512, dstate up to 256 (multiples of 8)
+    for dims in ((1, 2, 4, 1, 520, 64, 128), (1, 2, 4, 1, 256, 64, 264),
+                 (1, 2, 4, 1, 260, 64, 128)):
+        with pytest.raises(RuntimeError) as ei:
+            loom_hip.constraint_scope("helion_mamba2_chunk_scan_kernel", dims)
+        assert ei.value.code == 2, dims
     assert loom_hip.preferred_block_sizes("attention", (8, 4096, 4096, 256))["tile_m"] == 128
     with pytest.raises(RuntimeError) as ei:
         loom_hip.constraint_scope("conv2d", (1, 2, 3))
