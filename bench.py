@@ -449,7 +449,7 @@ def make_cases(torch, lh):
         return dict(fn=lambda i: lh.flash_decode(*sets[i % n], tile_s=1024, tile_n=128),
                     flop=4 * B * H * S * D, bytes=nb, bound="hbm", sets=n,
                     desc="mqa_decode B32 H32/1KV D128 S8192, tile_s 1024", cpu=cpu,
-                    kernel="decode_dma_kernel<128, false, false>")
+                    kernel="decode_dma_kernel<128, false, false, 4>")
     cases["mqa_decode"] = decode
 
     def mamba():
@@ -482,7 +482,7 @@ def make_cases(torch, lh):
             *sets[i % n], tile_m=256, tile_n=64, tile_k=64),
             flop=flop, bytes=nb, bound="hbm", sets=n, inputs=sets,
             desc="mamba chunk_scan b4 L4096 h32 P64 N128 g1 Q256", cpu=cpu,
-            kernel="mamba_chunk_scan_kernel<4, false, 8>")
+            kernel="mamba_chunk_scan_kernel<4, false, 8, 256, 128>")
     cases["mamba_chunk_scan"] = mamba
 
     def ssd():
