@@ -106,9 +106,11 @@ __global__ void __launch_bounds__(256) decode_combine_kernel(DecodeParams p) {
 // Split kernel, LDS-DMA form (the production path: S a multiple of 8).  One
 // workgroup of four waves per (batch, split, group of up to 32 query heads).
 // K and V of the split stream through LDS in 64-key stages copied by LDS DMA
-// (global_load_lds_dwordx4), four stages deep up to D 128 (two 64 KB stages
-// at D 256): up to 96 KB per workgroup in flight with no registers held by
-// loads, which is what streaming HBM at full rate takes.  Ks is [d][key] and Vs [key][d], as the tensors lay them
+// (global_load_lds_dwordx4), three stages deep up to D 128 (two 64 KB stages
+// at D 256): 64 KB per workgroup in flight with no registers held by loads
+// (a fourth stage, 96 KB in flight, streamed 2-3% slower at every shape
+// measured; two stages, 32 KB, slower at the large ones).  Ks is [d][key]
+// and Vs [key][d], as the tensors lay them
 // out; the MFMA operands that need k-contiguous data come from
 // ds_read_b64_tr_b16:
 //   S^T[key, h]  = K^T . Q^T : row operand K^T from Ks (lane r: key, eight
@@ -144,7 +146,7 @@ LOOM_DEV int dv_swz(int k) { return D >= 128 ? 2 * (k & 7) : 2 * ((k >> 1) & 3);
 template <int D, bool F16, bool KREG, int W>
 __global__ void __launch_bounds__(64 * W) decode_dma_kernel(DecodeParams p) {
   constexpr int KB = 64;                       // keys per stage
-  constexpr int NS = D > 128 ? 2 : 4;          // stages (64 KB each at D 256)
+  constexpr int NS = D > 128 ? 2 : 3;          // stages (64 KB each at D 256)
   constexpr int HS = 8 * W;                    // head slots (16 per pair of waves)
   constexpr int K_BYTES = D * KB * 2, V_BYTES = KB * D * 2;
   constexpr int K_INSTR = K_BYTES / 1024 / W, V_INSTR = V_BYTES / 1024 / W;
