@@ -532,8 +532,9 @@ int build_scope(const std::string& f, const int64_t* d, int nd, Scope& sc, std::
     ub(sym, extent);
     sc.hard.push_back(jlist("Or", {jdivisible(sym, kTileAlign), jop("Eq", js(sym), jc(extent))}));
   };
-  // GEMM workgroup tiles are square (64, 128 or 256); both A and B stage
-  // rings hold 64 KB for every built tile
+  // GEMM workgroup tiles are square (64, 128 or 256); the A and B stage
+  // rings hold at most 64 KB each (the 256 tile's four 16 KB stages; the
+  // smaller tiles' rings are half that), the bound given here
   auto gemm_tiles = [&](long long M, long long N) {
     sc.symbols.push_back(jsym("tile_m", M, kTileAlign));
     sc.symbols.push_back(jsym("tile_n", N, kTileAlign));
@@ -574,7 +575,7 @@ int build_scope(const std::string& f, const int64_t* d, int nd, Scope& sc, std::
     }
     // the kernel's (padded) head dim and its stages of 64-key K and V blocks
     const long long dk = d[3] <= 64 ? 64 : d[3] <= 128 ? 128 : 256;
-    const long long nst = dk > 128 ? 2 : 4;
+    const long long nst = dk > 128 ? 2 : 3;
     sc.symbols.push_back(jsym("tile_b", d[0], 1));
     sc.symbols.push_back(jsym("tile_m", d[1], kTileAlign));
     sc.symbols.push_back(jsym("tile_n", d[2], 1));

@@ -37,7 +37,7 @@ struct AttnParams {
 
 // ---------------------------------------------------------------------------
 // LDS-DMA variant: K and V blocks are copied global -> LDS unchanged
-// (global_load_lds_dwordx4, 4 stages of 64 keys, 2 at D 256), Ks [d][key] and
+// (global_load_lds_dwordx4, 3 stages of 64 keys, 2 at D 256), Ks [d][key] and
 // Vs [key][d],
 // and both operands that need k-contiguous data are built by
 // ds_read_b64_tr_b16:
@@ -78,8 +78,10 @@ LOOM_DEV int v_swz(int k) { return D >= 128 ? 2 * (k & 7) : 2 * ((k >> 1) & 3); 
 template <int D, int QT, int W, bool H, bool KREG>
 __global__ void __launch_bounds__(64 * W) attention_dma_kernel(AttnParams p) {
   constexpr int KB = 64;                        // keys per stage
-  // stages: four of 32 KB (K and V) up to D 128; two of 64 KB at D 256
-  constexpr int NS = D > 128 ? 2 : 4;
+  // stages: three of 32 KB (K and V) up to D 128; two of 64 KB at D 256
+  // (a fourth 32 KB stage measured 2% slower: causal B4 H32 S4096 572
+  // against 561 us; two stages 554-557 us, equal within box noise)
+  constexpr int NS = D > 128 ? 2 : 3;
   constexpr int BQ = 16 * QT * W;               // queries per workgroup
   constexpr int K_BYTES = D * KB * 2, V_BYTES = KB * D * 2;
   constexpr int K_INSTR = K_BYTES / 1024 / W;   // DMA instructions per wave per stage
@@ -90,11 +92,12 @@ __global__ void __launch_bounds__(64 * W) attention_dma_kernel(AttnParams p) {
   constexpr int V_ROWS_PER_I = 1024 / VROW;
   constexpr int DSTEPS = D / 32, DT = D / 16;
   static_assert(LPW * (NS - 2) <= 63, "vmcnt range");
-  constexpr int K_BYTES23 = NS > 2 ? K_BYTES : 16, V_BYTES23 = NS > 2 ? V_BYTES : 16;
+  constexpr int K_BYTES2 = NS > 2 ? K_BYTES : 16, V_BYTES2 = NS > 2 ? V_BYTES : 16;
+  constexpr int K_BYTES3 = NS > 3 ? K_BYTES : 16, V_BYTES3 = NS > 3 ? V_BYTES : 16;
   __shared__ __attribute__((aligned(1024))) char sK0[K_BYTES], sV0[V_BYTES];
   __shared__ __attribute__((aligned(1024))) char sK1[K_BYTES], sV1[V_BYTES];
-  __shared__ __attribute__((aligned(1024))) char sK2[K_BYTES23], sV2[V_BYTES23];
-  __shared__ __attribute__((aligned(1024))) char sK3[K_BYTES23], sV3[V_BYTES23];
+  __shared__ __attribute__((aligned(1024))) char sK2[K_BYTES2], sV2[V_BYTES2];
+  __shared__ __attribute__((aligned(1024))) char sK3[K_BYTES3], sV3[V_BYTES3];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;

@@ -440,7 +440,10 @@ __global__ void __launch_bounds__(256) gemm_dma_kernel(GemmParams p) {
 // Square T x T tile (T = 256, 128 or 64), software-pipelined: the production path
 // for K ranges that are whole multiples of NS*BK.  Four waves, each owning a
 // (T/2) x (T/2) block of C^T tiles; A [T][32] and B [32][T] stages arrive by
-// LDS DMA, NS deep (T 256: 4 stages, 128: 8, 64: 16; 128 KB in every case).
+// LDS DMA, NS deep (T 256: 4 stages of 32 KB; 128: 4 of 16 KB; 64: 8 of
+// 8 KB).  Deeper rings of the smaller tiles (8 and 16 stages, 128 KB) were
+// slower: split-K 512x512x16384 23.9 against 23.0 us, mm 1024^3 from HBM 8.0
+// against 7.6 us (4 and 2 stages: 31.9 us and 8.1 us).
 // The LDS layouts, swizzles and operand roles are those of gemm_dma_kernel
 // (and the accumulation order too: results are bitwise identical); what
 // differs is the schedule:
@@ -471,7 +474,7 @@ LOOM_DEV void acc_fence(f32x4_t (&acc)[TT][TT]) {
 }
 
 template <int T>
-constexpr int pipe_stages() { return T == 256 ? 4 : T == 128 ? 8 : 16; }
+constexpr int pipe_stages() { return T == 256 ? 4 : T == 128 ? 4 : 8; }
 
 // B swizzle of the pipelined kernels.  Rows of 256 bytes or more: b_swz.
 // T = 64 has 128-byte rows (8 chunks): rows k..k+3 of one pass already sit at
