@@ -67,6 +67,13 @@ LOOM_DEV int k_swz(int d) { return (2 * (d & 3)) ^ (2 * ((d >> 3) & 1)); }
 // r^4, r^6 share one, bits 1-2.
 template <int D>
 LOOM_DEV int v_swz(int k) { return D >= 128 ? 2 * (k & 7) : 2 * ((k >> 1) & 3); }
+// Q / O staging rows (2 D bytes): chunk c of row lr sits at position
+// c ^ q_swz(lr), so the 16 rows of a 32-lane pass (16-byte reads of chunks
+// c and c + 1, or 8-byte halves of one chunk) land on distinct banks: rows
+// 256 bytes apart at D 128, 128 bytes apart at D 64 (there bits 0-2 of the
+// row XOR bit 3, which tells rows 8 apart apart).
+template <int D>
+LOOM_DEV int q_swz(int lr) { return D >= 128 ? (lr & 15) : ((lr ^ (lr >> 3)) & 7); }
 
 // KREG (Skv not a multiple of 8): K rows [d][0..Skv) do not start on
 // 16-byte boundaries, so K cannot be copied by 16-byte LDS DMA.  Each lane
@@ -92,12 +99,17 @@ __global__ void __launch_bounds__(64 * W) attention_dma_kernel(AttnParams p) {
   constexpr int V_ROWS_PER_I = 1024 / VROW;
   constexpr int DSTEPS = D / 32, DT = D / 16;
   static_assert(LPW * (NS - 2) <= 63, "vmcnt range");
-  constexpr int K_BYTES2 = NS > 2 ? K_BYTES : 16, V_BYTES2 = NS > 2 ? V_BYTES : 16;
-  constexpr int K_BYTES3 = NS > 3 ? K_BYTES : 16, V_BYTES3 = NS > 3 ? V_BYTES : 16;
-  __shared__ __attribute__((aligned(1024))) char sK0[K_BYTES], sV0[V_BYTES];
-  __shared__ __attribute__((aligned(1024))) char sK1[K_BYTES], sV1[V_BYTES];
-  __shared__ __attribute__((aligned(1024))) char sK2[K_BYTES2], sV2[V_BYTES2];
-  __shared__ __attribute__((aligned(1024))) char sK3[K_BYTES3], sV3[V_BYTES3];
+  // Q reaches LDS by DMA up to D 128 (a region after the stages, which also
+  // stages O for the epilogue); at D 256 the two 64 KB stages leave no room
+  // and Q is loaded into registers
+  constexpr bool QDMA = D <= 128;
+  constexpr int QROW = D * 2;                   // Q / O staging row bytes
+  constexpr int Q_LDS = QDMA ? BQ * QROW : 0;
+  constexpr int Q_INSTR = QDMA ? Q_LDS / 1024 / W : 0;   // Q copies per wave
+  static_assert(!QDMA || Q_LDS % (1024 * W) == 0, "whole Q copies per wave");
+  constexpr int STAGE = K_BYTES + V_BYTES;
+  static_assert(NS * STAGE + Q_LDS <= 160 * 1024, "LDS");
+  __shared__ __attribute__((aligned(1024))) char smem[NS * STAGE + Q_LDS];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -114,18 +126,9 @@ __global__ void __launch_bounds__(64 * W) attention_dma_kernel(AttnParams p) {
   const uint16_t* __restrict__ vg = p.v + (int64_t)bh * Skv * Dr;
   const uint16_t* __restrict__ qg = p.q + (int64_t)bh * Sq * Dr;
 
-  auto stK = [&](int s) -> lds_char_t* {
-    if (s == 0) return (lds_char_t*)sK0;
-    if (s == 1 || NS == 2) return (lds_char_t*)sK1;
-    if (s == 2) return (lds_char_t*)sK2;
-    return (lds_char_t*)sK3;
-  };
-  auto stV = [&](int s) -> lds_char_t* {
-    if (s == 0) return (lds_char_t*)sV0;
-    if (s == 1 || NS == 2) return (lds_char_t*)sV1;
-    if (s == 2) return (lds_char_t*)sV2;
-    return (lds_char_t*)sV3;
-  };
+  auto stK = [&](int s) -> lds_char_t* { return (lds_char_t*)(smem + s * STAGE); };
+  auto stV = [&](int s) -> lds_char_t* { return (lds_char_t*)(smem + s * STAGE + K_BYTES); };
+  lds_char_t* const sQ = (lds_char_t*)(smem + NS * STAGE);
   // ---- DMA of block `blk` into stage s (keys past Skv are clamped: masked
   // later; Ks rows d >= Dr, eight to a copy, come from zeros; Vs chunks past
   // Dr repeat the row's last chunk).  A whole block inside [0, Skv) takes
@@ -211,8 +214,26 @@ __global__ void __launch_bounds__(64 * W) attention_dma_kernel(AttnParams p) {
 
   const int kv_end = p.causal ? min(Skv, q0 + BQ) : Skv;
   const int nblk = (kv_end + KB - 1) / KB;
-  // the first NS-1 KV blocks start loading before Q, so their latency and
-  // Q's overlap (the compiler's wait for Q then also covers these DMAs)
+  // ---- Q by LDS DMA (D <= 128): local query row lr of the workgroup at
+  // sQ + lr QROW, its 16-byte chunk c at position c ^ q_swz(lr) (rows past Sq
+  // repeat the last; chunks past Dr repeat the row's last one and are zeroed
+  // when read).  Issued before the first K/V stages, so the hand-placed wait
+  // for stage 0 covers Q too (copies complete in issue order): a register
+  // load of Q would make the compiler wait for every copy issued before it.
+  if constexpr (QDMA) {
+    const uint32_t lq = lds_addr(sQ);
+#pragma unroll
+    for (int i = 0; i < Q_INSTR; ++i) {
+      const int j = wave * Q_INSTR + i;
+      const int e = j * 1024 + lane * 16;                  // byte of the Q region
+      const int lr = e / QROW, cp = (e % QROW) / 16;
+      const int c = min(cp ^ q_swz<D>(lr), Dr / 8 - 1);
+      const int qrow = min(q0 + lr, Sq - 1);
+      dma_load16(qg + (int64_t)qrow * Dr + c * 8, lq + j * 1024);
+    }
+  }
+  // the first NS-1 KV blocks start loading before the loop (at D 256, before
+  // Q too, so their latency and Q's overlap)
 #pragma unroll
   for (int s = 0; s < NS - 1; ++s)
     if (s < nblk) {
@@ -228,17 +249,21 @@ __global__ void __launch_bounds__(64 * W) attention_dma_kernel(AttnParams p) {
   // (zero past Dr)
   const int q0w = q0 + 16 * QT * wave;
   u32x4_t qf[DSTEPS][QT];
+  auto q_operand = [&](int qt, int ds, u32x4_t raw) {
+    if (ds * 32 + g * 8 >= Dr) raw = u32x4_t{0u, 0u, 0u, 0u};
 #pragma unroll
-  for (int qt = 0; qt < QT; ++qt) {
-    const int qrow = min(q0w + 16 * qt + r, Sq - 1);
+    for (int e = 0; e < 4; ++e)
+      qf[ds][qt][e] = pack2<H>(lo16<H>(raw[e]) * p.c2, hi16<H>(raw[e]) * p.c2);
+  };
+  if constexpr (!QDMA) {
 #pragma unroll
-    for (int ds = 0; ds < DSTEPS; ++ds) {
-      const int d0 = ds * 32 + g * 8;
-      const u32x4_t raw = d0 < Dr ? *reinterpret_cast<const u32x4_t*>(qg + (int64_t)qrow * Dr + d0)
-                                  : u32x4_t{0u, 0u, 0u, 0u};
+    for (int qt = 0; qt < QT; ++qt) {
+      const int qrow = min(q0w + 16 * qt + r, Sq - 1);
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        qf[ds][qt][e] = pack2<H>(lo16<H>(raw[e]) * p.c2, hi16<H>(raw[e]) * p.c2);
+      for (int ds = 0; ds < DSTEPS; ++ds) {
+        const int d0 = min(ds * 32 + g * 8, Dr - 8);
+        q_operand(qt, ds, *reinterpret_cast<const u32x4_t*>(qg + (int64_t)qrow * Dr + d0));
+      }
     }
   }
 
@@ -383,6 +408,19 @@ __global__ void __launch_bounds__(64 * W) attention_dma_kernel(AttnParams p) {
         // KREG: this wave's K stores of the previous iteration are in LDS
         if constexpr (KREG) LOOM_WAIT_LGKM0();
         barrier_nofence();
+        if constexpr (QDMA) {
+          if (it == 0) {
+            // this wave's Q^T operands from the Q region (landed with stage 0)
+#pragma unroll
+            for (int qt = 0; qt < QT; ++qt) {
+              const int lr = 16 * QT * wave + 16 * qt + r;
+#pragma unroll
+              for (int ds = 0; ds < DSTEPS; ++ds)
+                q_operand(qt, ds, *reinterpret_cast<const __attribute__((address_space(3))) u32x4_t*>(
+                                      sQ + lr * QROW + ((4 * ds + g) ^ q_swz<D>(lr)) * 16));
+            }
+          }
+        }
         const bool ahead = it + NS - 1 < nblk;
         if constexpr (KREG) {
           if (ahead) kload(it + NS - 1);
@@ -399,7 +437,40 @@ __global__ void __launch_bounds__(64 * W) attention_dma_kernel(AttnParams p) {
     }
   }
 
-  // ---- out = acc / l; ot[dt][qt][i] is d = 16 dt + 4 g + i of query q0w + 16 qt + r
+  // ---- out = acc / l; ot[dt][qt][i] is d = 16 dt + 4 g + i of query q0w + 16 qt + r.
+  // With D <= 128 and rows of exactly D, each wave stages its rows in its
+  // own slice of the Q region (nothing else touches it after the first
+  // block) and writes them back as whole rows, 16 bytes per lane: 8-byte
+  // stores of 32-byte row pieces cost the workgroup's end far more.
+  if constexpr (QDMA) {
+    if (Dr == D) {
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) {
+        const float inv = 1.f / lacc[qt][0];
+        const int lr = 16 * QT * wave + 16 * qt + r;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+          const f32x4_t o = ot[dt][qt];
+          const int pos = (2 * dt + (g >> 1)) ^ q_swz<D>(lr);
+          *reinterpret_cast<__attribute__((address_space(3))) u32x2_t*>(
+              sQ + lr * QROW + pos * 16 + (g & 1) * 8) =
+              u32x2_t{pack2<H>(o[0] * inv, o[1] * inv), pack2<H>(o[2] * inv, o[3] * inv)};
+        }
+      }
+      constexpr int CPR = QROW / 16;                      // chunks per row
+#pragma unroll
+      for (int k = 0; k < 16 * QT * CPR / 64; ++k) {
+        const int idx = k * 64 + lane;
+        const int lr = 16 * QT * wave + idx / CPR, cp = idx % CPR;
+        const u32x4_t v = *reinterpret_cast<const __attribute__((address_space(3))) u32x4_t*>(
+            sQ + lr * QROW + cp * 16);
+        if (q0 + lr < Sq)
+          *reinterpret_cast<u32x4_t*>(p.out + ((int64_t)bh * Sq + q0 + lr) * Dr +
+                                      (cp ^ q_swz<D>(lr)) * 8) = v;
+      }
+      return;
+    }
+  }
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
     __builtin_amdgcn_sched_barrier(0);
