@@ -661,6 +661,51 @@ __global__ void __launch_bounds__(256) gemm_pipe_kernel(GemmParams p) {
   void* const cz = OUT_F32 ? (void*)(static_cast<float*>(p.C) + (int64_t)z * p.zc)
                            : (void*)(static_cast<uint16_t*>(p.C) + (int64_t)z * p.zc);
   const int64_t r0 = m0 + wm * (T / 2) + lr, c0 = n0 + wn * (T / 2) + lg * 4;
+  // Full tiles whose C fits the stage ring (all but fp32 at T 256) are
+  // staged there row-major and stored as whole rows, 16 bytes per lane:
+  // the register layout gives each lane 16-byte (fp32) or 8-byte (bf16)
+  // pieces of 16 rows per store, which reach memory as partial lines.  Chunk
+  // c of row rr sits at position c ^ c_swz(rr): each 32-lane pass of the
+  // staging writes (16 rows, two adjacent chunks or two halves of one) then
+  // lands on distinct banks.
+  constexpr int ES = OUT_F32 ? 4 : 2, CRB = T * ES, CNC = CRB / 16;
+  constexpr bool STAGED_C = T * CRB <= NS * (A_BYTES + B_BYTES);
+  constexpr int CRPW = CRB >= 512 ? 1 : 512 / CRB;         // rows per 512-byte bank window
+  auto c_swz = [](int rr) { return 2 * ((rr / CRPW) & (CNC / 2 - 1)); };
+  if constexpr (STAGED_C) {
+    if (m0 + T <= p.M && n0 + T <= p.N) {
+      LOOM_WAIT_LGKM0();      // this wave's last fragment reads; every wave's DMAs
+      barrier_nofence();      // landed (vmcnt 0 above): the ring is free
+#pragma unroll
+      for (int tm = 0; tm < TT; ++tm) {
+        const int rr = wm * (T / 2) + tm * 16 + lr;
+#pragma unroll
+        for (int tn = 0; tn < TT; ++tn) {
+          const int col = wn * (T / 2) + tn * 16 + lg * 4;
+          const int cpos = ((col * ES) / 16) ^ c_swz(rr);
+          lds_char_t* const dst = lds + rr * CRB + cpos * 16 + (col * ES) % 16;
+          if constexpr (OUT_F32)
+            *reinterpret_cast<__attribute__((address_space(3))) f32x4_t*>(dst) = acc[tn][tm];
+          else
+            *reinterpret_cast<__attribute__((address_space(3))) u32x2_t*>(dst) =
+                u32x2_t{pack2<H>(acc[tn][tm][0], acc[tn][tm][1]),
+                        pack2<H>(acc[tn][tm][2], acc[tn][tm][3])};
+        }
+      }
+      LOOM_WAIT_LGKM0();
+      barrier_nofence();
+      char* const cbase = static_cast<char*>(cz) + (m0 * p.ldc + n0) * ES;
+#pragma unroll
+      for (int k = 0; k < T * CNC / 4 / 64; ++k) {     // wave w: rows w T/4 .. (w+1) T/4 - 1
+        const int idx = (wave * (T / 4)) * CNC + k * 64 + lane;
+        const int rr = idx / CNC, cp = idx % CNC;
+        const u32x4_t v =
+            *reinterpret_cast<const __attribute__((address_space(3))) u32x4_t*>(lds + idx * 16);
+        *reinterpret_cast<u32x4_t*>(cbase + (int64_t)rr * p.ldc * ES + (cp ^ c_swz(rr)) * 16) = v;
+      }
+      return;
+    }
+  }
   if (m0 + T <= p.M && n0 + T <= p.N) {
     if constexpr (OUT_F32) {
       float* cb = static_cast<float*>(cz) + r0 * p.ldc + c0;
