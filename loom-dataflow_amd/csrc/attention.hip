@@ -458,6 +458,7 @@ __global__ void __launch_bounds__(64 * W) attention_dma_kernel(AttnParams p) {
         }
       }
       constexpr int CPR = QROW / 16;                      // chunks per row
+      lds_order();
 #pragma unroll
       for (int k = 0; k < 16 * QT * CPR / 64; ++k) {
         const int idx = k * 64 + lane;

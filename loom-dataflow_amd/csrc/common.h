@@ -461,6 +461,12 @@ LOOM_DEV void store_stream(V* p, const V& v) {
 // Workgroup barrier without the memory fence __syncthreads() adds (the fence
 // would force every outstanding load, LDS DMA included, to complete).  The
 // empty asm keeps the compiler from moving memory accesses across it.
+// Compiler-only ordering of one wave's LDS accesses through pointers of
+// different types (type-based alias analysis would otherwise let a read move
+// above a write to the same bytes); the hardware executes a wave's LDS
+// instructions in order, so no wait is needed.
+LOOM_DEV void lds_order() { asm volatile("" ::: "memory"); }
+
 LOOM_DEV void barrier_nofence() {
   asm volatile("" ::: "memory");
   __builtin_amdgcn_s_barrier();
