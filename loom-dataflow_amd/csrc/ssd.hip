@@ -424,6 +424,7 @@ __global__ void __launch_bounds__(64 * kSsdWaves) ssd_state_kernel(SsdStateParam
     const bool pre = u + NS - 1 < nu;
     const int sn = (u + NS - 1) % NS, un = u + NS - 1, half = (nlw + 1) / 2;
     make_w(dAs);
+    lds_order();   // the w row's float stores before its f32x4 reads below
     if (part == 0) {
       // prev(c) out, then R = exp(dA[c, Q-1]) R; states(c) accumulate below
       const float decay = fast_exp2(dAs[2 * DTO + 3] * kLog2e);
