@@ -665,13 +665,14 @@ __global__ void __launch_bounds__(256) gemm_pipe_kernel(GemmParams p) {
   // staged there row-major and stored as whole rows, 16 bytes per lane:
   // the register layout gives each lane 16-byte (fp32) or 8-byte (bf16)
   // pieces of 16 rows per store, which reach memory as partial lines.  Chunk
-  // c of row rr sits at position c ^ c_swz(rr): each 32-lane pass of the
-  // staging writes (16 rows, two adjacent chunks or two halves of one) then
-  // lands on distinct banks.
+  // c of row rr sits at position c ^ c_swz(rr): each pass of the staging
+  // writes (16 rows, one 16-byte chunk of each: 16 lanes of 16 bytes, or 32
+  // of 8) then covers the 64 banks (a 256-byte window) once.
   constexpr int ES = OUT_F32 ? 4 : 2, CRB = T * ES, CNC = CRB / 16;
   constexpr bool STAGED_C = T * CRB <= NS * (A_BYTES + B_BYTES);
-  constexpr int CRPW = CRB >= 512 ? 1 : 512 / CRB;         // rows per 512-byte bank window
-  auto c_swz = [](int rr) { return 2 * ((rr / CRPW) & (CNC / 2 - 1)); };
+  constexpr int CRPW = CRB >= 256 ? 1 : 256 / CRB;         // rows per 256-byte bank window
+  constexpr int CSWM = (CNC < 16 ? CNC : 16) - 1;
+  auto c_swz = [](int rr) { return (rr / CRPW) & CSWM; };
   if constexpr (STAGED_C) {
     if (m0 + T <= p.M && n0 + T <= p.N) {
       LOOM_WAIT_LGKM0();      // this wave's last fragment reads; every wave's DMAs

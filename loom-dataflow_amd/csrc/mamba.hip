@@ -386,8 +386,9 @@ __global__ void __launch_bounds__(64 * kWaves, kWaves == 8 ? 4 : 1)
     // 128-byte rows: each half (8 rows) is staged in this wave's 1 KB of LDS
     // and stored 16 bytes per lane (the register layout gives each lane 8
     // bytes of 16 rows per store, partial lines).  The row's 32-byte groups
-    // are XOR-swizzled by row bit 2 so the staging writes of rows r and r + 4
-    // take different banks.  Otherwise four consecutive columns per lane.
+    // are XOR-swizzled by row bits 1-2, so one column group's staging write
+    // (32 bytes from each of the 8 rows) covers all 64 banks once.
+    // Otherwise four consecutive columns per lane.
     if constexpr (PT == 4) {
       if (mrow0 + 16 <= mend && p0 + 64 <= P) {
         char* const st = reinterpret_cast<char*>(ostage + wave * 64);
@@ -398,14 +399,14 @@ __global__ void __launch_bounds__(64 * kWaves, kWaves == 8 ? 4 : 1)
 #pragma unroll
             for (int pt = 0; pt < 4; ++pt) {
               const f32x4_t o = acc_s[pt] * em + acc[pt];
-              *reinterpret_cast<u32x2_t*>(st + sr * 128 + ((pt ^ ((sr >> 2) & 1)) * 32) + g4 * 8) =
+              *reinterpret_cast<u32x2_t*>(st + sr * 128 + ((pt ^ ((sr >> 1) & 3)) * 32) + g4 * 8) =
                   u32x2_t{pack2<F16>(o[0], o[1]), pack2<F16>(o[2], o[3])};
             }
           }
           lds_order();
           const int lr8 = lane >> 3, c = lane & 7;
           const u32x4_t v = *reinterpret_cast<const u32x4_t*>(
-              st + lr8 * 128 + (((c >> 1) ^ ((lr8 >> 2) & 1)) * 32) + (c & 1) * 16);
+              st + lr8 * 128 + (((c >> 1) ^ ((lr8 >> 1) & 3)) * 32) + (c & 1) * 16);
           lds_order();
           *reinterpret_cast<u32x4_t*>(og + (int64_t)(mrow0 + 8 * h + lr8) * P + p0 + c * 8) = v;
         }
