@@ -39,12 +39,10 @@ namespace {
 // ---------------------------------------------------------------------------
 // dA_cumsum
 // ---------------------------------------------------------------------------
-__global__ void __launch_bounds__(64) ssd_cumsum_kernel(const float* __restrict__ dt,
-                                                        const float* __restrict__ A,
-                                                        float* __restrict__ dA, int H, int nc,
-                                                        int Q, int per_lane) {
-  const int row = blockIdx.x;                  // (b*H + h)*nc + c
-  const int lane = threadIdx.x;
+// one wave per (b, h, c) row
+LOOM_DEV void cumsum_row(const float* __restrict__ dt, const float* __restrict__ A,
+                         float* __restrict__ dA, int H, int nc, int Q, int per_lane,
+                         int row /* (b*H + h)*nc + c */, int lane) {
   const int h = (row / nc) % H;
   const float a = A[h];
   const float* src = dt + (int64_t)row * Q;
@@ -74,20 +72,26 @@ __global__ void __launch_bounds__(64) ssd_cumsum_kernel(const float* __restrict_
   }
 }
 
+__global__ void __launch_bounds__(64) ssd_cumsum_kernel(const float* __restrict__ dt,
+                                                        const float* __restrict__ A,
+                                                        float* __restrict__ dA, int H, int nc,
+                                                        int Q, int per_lane) {
+  cumsum_row(dt, A, dA, H, nc, Q, per_lane, blockIdx.x, threadIdx.x);
+}
+
 // ---------------------------------------------------------------------------
 // cb = C B^T, lower triangle
 // ---------------------------------------------------------------------------
 constexpr int kCbTiles = 4;  // 16x16 output tiles per wave (one row band)
 // NKS: 32-wide n steps held in registers (4: dstate <= 128, 8: <= 256)
+// one wave per (b, c, g) chunk bcg = (b*nc + c)*G + g, 16-row band `it` of
+// i and kCbTiles 16-column tiles of j from jz kCbTiles on
 template <bool F16, int NKS>
-__global__ void __launch_bounds__(64) ssd_cb_kernel(const uint16_t* __restrict__ Bm,
-                                                    const uint16_t* __restrict__ Cm,
-                                                    uint16_t* __restrict__ cb, int nc, int G,
-                                                    int L, int Q, int N) {
-  const int bcg = blockIdx.x;                  // (b*nc + c)*G + g
-  const int it = blockIdx.y;                   // 16-row band of i
-  const int jt0 = kCbTiles * blockIdx.z;       // first 16-column tile of j
-  const int lane = threadIdx.x, r = lane & 15, gq = lane >> 4;
+LOOM_DEV void cb_tiles(const uint16_t* __restrict__ Bm, const uint16_t* __restrict__ Cm,
+                       uint16_t* __restrict__ cb, int nc, int G, int L, int Q, int N, int bcg,
+                       int it, int jz, int lane) {
+  const int jt0 = kCbTiles * jz;               // first 16-column tile of j
+  const int r = lane & 15, gq = lane >> 4;
   const int g = bcg % G, c = (bcg / G) % nc, b = bcg / (G * nc);
   const int64_t rowbase = ((int64_t)(b * G + g) * L + (int64_t)c * Q);
   const uint16_t* Cc = Cm + rowbase * N;
@@ -133,6 +137,40 @@ __global__ void __launch_bounds__(64) ssd_cb_kernel(const uint16_t* __restrict__
     *reinterpret_cast<u32x2_t*>(orow) =
         u32x2_t{pack2<F16>(acc[0], acc[1]), pack2<F16>(acc[2], acc[3])};
   }
+}
+
+template <bool F16, int NKS>
+__global__ void __launch_bounds__(64) ssd_cb_kernel(const uint16_t* __restrict__ Bm,
+                                                    const uint16_t* __restrict__ Cm,
+                                                    uint16_t* __restrict__ cb, int nc, int G,
+                                                    int L, int Q, int N) {
+  cb_tiles<F16, NKS>(Bm, Cm, cb, nc, G, L, Q, N, blockIdx.x, blockIdx.y, blockIdx.z, threadIdx.x);
+}
+
+// The prologue's first two stages in one launch: they are independent (cb
+// does not use dA_cumsum), so the cumsum rows -- the first ncum blocks,
+// dispatched first -- run beside the cb tiles instead of ahead of them.
+struct CumsumCbParams {
+  const float* dt;
+  const float* A;
+  float* dA;
+  const uint16_t* B;
+  const uint16_t* C;
+  uint16_t* cb;
+  int H, nc, G, L, Q, N, per_lane;
+  int ncum, nbcg, nit;   // cumsum rows; cb chunks and row bands
+};
+
+template <bool F16, int NKS>
+__global__ void __launch_bounds__(64) ssd_cumsum_cb_kernel(CumsumCbParams p) {
+  const int id = blockIdx.x;
+  if (id < p.ncum) {
+    cumsum_row(p.dt, p.A, p.dA, p.H, p.nc, p.Q, p.per_lane, id, threadIdx.x);
+    return;
+  }
+  const int k = id - p.ncum;   // the cb grid's (x, y, z) in its dispatch order, x fastest
+  cb_tiles<F16, NKS>(p.B, p.C, p.cb, p.nc, p.G, p.L, p.Q, p.N, k % p.nbcg, (k / p.nbcg) % p.nit,
+                     k / (p.nbcg * p.nit), threadIdx.x);
 }
 
 // ---------------------------------------------------------------------------
@@ -763,7 +801,37 @@ int prologue_impl(const void* x, const void* dt, const void* A, const void* B,
   rc = stages();
   vo = outer;
   if (rc || outer) return rc;
-  return stages();
+  // cumsum and cb in one launch (independent of each other), then the states
+  const int64_t ncum = batch * nheads * nchunks, nbcg = batch * nchunks * ngroups;
+  const int64_t nit = chunk_size / 16, njz = (nit + kCbTiles - 1) / kCbTiles;
+  const int64_t nblocks = ncum + nbcg * nit * njz;
+  if (nblocks > 0x7fffffff) return stages();
+  CumsumCbParams q{};
+  q.dt = static_cast<const float*>(dt);
+  q.A = static_cast<const float*>(A);
+  q.dA = static_cast<float*>(dA_cumsum);
+  q.B = static_cast<const uint16_t*>(B);
+  q.C = static_cast<const uint16_t*>(C);
+  q.cb = static_cast<uint16_t*>(cb);
+  q.H = (int)nheads;
+  q.nc = (int)nchunks;
+  q.G = (int)ngroups;
+  q.L = (int)(nchunks * chunk_size);
+  q.Q = (int)chunk_size;
+  q.N = (int)dstate;
+  q.per_lane = (int)((chunk_size + 63) / 64);
+  q.ncum = (int)ncum;
+  q.nbcg = (int)nbcg;
+  q.nit = (int)nit;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dstate <= 128)
+    hipLaunchKernelGGL((ssd_cumsum_cb_kernel<F16, 4>), dim3((unsigned)nblocks), dim3(64), 0, st, q);
+  else
+    hipLaunchKernelGGL((ssd_cumsum_cb_kernel<F16, 8>), dim3((unsigned)nblocks), dim3(64), 0, st, q);
+  rc = loom_check_launch(err, errlen, "ssd_prologue (cumsum and cb)");
+  if (rc) return rc;
+  return state_passing_impl<F16>(x, dt, dA_cumsum, B, prev_states_T, batch, nchunks, nheads,
+                                 ngroups, chunk_size, headdim, dstate, stream, err, errlen);
 }
 
 }  // namespace
