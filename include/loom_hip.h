@@ -255,9 +255,10 @@ int loom_hip_ssd_chunk_state_passing(const void* x, const void* dt, const void* 
                                      int64_t chunk_size, int64_t headdim, int64_t dstate,
                                      void* stream, char* err, size_t errlen);
 
-/* All three stages in stream order: dA_cumsum, cb, prev_states_T.  Every
- * stage's checks run before the first launch: a rejected call enqueues
- * nothing. */
+/* All three stages in stream order: dA_cumsum and cb (independent of each
+ * other) in one launch, then prev_states_T; the outputs equal those of the
+ * three stage entry points above called in turn.  Every stage's checks run
+ * before the first launch: a rejected call enqueues nothing. */
 int loom_hip_ssd_prologue(const void* x, const void* dt, const void* A, const void* B,
                           const void* C, void* dA_cumsum, void* cb, void* prev_states_T,
                           int64_t batch, int64_t nchunks, int64_t nheads, int64_t ngroups,

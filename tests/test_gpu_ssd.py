@@ -171,3 +171,52 @@ def test_mamba_baseline_full_config(lh):
     _, dA2, cb2, prev2 = lh.ssd_prologue(dev(x), devf(dt), devf(A), dev(Bm), dev(C), Q)
     assert torch.equal(dA2, dA) and torch.equal(cb2.view(torch.int16), cb.view(torch.int16)) \
         and torch.equal(prev2, prev), "SSD prologue not deterministic"
+
+
+# (b, H, G, Q, nc, P, N, 16-bit type)
+STAGE_SHAPES = [
+    (2, 4, 1, 256, 3, 64, 128, torch.bfloat16),    # the BASELINE unit plan, cb over 4 n steps
+    (1, 4, 2, 192, 2, 160, 256, torch.bfloat16),   # two groups, cb over 8 n steps
+    (1, 2, 1, 176, 2, 128, 96, torch.bfloat16),    # a chunk the wave cumsum covers in 3 per lane
+    (1, 4, 2, 192, 2, 160, 128, torch.float16),
+]
+
+
+@pytest.mark.parametrize("b,H,G,Q,nc,P,N,ty", STAGE_SHAPES)
+def test_stage_entry_points_match_prologue(lh, b, H, G, Q, nc, P, N, ty):
+    """The prologue runs the cumsum rows and the cb tiles in one launch; the
+    standalone stage entry points (loom_hip_ssd_chunk_cumsum,
+    loom_hip_ssd_bmm_chunk, loom_hip_ssd_chunk_state_passing), called one
+    after another, give the same bits for all three outputs (the prologue's
+    outputs are checked against the oracle above)."""
+    import ctypes
+    print(f"ssd stages b{b} H{H} G{G} Q{Q} c{nc} P{P} N{N} {ty}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(b * 1000 + H * 10 + Q + N)
+    L = nc * Q
+    x = torch.randn(b, H, L, P, device="cuda", generator=g).to(ty)
+    Bm = torch.randn(b, G, L, N, device="cuda", generator=g).to(ty)
+    C = torch.randn(b, G, L, N, device="cuda", generator=g).to(ty)
+    dt = torch.nn.functional.softplus(torch.randn(b, H, L, device="cuda", generator=g))
+    A = -torch.exp(torch.rand(H, device="cuda", generator=g))
+    _, dA, cb, prev = lh.ssd_prologue(x, dt, A, Bm, C, Q)
+    dA2, cb2, prev2 = torch.empty_like(dA), torch.empty_like(cb), torch.empty_like(prev)
+    for t in (dA2, prev2):
+        t.fill_(float("nan"))
+    cb2.fill_(float("nan"))
+    sfx = "_f16" if ty == torch.float16 else ""
+    st = torch.cuda.current_stream().cuda_stream
+    p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+
+    def call(name, *args):
+        buf = ctypes.create_string_buffer(256)
+        rc = getattr(lh._lib, name)(*args, st, buf, len(buf))
+        assert rc == 0, (name, rc, buf.value.decode())
+
+    call("loom_hip_ssd_chunk_cumsum", p(dt), p(A), p(dA2), b, nc, H, Q)
+    call("loom_hip_ssd_bmm_chunk" + sfx, p(Bm), p(C), p(cb2), b, nc, G, Q, N)
+    call("loom_hip_ssd_chunk_state_passing" + sfx, p(x), p(dt), p(dA2), p(Bm), p(prev2), b, nc, H,
+         G, Q, P, N)
+    torch.cuda.synchronize()
+    assert torch.equal(dA.view(torch.int32), dA2.view(torch.int32)), "dA_cumsum"
+    assert torch.equal(cb.view(torch.int16), cb2.view(torch.int16)), "cb"
+    assert torch.equal(prev.view(torch.int32), prev2.view(torch.int32)), "prev_states_T"
