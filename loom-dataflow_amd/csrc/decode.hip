@@ -143,10 +143,12 @@ LOOM_DEV int dv_swz(int k) { return D >= 128 ? 2 * (k & 7) : 2 * ((k >> 1) & 3);
 // loads its 16-byte pieces of a K block into registers (row_piece8), issued
 // before the block NS-1 stages ahead of the one being computed and written to
 // the DMA's LDS positions after that computation; V keeps its DMA.
-template <int D, bool F16, bool KREG, int W>
+// NSX: stages when nonzero (2: a grid above one workgroup per CU then fits
+// two per CU), else three up to D 128 and two (64 KB each) at D 256
+template <int D, bool F16, bool KREG, int W, int NSX = 0>
 __global__ void __launch_bounds__(64 * W) decode_dma_kernel(DecodeParams p) {
   constexpr int KB = 64;                       // keys per stage
-  constexpr int NS = D > 128 ? 2 : 3;          // stages (64 KB each at D 256)
+  constexpr int NS = NSX ? NSX : (D > 128 ? 2 : 3);
   constexpr int HS = 8 * W;                    // head slots (16 per pair of waves)
   constexpr int K_BYTES = D * KB * 2, V_BYTES = KB * D * 2;
   constexpr int K_INSTR = K_BYTES / 1024 / W, V_INSTR = V_BYTES / 1024 / W;
@@ -692,17 +694,34 @@ void launch_split(const DecodeParams& p, hipStream_t st) {
   hipLaunchKernelGGL((decode_split_kernel<D, HT, F16>), grid, block, 0, st, p);
 }
 
+template <int D, bool F16, int NSX>
+void launch_dma_ns(const DecodeParams& p, bool kreg, bool wide, const dim3& grid, hipStream_t st) {
+  if (wide) {   // three stages only (NSX 0)
+    if (kreg) hipLaunchKernelGGL((decode_dma_kernel<D, F16, true, 8>), grid, dim3(512), 0, st, p);
+    else hipLaunchKernelGGL((decode_dma_kernel<D, F16, false, 8>), grid, dim3(512), 0, st, p);
+  } else {
+    if (kreg) hipLaunchKernelGGL((decode_dma_kernel<D, F16, true, 4, NSX>), grid, dim3(256), 0, st, p);
+    else hipLaunchKernelGGL((decode_dma_kernel<D, F16, false, 4, NSX>), grid, dim3(256), 0, st, p);
+  }
+}
+
+// Up to D 128 the 4-wave kernel's ring has three stages (64 KB in flight,
+// one workgroup per CU by LDS) while the grid fits the CUs, and two when it
+// has more workgroups than CUs, so that two fit per CU (72 KB of LDS and
+// about 160 VGPRs each) and the grid runs in one round.  Graph of 20 calls,
+// same run: B32 H32 D128 S8192 tile_s 1024 (256 workgroups) 30.0 us with
+// three stages against 31.7 with two; tile_s 512 35.3 against 31.8;
+// tile_s 256 44.1 against 38.5; B16 tile_s 256 23.4 against 20.8.  The
+// 8-wave kernel's registers allow one workgroup per CU either way, so it
+// keeps three stages.
 template <int D, bool F16>
 void launch_dma(const DecodeParams& p, bool kreg, bool wide, hipStream_t st) {
   const int hs = wide ? 64 : 32;
   const dim3 grid((unsigned)p.ns, (unsigned)p.B, (unsigned)((p.H + hs - 1) / hs));
-  if (wide) {
-    if (kreg) hipLaunchKernelGGL((decode_dma_kernel<D, F16, true, 8>), grid, dim3(512), 0, st, p);
-    else hipLaunchKernelGGL((decode_dma_kernel<D, F16, false, 8>), grid, dim3(512), 0, st, p);
-  } else {
-    if (kreg) hipLaunchKernelGGL((decode_dma_kernel<D, F16, true, 4>), grid, dim3(256), 0, st, p);
-    else hipLaunchKernelGGL((decode_dma_kernel<D, F16, false, 4>), grid, dim3(256), 0, st, p);
-  }
+  const int cus = stream_cus(st);
+  const bool two = D <= 128 && !wide && cus > 0 && (int64_t)grid.x * grid.y * grid.z > cus;
+  if (two) launch_dma_ns<D, F16, 2>(p, kreg, wide, grid, st);
+  else launch_dma_ns<D, F16, 0>(p, kreg, wide, grid, st);
 }
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
