@@ -449,7 +449,7 @@ def make_cases(torch, lh):
         return dict(fn=lambda i: lh.flash_decode(*sets[i % n], tile_s=1024, tile_n=128),
                     flop=4 * B * H * S * D, bytes=nb, bound="hbm", sets=n,
                     desc="mqa_decode B32 H32/1KV D128 S8192, tile_s 1024", cpu=cpu,
-                    kernel="decode_dma_kernel<128, false, false, 4>")
+                    kernel="decode_dma_kernel<128, false, false, 4, 0>")
     cases["mqa_decode"] = decode
 
     def mamba():
